@@ -1,0 +1,214 @@
+"""Pins the numpy oracle (CPU only): closed forms, autograd, finite differences,
+batched-vs-token-loop consistency and the checkpoint byte layout."""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import ckpt, model as om
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+# ---------------------------------------------------------------- primitives
+
+def test_rmsnorm_closed_form():
+    D = 64
+    for c in (0.5, 3.0, -2.0):
+        x = np.full((3, D), c, np.float32)
+        w = np.linspace(0.5, 1.5, D).astype(np.float32)
+        y, r = om.rmsnorm(x, w, 1e-5)
+        np.testing.assert_allclose(y, w * c / math.sqrt(c * c + 1e-5) * np.ones((3, 1)), rtol=1e-6)
+        np.testing.assert_allclose(r[:, 0], 1 / math.sqrt(c * c + 1e-5), rtol=1e-6)
+
+
+def test_rope_identity_at_pos0_and_norm_preserved():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 5, 3, 16)).astype(np.float32)
+    cos, sin = om.rope_tables(5, 16, 10000.0)
+    y = om.rope_apply(x, cos, sin)
+    np.testing.assert_array_equal(y[:, 0], x[:, 0])
+    # a rotation keeps each pair's norm
+    n0 = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n1 = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+    np.testing.assert_allclose(n1, n0, rtol=1e-5, atol=1e-6)
+    # closed-form angle of pair i at position p: p * theta^(-2i/hd); pair (1, 0) -> (cos, sin)
+    e = np.zeros((1, 5, 1, 16), np.float32)
+    e[..., 6] = 1.0                                   # pair i=3, first channel
+    y = om.rope_apply(e, cos, sin)
+    ang = np.arange(5) * 10000.0 ** (-6.0 / 16)
+    np.testing.assert_allclose(y[0, :, 0, 6], np.cos(ang), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(y[0, :, 0, 7], np.sin(ang), rtol=1e-6, atol=1e-7)
+    # backward is the transpose: <rope(x), g> == <x, rope_bwd(g)>
+    g = rng.standard_normal(x.shape).astype(np.float32)
+    lhs = np.sum(om.rope_apply(x, cos, sin).astype(np.float64) * g)
+    rhs = np.sum(x.astype(np.float64) * om.rope_bwd(g, cos, sin))
+    assert abs(lhs - rhs) < 1e-4 * abs(lhs) + 1e-5
+
+
+@pytest.mark.parametrize("V", [512, 32000])
+def test_ce_zero_weights_is_ln_vocab(V):
+    cfg = om.tiny(vocab=V, n_layers=1)
+    P = om.init_params(cfg, zero=True)
+    tok = om.tokens_for_step(cfg, 2, 16, seed=1)
+    loss, cache = om.forward(cfg, P, tok)
+    assert abs(loss - (-math.log(1.0 / V + 1e-10))) < 1e-5
+    assert abs(loss - math.log(V)) < 1e-4
+    # dlogits rows sum to zero (softmax minus one-hot)
+    assert np.abs(cache["dlogits"].sum(axis=1)).max() < 1e-6
+
+
+def test_adam_closed_form_t1():
+    rng = np.random.default_rng(3)
+    w0 = rng.standard_normal(1000).astype(np.float32) * 0.02
+    g = rng.standard_normal(1000).astype(np.float32) * 1e-3
+    w, m, v = w0.copy(), np.zeros_like(w0), np.zeros_like(w0)
+    lr, wd, eps = 3e-4, 0.1, 1e-8
+    om.adam_update(w, g, m, v, 1, lr, 0.9, 0.95, eps, wd)
+    expect = w0 - lr * (g / (np.abs(g) + eps) + wd * w0)
+    np.testing.assert_allclose(w, expect, rtol=1e-5, atol=1e-9)
+
+
+def test_lr_schedule_and_clip_closed_form():
+    assert om.lr_at(0, 3e-4, 100, 1000) == pytest.approx(3e-6, rel=1e-6)
+    assert om.lr_at(99, 3e-4, 100, 1000) == pytest.approx(3e-4, rel=1e-6)
+    assert om.lr_at(100, 3e-4, 100, 1000) == pytest.approx(3e-4, rel=1e-6)
+    assert om.lr_at(1000, 3e-4, 100, 1000) == pytest.approx(3e-5, rel=1e-5)
+    mid = om.lr_at(550, 3e-4, 100, 1000)
+    assert mid == pytest.approx(3e-5 + 0.5 * 2.7e-4, rel=1e-5)
+    assert om.clip_scale(2.0, 1.0) == 0.5
+    assert om.clip_scale(0.5, 1.0) == 1.0
+    assert om.clip_scale(5.0, 0.0) == 1.0
+
+
+def test_bf16_rounding():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -9, -3.14159, 1e-30], np.float32)
+    r = om.round_bf16(x)
+    assert r[0] == 1.0
+    assert r[1] == 1.0                       # tie -> even
+    assert r[2] == 1.0 + 2 ** -7             # above half -> up
+    assert abs(r[3] + 3.140625) < 1e-7
+
+
+# ---------------------------------------------------------------- backward
+
+CASES = [
+    dict(qk_norm=False, res_alpha=1.0, rope_theta=1e4),
+    dict(qk_norm=True, res_alpha=om.train_alpha(2), rope_theta=1e6),
+]
+
+
+@pytest.mark.parametrize("kw", CASES)
+def test_backward_matches_float64_autograd(kw):
+    torch = pytest.importorskip("torch")
+    import torch_ref
+    cfg = om.tiny(**kw, dim=64, hidden=128, head_dim=16, vocab=97)
+    P = om.init_params(cfg, seed=5, std=0.1)
+    rng = np.random.default_rng(9)
+    for n in P:                                   # gains away from 1 exercise the exact bwd
+        if om.is_gain(n):
+            P[n] = (1 + 0.3 * rng.standard_normal(P[n].shape)).astype(np.float32)
+    tok = om.tokens_for_step(cfg, 2, 12, seed=4)
+    loss, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    G = om.backward(cfg, P, cache)
+    tl, TG = torch_ref.grads(cfg, P, tok, loss_scale=256.0)
+    assert abs(loss - tl) < 1e-5 * abs(tl)
+    for n in P:
+        assert rel_l2(G[n], TG[n]) < 2e-4, n
+
+
+def test_torch_ref_matches_finite_differences():
+    torch = pytest.importorskip("torch")
+    import torch_ref
+    cfg = om.tiny(dim=32, hidden=64, head_dim=8, vocab=31, n_layers=1, qk_norm=True,
+                  res_alpha=0.5, rope_theta=1e6)
+    P = om.init_params(cfg, seed=2, std=0.2)
+    tok = om.tokens_for_step(cfg, 1, 6, seed=8)
+    _, TG = torch_ref.grads(cfg, P, tok)
+    params = {k: torch.tensor(v, dtype=torch.float64) for k, v in P.items()}
+    rng = np.random.default_rng(1)
+    for n in ("layers.0.Wq", "layers.0.Wk", "layers.0.W2", "layers.0.q_norm", "layers.0.rms_att",
+              "rms_final", "embed"):
+        flat = params[n].view(-1)
+        for idx in rng.choice(flat.numel(), 3, replace=False):
+            h = 1e-6
+            old = float(flat[idx])
+            flat[idx] = old + h
+            lp = float(torch_ref.loss_fn(cfg, params, tok))
+            flat[idx] = old - h
+            lm = float(torch_ref.loss_fn(cfg, params, tok))
+            flat[idx] = old
+            fd = (lp - lm) / (2 * h)
+            an = TG[n].reshape(-1)[idx]
+            assert abs(fd - an) < 1e-6 + 1e-4 * abs(an), (n, idx, fd, an)
+
+
+# ---------------------------------------------------------------- forward consistency
+
+@pytest.mark.parametrize("kw", CASES)
+def test_batched_forward_equals_token_loop(kw):
+    cfg = om.tiny(**kw, vocab=300)
+    P = om.init_params(cfg, seed=0, std=0.05)
+    tok = om.tokens_for_step(cfg, 2, 10, seed=3)
+    _, cache = om.forward(cfg, P, tok)
+    xf = cache["xf"]
+    logits = xf @ P["embed"].T
+    for k in (1, 4, 10):
+        _, _, rows = om.decode(cfg, P, tok[:, :k], 1, return_logits=True)
+        np.testing.assert_allclose(rows[0], logits[:, k - 1], rtol=2e-4, atol=2e-5)
+
+
+def test_decode_sampling_matches_numpy_choice():
+    """Inverse-CDF sampling with a supplied uniform equals RandomState.choice's draw."""
+    cfg = om.tiny(vocab=200, n_layers=1)
+    P = om.init_params(cfg, seed=1, std=0.3)
+    prompt = np.array([[3, 7, 11]], np.int32)
+    u = np.random.RandomState(5).random_sample((1, 6))
+    toks, _, rows = om.decode(cfg, P, prompt, 6, temperature=0.6, uniforms=u, return_logits=True)
+    rs = np.random.RandomState(5)
+    for j in range(6):
+        pr = om.softmax_rows((rows[j, 0] / np.float32(0.6))[None])[0]
+        assert toks[0, j] == rs.choice(200, p=pr)
+
+
+# ---------------------------------------------------------------- checkpoint
+
+def test_ckpt_header_offsets_and_roundtrip(tmp_path):
+    cfg = om.tiny(n_layers=1, qk_norm=True)
+    P = om.init_params(cfg, seed=1)
+    M = {k: v * 0.5 for k, v in P.items()}
+    V = {k: v * 0.25 for k, v in P.items()}
+    path = tmp_path / "c.bin"
+    ckpt.write(path, cfg, P, M, V, step=7, total_steps=100, lr=1e-3, loss=2.5, adam_t=3,
+               cum_train=1.5)
+    raw = path.read_bytes()
+    assert len(raw) == ckpt.expected_size(cfg)
+    # hand-decoded offsets of the 96-byte header (TD/config.h:82-91)
+    assert struct.unpack_from("<i", raw, 0)[0] == 0x424C5A54
+    assert struct.unpack_from("<i", raw, 4)[0] == 4
+    assert struct.unpack_from("<i", raw, 8)[0] == 7
+    assert struct.unpack_from("<i", raw, 16)[0] == 1          # n_layers
+    assert struct.unpack_from("<i", raw, 20)[0] == cfg.vocab
+    assert struct.unpack_from("<f", raw, 44)[0] == 2.5        # loss
+    assert struct.unpack_from("<d", raw, 56)[0] == 1.5        # cum_train
+    assert struct.unpack_from("<i", raw, 80)[0] == 3          # adam_t
+    assert struct.unpack_from("<iii", raw, 84) == (cfg.kv_heads, cfg.head_dim, cfg.q_dim)
+    # first tensor (Wq) starts right after the header
+    np.testing.assert_array_equal(np.frombuffer(raw, np.float32, 4, 96), P["layers.0.Wq"].reshape(-1)[:4])
+    h, P2, M2, V2 = ckpt.read(path)
+    assert h["step"] == 7 and h["adam_t"] == 3
+    for k in P:
+        np.testing.assert_array_equal(P2[k], P[k])
+        np.testing.assert_array_equal(M2[k], M[k])
+        np.testing.assert_array_equal(V2[k], V[k])
+
+
+def test_ckpt_reference_sizes():
+    """Byte counts of the reference checkpoints computed from TD/train.m:97-131."""
+    assert ckpt.expected_size(om.stories110m()) == 1_314_358_368
+    assert ckpt.expected_size(om.qwen3_06b(qk_norm=False)) == 7_152_513_120
