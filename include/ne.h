@@ -1,0 +1,221 @@
+/*
+ * ne.h - C-ABI of the MI355X (gfx950) training_dynamic step: forward, backward, AdamW and
+ * the KV-cached token loop, over device-resident weights.
+ *
+ * This library replaces the reference's ANE dispatch and staging layer and the CPU ops
+ * between the ANE kernels.  Reference paths below are relative to the reference repo,
+ * TD = ane-training/training/training_dynamic.  Conventions follow the reference's own
+ * exported C-ABI precedent (ane-training/bridge/ane_bridge.h:15-94): an opaque handle,
+ * NULL on create failure, int status (0 ok, negative error), caller-owned host buffers.
+ *
+ * Status codes: 0 success; -1 bad argument/shape; -2 bad state; -3 file I/O; -4 bad
+ * checkpoint format; -5 out of memory; -1000-hipError_t for a HIP runtime error.
+ * ne_last_error() gives a thread-local message for the last failure.  The library never
+ * prints and never exits.
+ *
+ * Threading: one context per thread; each context owns one HIP stream.  Calls return after
+ * their stream work completes, except ne_train_step (work may stay queued until the next
+ * synchronising call: ne_sync, ne_get_tensor, ne_optimizer_step with gnorm_out, ...).
+ */
+#ifndef NE_H
+#define NE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ne_ctx ne_ctx;
+
+/* Model and step shape.  Replaces the compile-time model headers
+ * TD/models/{stories110m,qwen3_06b,qwen3_06b_seq512}.h:6-19 (DIM, HIDDEN, HEADS, KV_HEADS,
+ * HD, SEQ, NLAYERS, VOCAB) plus the values hardcoded in the reference: RoPE base 10000
+ * (TD/cpu_ops.h:466), residual scale 1/sqrt(2*NLAYERS) (TD/train.m:181), eps 1e-5
+ * (TD/cpu_ops.h:42).  qk_norm adds Qwen3's per-head RMSNorm on q and k (absent in the
+ * reference). */
+typedef struct ne_config {
+  int32_t dim, hidden, n_heads, kv_heads, head_dim, n_layers, vocab;
+  int32_t seq;          /* training sequence length S (multiple of 64) */
+  int32_t batch;        /* training sequences per step B (T = B*S tokens) */
+  int32_t qk_norm;      /* 0: reference (no QK-norm), 1: per-head QK-RMSNorm */
+  float rope_theta;     /* reference: 10000 */
+  float res_alpha;      /* residual branch scale; TD/train.m:181 uses 1/sqrt(2L), generate.py 1 */
+  float norm_eps;       /* 1e-5 */
+  int32_t decode_batch; /* max sequences of ne_decode (0: no decode buffers) */
+  int32_t decode_ctx;   /* max prompt + generated tokens of ne_decode */
+} ne_config;
+
+/* Counters of the v4 checkpoint header (TD/config.h:82-91 CkptHdr). */
+typedef struct ne_train_state {
+  int32_t step, total_steps;
+  float lr, loss;
+  double cum_compile, cum_train, cum_wall;
+  int32_t cum_steps, cum_batches, adam_t;
+} ne_train_state;
+
+/* Tensor kinds for ne_set_tensor / ne_get_tensor. */
+enum { NE_PARAM = 0, NE_GRAD = 1, NE_ADAM_M = 2, NE_ADAM_V = 3 };
+
+/* ---------------------------------------------------------------- context ---- */
+
+/* Allocate device-resident fp32 master weights, grads, Adam m/v, the bf16 weight shadow and
+ * all activation/workspace buffers.  Replaces ane_init (TD/config.h:99-107), the per-layer
+ * host allocations (TD/config.h:110-176, TD/train.m:199-210), kernel compilation
+ * (TD/train.m:25-94, TD/io.h:135-171) and IOSurface/request setup (TD/train.m:304-329).
+ * Weights start at zero (gains at 1); load them with ne_set_tensor or ne_load_ckpt_v4. */
+ne_ctx *ne_create(const ne_config *cfg);
+/* Frees everything.  Replaces free_kern / free_per_layer (TD/io.h:172-181, 412-419). */
+void ne_destroy(ne_ctx *ctx);
+/* Thread-local message for the last failing call. */
+const char *ne_last_error(void);
+/* Wait for all queued work of the context. */
+int ne_sync(ne_ctx *ctx);
+
+/* Tensor ids follow the checkpoint order (TD/train.m:111-129): for layer l,
+ * 9*l + {0:Wq[Q,D] 1:Wk[KV,D] 2:Wv[KV,D] 3:Wo[D,Q] 4:W1[H,D] 5:W2[D,H] 6:W3[H,D]
+ * 7:rms_att[D] 8:rms_ffn[D]}; then 9L: rms_final[D]; 9L+1: embed[V,D]; with qk_norm,
+ * 9L+2+2l: q_norm[HD] and 9L+3+2l: k_norm[HD]. */
+int ne_num_tensors(const ne_ctx *ctx);
+int64_t ne_tensor_numel(const ne_ctx *ctx, int tensor_id);
+/* Copy fp32 host data in/out of one tensor (row-major, reference layout).  Setting a
+ * parameter also refreshes its bf16 shadow.  Replaces the per-layer stage_* / transpose
+ * restaging of TD/io.h:263-409 and TD/train.m:261-274 (weights never leave the device
+ * during training). */
+int ne_set_tensor(ne_ctx *ctx, int kind, int tensor_id, const float *host, size_t n);
+int ne_get_tensor(ne_ctx *ctx, int kind, int tensor_id, float *host, size_t n);
+
+/* ------------------------------------------------------------ training step ---- */
+
+/* One forward + backward over B sequences: tokens is [B, S+1] int32 (inputs [:, :S],
+ * targets [:, 1:]).  Gradients (times loss_scale) ACCUMULATE into the context's grads.
+ * loss_out (may be NULL; non-NULL synchronises) receives the mean token loss
+ * -log(p_tgt + 1e-10).  Replaces the step body of TD/train.m:403-757: embed_lookup, the 28
+ * sdpaFwd/ffnFused + 5 backward ANE evals per layer (TD/io.h:190-229), the CPU RMSNorm /
+ * residual / RoPE / GQA ops, cross_entropy_loss (TD/cpu_ops.h:348-382), the dW sgemms and
+ * embed_backward. */
+int ne_train_step(ne_ctx *ctx, const int32_t *tokens, float loss_scale, float *loss_out);
+
+/* Scale grads by grad_scale, global L2 norm, clip to `clip` (if > 0), AdamW with
+ * bias-corrected moments (t = ++adam_t), weight decay wd on matrices and the embedding
+ * (0 on the RMSNorm / QK-norm gains), refresh the bf16 shadow, zero the grads.  gnorm_out
+ * (may be NULL; non-NULL synchronises) receives the pre-clip norm.  Replaces
+ * TD/train.m:782-903 and adam_update (TD/cpu_ops.h:266-303). */
+int ne_optimizer_step(ne_ctx *ctx, float lr, float b1, float b2, float eps, float wd,
+                      float grad_scale, float clip, float *gnorm_out);
+/* Zero all gradients.  Replaces layer_grads_zero (TD/config.h:164-170). */
+int ne_zero_grads(ne_ctx *ctx);
+int ne_get_state(const ne_ctx *ctx, ne_train_state *st);
+int ne_set_state(ne_ctx *ctx, const ne_train_state *st);
+
+/* ------------------------------------------------------------- checkpoints ---- */
+
+/* v4 checkpoint (TD/train.m:97-165, header TD/config.h:82-91): 96-byte header, per layer
+ * Wq Wk Wv Wo W1 W2 W3 rms_att rms_ffn then their (m, v), rms_final+m+v, embed+m+v, all
+ * fp32.  With qk_norm a trailer "QKN1" + per layer q_norm,m,v,k_norm,m,v follows (v4
+ * readers stop before it).  Load checks magic, version, dims against the context and the
+ * file size.  st may be NULL. */
+int ne_load_ckpt_v4(ne_ctx *ctx, const char *path, ne_train_state *st);
+int ne_save_ckpt_v4(ne_ctx *ctx, const char *path, const ne_train_state *st);
+
+/* ------------------------------------------------------------- token loop ---- */
+
+/* KV-cached autoregressive generation (TD/tools/generate.py:113-228) for B sequences
+ * sharing one prompt length P: prompt is [B, P] int32, out_tokens receives [B, n_new].
+ * temperature < 1e-6 selects greedy argmax; otherwise softmax(logits/temperature), an
+ * optional top-p mask (top_p < 1) and inverse-CDF sampling in vocabulary order with
+ * uniforms[b*n_new + j] in [0,1) (the draw of numpy's RandomState.choice, generate.py:215).
+ * Uses the bf16 weight shadow with fp32 activations and an fp32 KV cache.  Requires
+ * B <= decode_batch and P + n_new <= decode_ctx. */
+int ne_decode(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temperature,
+              float top_p, const double *uniforms, int32_t *out_tokens);
+
+/* ------------------------------------------------------------- profiling ---- */
+
+/* Per-kernel-family HIP-event timing on the context's stream (off by default). */
+enum {
+  NE_PROF_GEMM_FWD = 0, NE_PROF_GEMM_BWD, NE_PROF_ATTN_FWD, NE_PROF_ATTN_BWD, NE_PROF_NORM,
+  NE_PROF_CE, NE_PROF_ADAM, NE_PROF_GNORM, NE_PROF_EMBED, NE_PROF_DECODE, NE_PROF_COUNT
+};
+int ne_prof_enable(ne_ctx *ctx, int on);
+int ne_prof_reset(ne_ctx *ctx);
+/* Total milliseconds and launch count of one family since the last reset (synchronises). */
+int ne_prof_get(ne_ctx *ctx, int family, double *ms, int64_t *count);
+
+/* ------------------------------------------------------ kernel-level entry points ---- */
+/* Device-pointer entry points of the individual kernels (bf16 = uint16 bit patterns),
+ * for testing and for callers composing their own step.  stream: a hipStream_t or NULL.
+ * They launch asynchronously and return the launch status. */
+
+/* y[T,D] bf16 = x*r*g, r[T] = (mean(x^2)+eps)^-1/2.  TD/cpu_ops.h:20-60 rmsnorm. */
+int ne_k_rmsnorm_fwd(const float *x, const float *g, void *y, float *r, int T, int D, float eps,
+                     void *stream);
+/* Exact RMSNorm backward + residual (may be NULL) + gain-grad accumulation into dg; dxb
+ * (may be NULL) receives bf16(bscale*dx).  TD/cpu_ops.h:108-261 rmsnorm_bwd(_add). */
+int ne_k_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
+                     const float *resid, float *dx, void *dxb, float bscale, float *dg, int T,
+                     int D, void *stream);
+/* C = epi(alpha * A.B) on bf16 MFMA.  layout 0: A[M,K] B[N,K] (forward, weights [out,in]);
+ * 2: A[M,K] B[K,N] (input gradient); 3: A[K,M] B[K,N] (weight gradient).  epi 0: C bf16,
+ * 1: C fp32, 2: C fp32 +=, 3: C fp32 = R fp32 + result, 4: SwiGLU backward (result =
+ * dgate, R = h13 bf16 [M,2N], C = dh13 bf16 [M,2N]).  M, N, K multiples of 64.
+ * Replaces the matmuls of TD/mil_dynamic.h:14-35, 57-234, 238-306, 320-576 and the
+ * cblas_sgemm calls of TD/train.m:500-524, 554-738. */
+int ne_k_gemm(int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
+              const void *B, int64_t ldb, void *C, int64_t ldc, const void *R, int64_t ldr,
+              float alpha, void *stream);
+/* Per-head QK-RMSNorm (gq/gk NULL: off) + interleaved RoPE of the q and k column blocks of
+ * qkv [T, ld] bf16 at positions t % S with fp32 tables cos/sin [S, HD/2]; writes qr, kr
+ * bf16 and the norm factors rq [T,NH], rk [T,NKV].  TD/mil_dynamic.h:133-169. */
+int ne_k_qk_prep_fwd(const void *qkv, int64_t ld, const float *cosb, const float *sinb,
+                     const float *gq, const float *gk, void *qr, void *kr, float *rq, float *rk,
+                     int T, int S, int NH, int NKV, int HD, float eps, void *stream);
+/* Backward of ne_k_qk_prep_fwd: dq [T,NH*HD], dk [T,NKV*HD] fp32 -> q/k column blocks of
+ * dqkv bf16; gain grads accumulate into dgq/dgk.  TD/cpu_ops.h:510-537. */
+int ne_k_qk_prep_bwd(const float *dq, const float *dk, const void *qkv, int64_t ld,
+                     const float *cosb, const float *sinb, const float *gq, const float *gk,
+                     const float *rq, const float *rk, void *dqkv, float *dgq, float *dgk,
+                     int T, int S, int NH, int NKV, int HD, void *stream);
+/* Causal GQA flash attention forward: o [T,NH*HD] bf16 and lse [T,NH] fp32 (natural log of
+ * the row sum of exp(scale*q.k)).  Rows are t = b*S + s.  TD/mil_dynamic.h:171-223. */
+int ne_k_attn_fwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+                  int64_t ldv, void *o, int64_t ldo, float *lse, int B, int S, int NH, int NKV,
+                  int HD, float scale, void *stream);
+/* Backward: dq [T,NH*HD] fp32, dk [T,NKV*HD] fp32, dv bf16 (GQA-reduced); delta [T,NH] is
+ * scratch.  TD/mil_dynamic.h:583-707, TD/cpu_ops.h:585-605. */
+int ne_k_attn_bwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+                  int64_t ldv, const void *o, int64_t ldo, const float *lse, const void *dout,
+                  int64_t lddo, float *delta, float *dq, int64_t lddq, float *dk, int64_t lddk,
+                  void *dv, int64_t lddv, int B, int S, int NH, int NKV, int HD, float scale,
+                  void *stream);
+/* Fused LM-head + softmax cross-entropy (TD/train.m:493-524, TD/cpu_ops.h:348-382):
+ * logits = x[T,D] . E[V,D]^T are produced tile by tile and never stored.  Forward writes
+ * lse[T] and loss[0] = mean(-log(p_tgt + 1e-10)); part is scratch [T, V/64*2] floats
+ * and tgt_logit/loss_rows scratch [T]. */
+int ne_k_ce_fwd(const void *x, const void *E, const int32_t *targets, int T, int D, int V,
+                float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+                void *stream);
+/* Backward: dlogits bf16 [T,V] = (softmax - onehot) * scale, recomputing the logits. */
+int ne_k_ce_bwd(const void *x, const void *E, const int32_t *targets, const float *lse, int T,
+                int D, int V, float scale, void *dlogits, void *stream);
+/* In-place AdamW over n fp32 elements; elements [0, n_decay) get weight decay.  The grad is
+ * multiplied by *gscale (device scalar).  pb (may be NULL) receives the bf16 weights; the
+ * grad is zeroed when zero_grad.  TD/cpu_ops.h:266-303. */
+int ne_k_adam(float *p, float *g, float *m, float *v, void *pb, int64_t n, int64_t n_decay,
+              float lr, float b1, float b2, float eps, float wd, int t, const float *gscale,
+              int zero_grad, void *stream);
+/* Global grad norm and clip factor: gscale[0] = grad_scale * min(1, clip/norm),
+ * gnorm[0] = grad_scale * ||g||.  partials: scratch of 1024 doubles.  TD/train.m:785-849. */
+int ne_k_grad_norm(const float *g, int64_t n, float grad_scale, float clip, double *partials,
+                   float *gscale, float *gnorm, void *stream);
+/* x[T,D] fp32 = E[tok[t]] (TD/cpu_ops.h:433-439); gE[tok[t]] += dx[t] (TD/cpu_ops.h:441-447). */
+int ne_k_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, void *stream);
+int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, void *stream);
+/* gate[T,H] bf16 = silu(h1)*h3 with h13 = [h1 | h3] rows [T,2H] (TD/mil_dynamic.h:276-281). */
+int ne_k_swiglu_fwd(const void *h13, void *gate, int T, int H, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NE_H */

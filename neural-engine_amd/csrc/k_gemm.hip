@@ -1,0 +1,273 @@
+// bf16 MFMA GEMM for gfx950 with LDS-staged tiles and fused epilogues.
+//
+// C[M,N] = epi(alpha * sum_k A[m,k] B[k,n]).  Operands are bf16 with fp32 accumulation
+// on v_mfma_f32_32x32x16_bf16.  Each operand may be K-contiguous (activation rows,
+// weight rows [N,K]) or M/N-contiguous (the dY^T and X of a weight-gradient GEMM);
+// both are staged into LDS K-contiguous so every MFMA operand is one 16-byte LDS read.
+// M/N-contiguous tiles are transposed in registers in 4x8 blocks on the way into LDS.
+//
+// Replaces the ANE matmuls of TD/mil_dynamic.h (gen_sdpa_fwd_dynamic QKV/Wo,
+// gen_ffn_fused_dynamic W1/W3/W2, gen_ffn_bwd_full_dynamic, gen_wot_dynamic,
+// gen_qkv_bwd_dynamic) and the cblas_sgemm weight-gradient / classifier calls of
+// TD/train.m:500-524, 554-557, 594-597, 654-655, 733-738.
+#include "common.h"
+#include "ne_internal.h"
+
+namespace {
+
+constexpr int NTHREADS = 256;
+
+template <int R, int BK, bool KC>
+struct Stage {
+  // KC: element (r, k) at p[r*ld + k]; otherwise at p[k*ld + r].
+  static constexpr int NCH = KC ? R * BK / 8 : (R / 8) * (BK / 4);
+  static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+  static constexpr int NV = KC ? PER : PER * 4;
+  u16x8 v[NV];
+
+  __device__ __forceinline__ void load(const bf16_t *p, long ld, int r0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      int c = tid + i * NTHREADS;
+      if (NCH % NTHREADS == 0 || c < NCH) {
+        if (KC) {
+          int r = c / (BK / 8), k8 = c % (BK / 8);
+          v[i] = *(const u16x8 *)(p + (long)(r0 + r) * ld + k0 + k8 * 8);
+        } else {
+          int kb = c / (R / 8), rc = c % (R / 8);
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            v[i * 4 + j] = *(const u16x8 *)(p + (long)(k0 + kb * 4 + j) * ld + r0 + rc * 8);
+        }
+      }
+    }
+  }
+
+  template <int PITCH>
+  __device__ __forceinline__ void store(bf16_t *lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      int c = tid + i * NTHREADS;
+      if (NCH % NTHREADS == 0 || c < NCH) {
+        if (KC) {
+          int r = c / (BK / 8), k8 = c % (BK / 8);
+          *(u16x8 *)(lds + r * PITCH + k8 * 8) = v[i];
+        } else {
+          int kb = c / (R / 8), rc = c % (R / 8);
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            u16x4 t;
+            t[0] = v[i * 4 + 0][e];
+            t[1] = v[i * 4 + 1][e];
+            t[2] = v[i * 4 + 2][e];
+            t[3] = v[i * 4 + 3][e];
+            *(u16x4 *)(lds + (rc * 8 + e) * PITCH + kb * 4) = t;
+          }
+        }
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
+__global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
+  constexpr int PITCH = BK + 8;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  static_assert(WM * WN == 4, "4 waves");
+  static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][(BM + BN) * PITCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const bf16_t *A = (const bf16_t *)g.A;
+  const bf16_t *B = (const bf16_t *)g.B;
+
+  Stage<BM, BK, AKC> sa;
+  Stage<BN, BK, BKC> sb;
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  const int nk = g.K / BK;
+  sa.load(A, g.lda, m0, 0, tid);
+  sb.load(B, g.ldb, n0, 0, tid);
+  sa.template store<PITCH>(lds[0], tid);
+  sb.template store<PITCH>(lds[0] + BM * PITCH, tid);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      sa.load(A, g.lda, m0, (kt + 1) * BK, tid);
+      sb.load(B, g.ldb, n0, (kt + 1) * BK, tid);
+    }
+    const bf16_t *As = lds[cur];
+    const bf16_t *Bs = lds[cur] + BM * PITCH;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; kk++) {
+      bf16x8 a[FM], b[FN];
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+        a[i] = as_bf16x8(*(const u16x8 *)(As + (wm * TM + i * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        b[j] = as_bf16x8(*(const u16x8 *)(Bs + (wn * TN + j * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) {
+      sa.template store<PITCH>(lds[cur ^ 1], tid);
+      sb.template store<PITCH>(lds[cur ^ 1] + BM * PITCH, tid);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane owns column (lane & 31) and rows 8*(e/4) + 4*(lane/32) + e%4 ----
+  const float alpha = g.alpha;
+  if constexpr (EPI == EPI_CE_FWD) {
+    // Per row of this N-tile: max and sum of exp over the tile's columns, plus the
+    // target logit when the target column falls in the tile.
+    __shared__ float red_m[WN][BM], red_s[WN][BM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int rl = wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int row = m0 + rl;
+        const int tgt = g.targets[row];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const float v = acc[i][j][e] * alpha;
+          mx = fmaxf(mx, v);
+          const int col = n0 + wn * TN + j * 32 + (lane & 31);
+          if (col == tgt) g.tgt_logit[row] = v;
+        }
+        // reduce over the 32 lanes sharing this row (lanes with equal lane>>5)
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] * alpha - mx);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        if ((lane & 31) == 0) {
+          red_m[wn][rl] = mx;
+          red_s[wn][rl] = s;
+        }
+      }
+    }
+    __syncthreads();
+    for (int r = tid; r < BM; r += NTHREADS) {
+      float mx = red_m[0][r];
+#pragma unroll
+      for (int w = 1; w < WN; w++) mx = fmaxf(mx, red_m[w][r]);
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < WN; w++) s += red_s[w][r] * __expf(red_m[w][r] - mx);
+      float *p = g.part + ((long)(m0 + r) * g.n_tiles + blockIdx.x) * 2;
+      p[0] = mx;
+      p[1] = s;
+    }
+    return;
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn * TN + j * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const float v = acc[i][j][e] * alpha;
+        if constexpr (EPI == EPI_BF16) {
+          ((bf16_t *)g.C)[(long)row * g.ldc + col] = f2bf(v);
+        } else if constexpr (EPI == EPI_F32) {
+          ((float *)g.C)[(long)row * g.ldc + col] = v;
+        } else if constexpr (EPI == EPI_F32_ACC) {
+          ((float *)g.C)[(long)row * g.ldc + col] += v;
+        } else if constexpr (EPI == EPI_RESID) {
+          ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
+        } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+          const bf16_t *h = (const bf16_t *)g.R + (long)row * g.ldr;
+          const float h1 = bf2f(h[col]), h3 = bf2f(h[g.N + col]);
+          const float sg = fast_sigmoid(h1);
+          bf16_t *d = (bf16_t *)g.C + (long)row * g.ldc;
+          d[col] = f2bf(v * h3 * sg * (1.f + h1 * (1.f - sg)));
+          d[g.N + col] = f2bf(v * h1 * sg);
+        } else if constexpr (EPI == EPI_CE_BWD) {
+          float p = __expf(v - g.lse[row]);
+          if (col == g.targets[row]) p -= 1.f;
+          ((bf16_t *)g.C)[(long)row * g.ldc + col] = f2bf(p * g.scale);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+namespace {
+
+template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int EPI>
+int launch_t(GemmArgs g, hipStream_t s) {
+  g.n_tiles = g.N / BN;
+  dim3 grid(g.N / BN, g.M / BM);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(NTHREADS), 0, s, g);
+  return ne_hip_status(hipGetLastError(), "gemm launch");
+}
+
+template <bool AKC, bool BKC, int EPI>
+int launch_e(GemmArgs g, hipStream_t s) {
+  if (gemm_tile_n(g.M, g.N, g.K, EPI) == 128) return launch_t<128, 128, 2, 2, AKC, BKC, EPI>(g, s);
+  return launch_t<64, 64, 2, 2, AKC, BKC, EPI>(g, s);
+}
+
+template <bool AKC, bool BKC>
+int launch_l(int epi, GemmArgs g, hipStream_t s) {
+  switch (epi) {
+    case EPI_BF16: return launch_e<AKC, BKC, EPI_BF16>(g, s);
+    case EPI_F32: return launch_e<AKC, BKC, EPI_F32>(g, s);
+    case EPI_F32_ACC: return launch_e<AKC, BKC, EPI_F32_ACC>(g, s);
+    case EPI_RESID: return launch_e<AKC, BKC, EPI_RESID>(g, s);
+    case EPI_SWIGLU_BWD: return launch_e<AKC, BKC, EPI_SWIGLU_BWD>(g, s);
+    case EPI_CE_FWD: return launch_e<AKC, BKC, EPI_CE_FWD>(g, s);
+    case EPI_CE_BWD: return launch_e<AKC, BKC, EPI_CE_BWD>(g, s);
+  }
+  return ne_fail(NE_ERR_ARG, "gemm: unknown epilogue %d", epi);
+}
+
+}  // namespace
+
+int gemm_tile_n(int M, int N, int K, int epi) {
+  (void)K;
+  (void)epi;
+  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= 512) return 128;
+  return 64;
+}
+
+int gemm_launch(int layout, int epi, GemmArgs g, hipStream_t s) {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
+    return ne_fail(NE_ERR_ARG, "gemm: M=%d N=%d K=%d must be positive multiples of 64", g.M, g.N, g.K);
+  if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
+    return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
+  switch (layout) {
+    case 0: return launch_l<true, true>(epi, g, s);
+    case 1: return launch_l<false, true>(epi, g, s);
+    case 2: return launch_l<true, false>(epi, g, s);
+    case 3: return launch_l<false, false>(epi, g, s);
+  }
+  return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
+}

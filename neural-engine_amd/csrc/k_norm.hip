@@ -1,0 +1,334 @@
+// Embedding gather/scatter, RMSNorm fwd/bwd, SwiGLU gate, and the RoPE + QK-RMSNorm
+// prologue/epilogue of attention.  All HBM-bound: one wavefront per token row,
+// float4 / 8-byte vector accesses, fp32 arithmetic.
+#include "common.h"
+#include "ne_internal.h"
+
+namespace {
+
+// x[t, :] = E[tok[t], :]   (TD/cpu_ops.h:433-439 embed_lookup; token-major here)
+__global__ void embed_fwd_kernel(const float *__restrict__ E, const int32_t *__restrict__ tok,
+                                 float *__restrict__ x, int T, int D) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const float4 *src = (const float4 *)(E + (long)tok[row] * D);
+  float4 *dst = (float4 *)(x + (long)row * D);
+  for (int i = lane; i < D / 4; i += 64) dst[i] = src[i];
+}
+
+// gE[tok[t], :] += dx[t, :]   (TD/cpu_ops.h:441-447 embed_backward)
+__global__ void embed_bwd_kernel(float *__restrict__ gE, const int32_t *__restrict__ tok,
+                                 const float *__restrict__ dx, int T, int D) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  float *dst = gE + (long)tok[row] * D;
+  const float *src = dx + (long)row * D;
+  for (int i = lane; i < D; i += 64) atomicAdd(dst + i, src[i]);
+}
+
+// y = x * r * g, r = (mean(x^2) + eps)^-1/2   (TD/cpu_ops.h:20-60 rmsnorm)
+__global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
+                                   bf16_t *__restrict__ y, float *__restrict__ rr, int T, int D,
+                                   float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const float4 *xr = (const float4 *)(x + (long)row * D);
+  float ss = 0.f;
+  for (int i = lane; i < D / 4; i += 64) {
+    float4 v = xr[i];
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  if (lane == 0) rr[row] = r;
+  u16x4 *yr = (u16x4 *)(y + (long)row * D);
+  const float4 *gv = (const float4 *)g;
+  for (int i = lane; i < D / 4; i += 64) {
+    float4 v = xr[i], w = gv[i];
+    u16x4 o;
+    o[0] = f2bf(v.x * r * w.x);
+    o[1] = f2bf(v.y * r * w.y);
+    o[2] = f2bf(v.z * r * w.z);
+    o[3] = f2bf(v.w * r * w.w);
+    yr[i] = o;
+  }
+}
+
+// Exact RMSNorm backward with fused residual add and gain-gradient accumulation:
+//   dx = r*g*dy - x*r^3*sum(dy*x*g)/D (+ resid);  dg += sum_t dy*x*r
+//   dxb = bf16(bscale * dx)  (the alpha-scaled operand of the next GEMM)
+// Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).
+constexpr int RMSB_MAXV = 8;  // float4 per lane: D <= 2048
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+    const float *__restrict__ dy, const float *__restrict__ x, const float *__restrict__ g,
+    const float *__restrict__ rr, const float *__restrict__ resid, float *__restrict__ dx,
+    bf16_t *__restrict__ dxb, float bscale, float *__restrict__ dg, int T, int D, int rows_per_block) {
+  __shared__ float red[4][2048];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int D4 = D / 4;
+  const int nv = (D4 + 63) / 64;  // float4 per lane
+  float4 acc[RMSB_MAXV];
+  for (int j = 0; j < RMSB_MAXV; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 *gv = (const float4 *)g;
+  const float invD = 1.0f / (float)D;
+  const int r0 = blockIdx.x * rows_per_block;
+  const int r1 = min(T, r0 + rows_per_block);
+  for (int row = r0 + wave; row < r1; row += 4) {
+    const float4 *dyr = (const float4 *)(dy + (long)row * D);
+    const float4 *xr = (const float4 *)(x + (long)row * D);
+    const float r = rr[row];
+    float dot = 0.f;
+    float4 dyv[RMSB_MAXV], xv[RMSB_MAXV];
+#pragma unroll
+    for (int j = 0; j < RMSB_MAXV; j++) {
+      dyv[j] = xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < nv && lane + 64 * j < D4) {
+        dyv[j] = dyr[lane + 64 * j];
+        xv[j] = xr[lane + 64 * j];
+        float4 w = gv[lane + 64 * j];
+        dot += dyv[j].x * xv[j].x * w.x + dyv[j].y * xv[j].y * w.y + dyv[j].z * xv[j].z * w.z +
+               dyv[j].w * xv[j].w * w.w;
+      }
+    }
+    dot = wave_sum(dot);
+    const float c = r * r * r * dot * invD;
+    float4 *dxr = (float4 *)(dx + (long)row * D);
+    const float4 *rsr = resid ? (const float4 *)(resid + (long)row * D) : nullptr;
+    u16x4 *dbr = dxb ? (u16x4 *)(dxb + (long)row * D) : nullptr;
+#pragma unroll
+    for (int j = 0; j < RMSB_MAXV; j++) {
+      if (j < nv && lane + 64 * j < D4) {
+        const int i = lane + 64 * j;
+        float4 w = gv[i];
+        float4 o;
+        o.x = r * w.x * dyv[j].x - xv[j].x * c;
+        o.y = r * w.y * dyv[j].y - xv[j].y * c;
+        o.z = r * w.z * dyv[j].z - xv[j].z * c;
+        o.w = r * w.w * dyv[j].w - xv[j].w * c;
+        if (rsr) {
+          float4 q = rsr[i];
+          o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+        }
+        dxr[i] = o;
+        if (dbr) {
+          u16x4 b;
+          b[0] = f2bf(o.x * bscale);
+          b[1] = f2bf(o.y * bscale);
+          b[2] = f2bf(o.z * bscale);
+          b[3] = f2bf(o.w * bscale);
+          dbr[i] = b;
+        }
+        acc[j].x += dyv[j].x * xv[j].x * r;
+        acc[j].y += dyv[j].y * xv[j].y * r;
+        acc[j].z += dyv[j].z * xv[j].z * r;
+        acc[j].w += dyv[j].w * xv[j].w * r;
+      }
+    }
+  }
+  // reduce the 4 waves' gain gradients, one atomic per channel per block
+#pragma unroll
+  for (int j = 0; j < RMSB_MAXV; j++) {
+    if (j < nv && lane + 64 * j < D4) {
+      const int i = (lane + 64 * j) * 4;
+      red[wave][i] = acc[j].x;
+      red[wave][i + 1] = acc[j].y;
+      red[wave][i + 2] = acc[j].z;
+      red[wave][i + 3] = acc[j].w;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < D; i += 256)
+    atomicAdd(dg + i, red[0][i] + red[1][i] + red[2][i] + red[3][i]);
+}
+
+// gate = silu(h1) * h3, h13 = [h1 | h3] per row   (TD/mil_dynamic.h:276-281)
+__global__ void swiglu_fwd_kernel(const bf16_t *__restrict__ h13, bf16_t *__restrict__ gate, int T,
+                                  int H) {
+  const long n4 = (long)T * H / 4;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
+    const long e = i * 4;
+    const long t = e / H, c = e % H;
+    u16x4 a = *(const u16x4 *)(h13 + t * 2 * H + c);
+    u16x4 b = *(const u16x4 *)(h13 + t * 2 * H + H + c);
+    u16x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float h1 = bf2f(a[j]), h3 = bf2f(b[j]);
+      o[j] = f2bf(h1 / (1.f + __expf(-h1)) * h3);
+    }
+    *(u16x4 *)(gate + e) = o;
+  }
+}
+
+// Per (token, head, pair): optional per-head RMSNorm with gain g[HD], then interleaved
+// RoPE on pair (2i, 2i+1) at position t % S with fp32 tables cos/sin [S, HD/2].
+// Head slots 0..NH-1 are q heads (qkv columns h*HD), NH..NH+NKV-1 are k heads
+// (columns NH*HD + (h-NH)*HD).  Replaces the RoPE of gen_sdpa_fwd_dynamic
+// (TD/mil_dynamic.h:133-169).
+template <bool QKN>
+__global__ void qk_prep_fwd_kernel(const bf16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
+                                   const float *__restrict__ sinb, const float *__restrict__ gq,
+                                   const float *__restrict__ gk, bf16_t *__restrict__ qr,
+                                   bf16_t *__restrict__ kr, float *__restrict__ rq, float *__restrict__ rk,
+                                   int T, int S, int NH, int NKV, int HD, float eps) {
+  const int half = HD / 2;
+  const long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  const long total = (long)T * (NH + NKV) * half;
+  if (gid >= total) return;  // total is a multiple of 64: whole waves exit together
+  const int i = gid % half;
+  const long th = gid / half;
+  const int h = th % (NH + NKV);
+  const long t = th / (NH + NKV);
+  const bool isq = h < NH;
+  const int hh = isq ? h : h - NH;
+  const long col = (isq ? 0 : (long)NH * HD) + (long)hh * HD + 2 * i;
+  const uint32_t pr = *(const uint32_t *)(qkv + t * ld + col);
+  float x0 = bf2f((bf16_t)(pr & 0xFFFF)), x1 = bf2f((bf16_t)(pr >> 16));
+  if (QKN) {
+    float ss = x0 * x0 + x1 * x1;
+    for (int o = 1; o < half; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    const float r = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float *gg = isq ? gq : gk;
+    x0 = x0 * r * gg[2 * i];
+    x1 = x1 * r * gg[2 * i + 1];
+    if (i == 0) {
+      if (isq) rq[t * NH + hh] = r;
+      else rk[t * NKV + hh] = r;
+    }
+  }
+  const int pos = t % S;
+  const float c = cosb[pos * half + i], s = sinb[pos * half + i];
+  const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+  const uint32_t out = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+  if (isq) *(uint32_t *)(qr + t * (long)NH * HD + (long)hh * HD + 2 * i) = out;
+  else *(uint32_t *)(kr + t * (long)NKV * HD + (long)hh * HD + 2 * i) = out;
+}
+
+// Backward of qk_prep: inverse rotation (TD/cpu_ops.h:510-537), then the exact
+// per-head RMSNorm backward; gain gradients reduced per block, one atomic per channel.
+// Block = 256 threads = 256/(HD/2) token rows of one head slot; grid.y = head slot.
+template <bool QKN>
+__global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
+    const float *__restrict__ dq, const float *__restrict__ dk, const bf16_t *__restrict__ qkv, long ld,
+    const float *__restrict__ cosb, const float *__restrict__ sinb, const float *__restrict__ gq,
+    const float *__restrict__ gk, const float *__restrict__ rq, const float *__restrict__ rk,
+    bf16_t *__restrict__ dqkv, float *__restrict__ dgq, float *__restrict__ dgk, int T, int S, int NH,
+    int NKV, int HD, int tok_per_block) {
+  __shared__ float red[256 * 2];
+  const int half = HD / 2;
+  const int i = threadIdx.x % half;
+  const int sub = threadIdx.x / half, nsub = 256 / half;
+  const int h = blockIdx.y;
+  const bool isq = h < NH;
+  const int hh = isq ? h : h - NH;
+  const long col = (isq ? 0 : (long)NH * HD) + (long)hh * HD + 2 * i;
+  const float *gg = isq ? gq : gk;
+  float g0 = 0.f, g1 = 0.f;
+  if (QKN) {
+    g0 = gg[2 * i];
+    g1 = gg[2 * i + 1];
+  }
+  float a0 = 0.f, a1 = 0.f;
+  const long t0 = (long)blockIdx.x * tok_per_block;
+  const long t1 = min((long)T, t0 + tok_per_block);
+  for (long t = t0 + sub; t < t1; t += nsub) {
+    const float *d = isq ? dq + t * (long)NH * HD + (long)hh * HD : dk + t * (long)NKV * HD + (long)hh * HD;
+    const float2 dd = *(const float2 *)(d + 2 * i);
+    const int pos = t % S;
+    const float c = cosb[pos * half + i], s = sinb[pos * half + i];
+    float d0 = dd.x * c + dd.y * s;
+    float d1 = dd.y * c - dd.x * s;
+    if (QKN) {
+      const uint32_t pr = *(const uint32_t *)(qkv + t * ld + col);
+      const float x0 = bf2f((bf16_t)(pr & 0xFFFF)), x1 = bf2f((bf16_t)(pr >> 16));
+      const float r = isq ? rq[t * NH + hh] : rk[t * NKV + hh];
+      float dot = d0 * x0 * g0 + d1 * x1 * g1;
+      for (int o = 1; o < half; o <<= 1) dot += __shfl_xor(dot, o, 64);
+      const float cc = r * r * r * dot / (float)HD;
+      a0 += d0 * x0 * r;
+      a1 += d1 * x1 * r;
+      d0 = r * g0 * d0 - x0 * cc;
+      d1 = r * g1 * d1 - x1 * cc;
+    }
+    *(uint32_t *)(dqkv + t * ld + col) = (uint32_t)f2bf(d0) | ((uint32_t)f2bf(d1) << 16);
+  }
+  if (QKN) {
+    red[threadIdx.x * 2] = a0;
+    red[threadIdx.x * 2 + 1] = a1;
+    __syncthreads();
+    if (sub == 0) {
+      float s0 = 0.f, s1 = 0.f;
+      for (int k = 0; k < nsub; k++) {
+        s0 += red[(k * half + i) * 2];
+        s1 += red[(k * half + i) * 2 + 1];
+      }
+      float *dg = isq ? dgq : dgk;
+      atomicAdd(dg + 2 * i, s0);
+      atomicAdd(dg + 2 * i + 1, s1);
+    }
+  }
+}
+
+}  // namespace
+
+int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, hipStream_t s) {
+  if (D % 4) return ne_fail(NE_ERR_ARG, "embed: D %% 4 != 0");
+  hipLaunchKernelGGL(embed_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, E, tok, x, T, D);
+  return ne_hip_status(hipGetLastError(), "embed_fwd");
+}
+
+int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, hipStream_t s) {
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, dx, T, D);
+  return ne_hip_status(hipGetLastError(), "embed_bwd");
+}
+
+int launch_rmsnorm_fwd(const float *x, const float *g, bf16_t *y, float *r, int T, int D, float eps,
+                       hipStream_t s) {
+  if (D % 4) return ne_fail(NE_ERR_ARG, "rmsnorm: D %% 4 != 0");
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, g, y, r, T, D, eps);
+  return ne_hip_status(hipGetLastError(), "rmsnorm_fwd");
+}
+
+int launch_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
+                       const float *resid, float *dx, bf16_t *dxb, float bscale, float *dg, int T,
+                       int D, hipStream_t s) {
+  if (D % 4 || D > 2048) return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
+  const int rows = 64;
+  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((T + rows - 1) / rows), dim3(256), 0, s, dy, x, g, r,
+                     resid, dx, dxb, bscale, dg, T, D, rows);
+  return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
+}
+
+int launch_swiglu_fwd(const bf16_t *h13, bf16_t *gate, int T, int H, hipStream_t s) {
+  if (H % 4) return ne_fail(NE_ERR_ARG, "swiglu: H %% 4 != 0");
+  const long n4 = (long)T * H / 4;
+  const int blocks = (int)std::min<long>((n4 + 255) / 256, 8192);
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(blocks), dim3(256), 0, s, h13, gate, T, H);
+  return ne_hip_status(hipGetLastError(), "swiglu_fwd");
+}
+
+int launch_qk_prep_fwd(const bf16_t *qkv, long ld, const float *cosb, const float *sinb,
+                       const float *gq, const float *gk, bf16_t *qr, bf16_t *kr, float *rq,
+                       float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s) {
+  if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
+  const long total = (long)T * (NH + NKV) * (HD / 2);
+  const int blocks = (int)((total + 255) / 256);
+  if (gq) hipLaunchKernelGGL(qk_prep_fwd_kernel<true>, dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
+  else hipLaunchKernelGGL(qk_prep_fwd_kernel<false>, dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
+  return ne_hip_status(hipGetLastError(), "qk_prep_fwd");
+}
+
+int launch_qk_prep_bwd(const float *dq, const float *dk, const bf16_t *qkv, long ld,
+                       const float *cosb, const float *sinb, const float *gq, const float *gk,
+                       const float *rq, const float *rk, bf16_t *dqkv, float *dgq, float *dgk,
+                       int T, int S, int NH, int NKV, int HD, hipStream_t s) {
+  if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
+  const int tpb = 256;
+  dim3 grid((T + tpb - 1) / tpb, NH + NKV);
+  if (gq) hipLaunchKernelGGL(qk_prep_bwd_kernel<true>, grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, T, S, NH, NKV, HD, tpb);
+  else hipLaunchKernelGGL(qk_prep_bwd_kernel<false>, grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, T, S, NH, NKV, HD, tpb);
+  return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
+}

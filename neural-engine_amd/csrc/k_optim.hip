@@ -1,0 +1,121 @@
+// Gradient norm / clip and the single-pass fused AdamW over the flat parameter buffer.
+//
+// Replaces TD/train.m:782-849 (grad scale, global L2 norm, clip) and
+// TD/cpu_ops.h:266-303 adam_update called per tensor (TD/train.m:861-897), plus the
+// fp16 weight restaging of TD/train.m:872-895: here the update writes the bf16 shadow
+// the GEMMs read, in the same pass.  Per element: read p, g, m, v (16 B), write
+// p, m, v (12 B), bf16 shadow (2 B), zeroed g (4 B) = 34 B.
+#include "common.h"
+#include "ne_internal.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void sumsq_kernel(const float *__restrict__ g, long n,
+                                                    double *__restrict__ partials) {
+  __shared__ float red[4];
+  const long n4 = n / 4;
+  float acc = 0.f;
+  const float4 *g4 = (const float4 *)g;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const float4 v = g4[i];
+    acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  if (blockIdx.x == 0)
+    for (long i = n4 * 4 + threadIdx.x; i < n; i += 256) acc += g[i] * g[i];
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partials[blockIdx.x] = (double)red[0] + red[1] + red[2] + red[3];
+}
+
+// norm = grad_scale * sqrt(sum partials); factor = grad_scale * (clip / norm if norm > clip)
+__global__ void clip_finalize_kernel(const double *__restrict__ partials, int nparts, float grad_scale,
+                                     float clip, float *__restrict__ gscale, float *__restrict__ gnorm) {
+  double s = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += 64) s += partials[i];
+  s = wave_sum_d(s);
+  if (threadIdx.x == 0) {
+    const float norm = (float)(sqrt(s) * (double)grad_scale);
+    float f = grad_scale;
+    if (clip > 0.f && norm > clip) f *= clip / norm;
+    gscale[0] = f;
+    gnorm[0] = norm;
+  }
+}
+
+template <bool SHADOW>
+__global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
+  const float gs = a.gscale[0];
+  const float ob1 = 1.f - a.b1, ob2 = 1.f - a.b2;
+  const float ibc1 = 1.f / a.bc1, ibc2 = 1.f / a.bc2;
+  const long n4 = a.n / 4;
+  float4 *p4 = (float4 *)a.p, *g4 = (float4 *)a.g, *m4 = (float4 *)a.m, *v4 = (float4 *)a.v;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    float4 p = p4[i], g = g4[i], m = m4[i], v = v4[i];
+    const float wd = (i * 4 < a.n_decay) ? a.wd : 0.f;
+    float pe[4] = {p.x, p.y, p.z, p.w}, ge[4] = {g.x, g.y, g.z, g.w};
+    float me[4] = {m.x, m.y, m.z, m.w}, ve[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float gg = ge[j] * gs;
+      me[j] = a.b1 * me[j] + ob1 * gg;
+      ve[j] = a.b2 * ve[j] + ob2 * (gg * gg);
+      const float mh = me[j] * ibc1, vh = ve[j] * ibc2;
+      pe[j] -= a.lr * (mh / (sqrtf(vh) + a.eps) + wd * pe[j]);
+    }
+    p4[i] = make_float4(pe[0], pe[1], pe[2], pe[3]);
+    m4[i] = make_float4(me[0], me[1], me[2], me[3]);
+    v4[i] = make_float4(ve[0], ve[1], ve[2], ve[3]);
+    if (a.zero_grad) g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (SHADOW) {
+      u16x4 b;
+      b[0] = f2bf(pe[0]);
+      b[1] = f2bf(pe[1]);
+      b[2] = f2bf(pe[2]);
+      b[3] = f2bf(pe[3]);
+      ((u16x4 *)a.pb)[i] = b;
+    }
+  }
+}
+
+__global__ void f32_to_bf16_kernel(const float *__restrict__ src, bf16_t *__restrict__ dst, long n) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = f2bf(src[i]);
+}
+
+__global__ void fill_f32_kernel(float *__restrict__ dst, float v, long n) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = v;
+}
+
+int grid_for(long n) { return (int)std::max<long>(1, std::min<long>((n + 255) / 256, 256L * 32)); }
+
+}  // namespace
+
+int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s) {
+  hipLaunchKernelGGL(sumsq_kernel, dim3(nparts), dim3(256), 0, s, g, n, partials);
+  return ne_hip_status(hipGetLastError(), "sumsq");
+}
+
+int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
+                         float *gscale_out, float *gnorm_out, hipStream_t s) {
+  hipLaunchKernelGGL(clip_finalize_kernel, dim3(1), dim3(64), 0, s, partials, nparts, grad_scale, clip,
+                     gscale_out, gnorm_out);
+  return ne_hip_status(hipGetLastError(), "clip_finalize");
+}
+
+int launch_adam(const AdamArgs &a, hipStream_t s) {
+  if (a.n % 4 || a.n_decay % 4) return ne_fail(NE_ERR_ARG, "adam: sizes must be multiples of 4");
+  const int grid = grid_for(a.n / 4);
+  if (a.pb) hipLaunchKernelGGL(adam_kernel<true>, dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(adam_kernel<false>, dim3(grid), dim3(256), 0, s, a);
+  return ne_hip_status(hipGetLastError(), "adam");
+}
+
+int launch_f32_to_bf16(const float *src, bf16_t *dst, long n, hipStream_t s) {
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+  return ne_hip_status(hipGetLastError(), "f32_to_bf16");
+}
+
+int launch_fill_f32(float *dst, float v, long n, hipStream_t s) {
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, s, dst, v, n);
+  return ne_hip_status(hipGetLastError(), "fill_f32");
+}

@@ -1,0 +1,65 @@
+// The context object shared by the orchestrator (ne_host.hip) and the token loop
+// (k_decode.hip).
+#pragma once
+#include <vector>
+
+#include "../../include/ne.h"
+#include "ne_internal.h"
+
+struct Prof {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  struct Rec { int fam; hipEvent_t a, b; };
+  std::vector<Rec> pending;
+  double ms[NE_PROF_COUNT] = {};
+  int64_t cnt[NE_PROF_COUNT] = {};
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e;
+    hipEventCreate(&e);
+    return e;
+  }
+};
+
+struct LayerAct {
+  float *x_in, *r1, *x2, *r2, *rq, *rk, *lse;
+  bf16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
+};
+
+struct LayerOff {
+  long wqkv, wo, w13, w2, g_att, g_ffn, gq, gk;
+};
+
+struct ne_ctx {
+  ne_config c;
+  int D, H, NH, NKV, HD, L, V, S, B, T, Q, KV, QKV;
+  hipStream_t st = nullptr;
+  long n_params = 0, n_decay = 0;
+  float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
+  bf16_t *Pb = nullptr;
+  std::vector<LayerOff> lo;
+  long off_E = 0, off_gfinal = 0;
+  std::vector<long> t_off, t_numel;  // per tensor id
+  void *arena = nullptr;
+  std::vector<LayerAct> act;
+  float *xL, *rf;
+  bf16_t *xf;
+  float *dx, *dx2, *dtmp, *dq, *dk, *delta;
+  bf16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
+  float *ce_part, *ce_tgt, *ce_lse, *ce_rows, *loss;
+  int32_t *tok_in, *tok_tgt;
+  float *cosb, *sinb;
+  double *gn_part;
+  float *gscale, *gnorm;
+  int32_t *h_tok = nullptr;  // pinned [2T]
+  float *h_scalar = nullptr; // pinned [4]
+  ne_train_state state = {};
+  Prof prof;
+  // token loop (k_decode.hip)
+  void *dec = nullptr;
+};
+

@@ -1,0 +1,638 @@
+// Context, device memory plan, the training-step orchestration, the optimizer step and
+// v4 checkpoint I/O.  Host code only; every numeric operation runs in the kernels of
+// k_*.hip on the context's single stream.
+//
+// Device memory (all resident, nothing round-trips through the host during a step):
+//   flat fp32 buffers P (master weights), G (grads), M, V (Adam) and the bf16 shadow Pb
+//   of P, one element order for all five:
+//     per layer: Wqkv [Q+2KV, D] (= Wq;Wk;Wv rows), Wo [D,Q], W13 [2H, D] (= W1;W3 rows),
+//                W2 [D,H]
+//     E [V, D]
+//     gains: per layer rms_att [D], rms_ffn [D] (+ q_norm, k_norm [HD]); rms_final [D]
+//   so AdamW is one pass over all parameters and weight decay applies to the prefix
+//   before the gains.  Activations are token-major [T, features] (T = B*S).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "ne_ctx.h"
+
+int ce_forward(const void *x, const void *E, const int32_t *targets, int T, int D, int V, float *part,
+               float *tgt_logit, float *lse, float *loss_rows, float *loss, hipStream_t s);
+int ce_backward(const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D, int V,
+                float scale, void *dlogits, hipStream_t s);
+int decode_run(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temp, float top_p,
+               const double *uniforms, int32_t *out);
+int decode_alloc(ne_ctx *ctx);
+void decode_free(ne_ctx *ctx);
+
+namespace {
+
+constexpr int CKPT_MAGIC = 0x424C5A54;
+constexpr int QKN_TAG = 0x314E4B51;
+
+#pragma pack(push, 4)
+struct CkptHdr {  // TD/config.h:82-91, 96 bytes with native alignment
+  int32_t magic, version, step, total_steps;
+  int32_t n_layers, vocab_size, dim, hidden_dim, n_heads, seq_len;
+  float lr, loss;
+  double cum_compile, cum_train, cum_wall;
+  int32_t cum_steps, cum_batches, adam_t;
+  int32_t kv_heads, head_dim, q_dim;
+};
+#pragma pack(pop)
+static_assert(sizeof(CkptHdr) == 96, "v4 header is 96 bytes");
+
+}  // namespace
+
+namespace {
+
+// Two-pass bump allocator: sizes are summed first, then carved out of one allocation.
+struct Plan {
+  size_t total = 0;
+  std::vector<std::pair<void **, size_t>> items;
+  template <typename T>
+  void add(T **p, size_t n) {
+    items.push_back({(void **)p, n * sizeof(T)});
+    total += (n * sizeof(T) + 255) & ~(size_t)255;
+  }
+  void assign(char *base) {
+    size_t off = 0;
+    for (auto &it : items) {
+      *it.first = base + off;
+      off += (it.second + 255) & ~(size_t)255;
+    }
+  }
+};
+
+void prof_begin(ne_ctx *c, int fam, hipEvent_t *e0) {
+  if (!c->prof.on) return;
+  *e0 = c->prof.get();
+  hipEventRecord(*e0, c->st);
+  (void)fam;
+}
+void prof_end(ne_ctx *c, int fam, hipEvent_t e0) {
+  if (!c->prof.on) return;
+  hipEvent_t e1 = c->prof.get();
+  hipEventRecord(e1, c->st);
+  c->prof.pending.push_back({fam, e0, e1});
+}
+
+struct ProfScope {
+  ne_ctx *c;
+  int fam;
+  hipEvent_t e0 = nullptr;
+  ProfScope(ne_ctx *c_, int f) : c(c_), fam(f) { prof_begin(c, fam, &e0); }
+  ~ProfScope() { prof_end(c, fam, e0); }
+};
+
+int prof_collect(ne_ctx *c) {
+  if (c->prof.pending.empty()) return 0;
+  NE_HIP(hipStreamSynchronize(c->st));
+  for (auto &r : c->prof.pending) {
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, r.a, r.b);
+    c->prof.ms[r.fam] += ms;
+    c->prof.cnt[r.fam] += 1;
+    c->prof.pool.push_back(r.a);
+    c->prof.pool.push_back(r.b);
+  }
+  c->prof.pending.clear();
+  return 0;
+}
+
+int gemm(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, const void *A, long lda, const void *B,
+         long ldb, void *C, long ldc, const void *R = nullptr, long ldr = 0, float alpha = 1.f) {
+  ProfScope ps(c, fam);
+  GemmArgs g = {};
+  g.M = M; g.N = N; g.K = K;
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.R = R; g.ldr = ldr;
+  g.alpha = alpha;
+  return gemm_launch(layout, epi, g, c->st);
+}
+
+int validate(const ne_config *c) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null config");
+  if (c->dim <= 0 || c->hidden <= 0 || c->n_heads <= 0 || c->kv_heads <= 0 || c->head_dim <= 0 ||
+      c->n_layers <= 0 || c->vocab <= 0 || c->seq <= 0 || c->batch <= 0)
+    return ne_fail(NE_ERR_ARG, "config: all dims must be positive");
+  if (c->n_heads % c->kv_heads) return ne_fail(NE_ERR_ARG, "config: n_heads %% kv_heads != 0");
+  if (c->head_dim != 64 && c->head_dim != 128) return ne_fail(NE_ERR_ARG, "config: head_dim must be 64 or 128");
+  if (c->seq % 64) return ne_fail(NE_ERR_ARG, "config: seq must be a multiple of 64");
+  if (c->dim % 64 || c->hidden % 64 || c->vocab % 64)
+    return ne_fail(NE_ERR_ARG, "config: dim, hidden and vocab must be multiples of 64");
+  if (c->dim > 2048) return ne_fail(NE_ERR_ARG, "config: dim > 2048 unsupported");
+  if (c->decode_batch < 0 || c->decode_ctx < 0) return ne_fail(NE_ERR_ARG, "config: negative decode sizes");
+  return 0;
+}
+
+void layout_params(ne_ctx *c) {
+  const long D = c->D, H = c->H, Q = c->Q, KV = c->KV, HD = c->HD;
+  long off = 0;
+  c->lo.resize(c->L);
+  for (int l = 0; l < c->L; l++) {
+    LayerOff &o = c->lo[l];
+    o.wqkv = off; off += (Q + 2 * KV) * D;
+    o.wo = off; off += D * Q;
+    o.w13 = off; off += 2 * H * D;
+    o.w2 = off; off += D * H;
+  }
+  c->off_E = off; off += (long)c->V * D;
+  c->n_decay = off;
+  for (int l = 0; l < c->L; l++) {
+    LayerOff &o = c->lo[l];
+    o.g_att = off; off += D;
+    o.g_ffn = off; off += D;
+    if (c->c.qk_norm) {
+      o.gq = off; off += HD;
+      o.gk = off; off += HD;
+    } else {
+      o.gq = o.gk = -1;
+    }
+  }
+  c->off_gfinal = off; off += D;
+  c->n_params = off;
+  // tensor ids in checkpoint order
+  c->t_off.clear();
+  c->t_numel.clear();
+  auto push = [&](long o, long n) { c->t_off.push_back(o); c->t_numel.push_back(n); };
+  for (int l = 0; l < c->L; l++) {
+    const LayerOff &o = c->lo[l];
+    push(o.wqkv, Q * D);
+    push(o.wqkv + Q * D, KV * D);
+    push(o.wqkv + (Q + KV) * D, KV * D);
+    push(o.wo, D * Q);
+    push(o.w13, H * D);
+    push(o.w2, D * H);
+    push(o.w13 + H * D, H * D);
+    push(o.g_att, D);
+    push(o.g_ffn, D);
+  }
+  push(c->off_gfinal, D);
+  push(c->off_E, (long)c->V * D);
+  if (c->c.qk_norm)
+    for (int l = 0; l < c->L; l++) {
+      push(c->lo[l].gq, HD);
+      push(c->lo[l].gk, HD);
+    }
+}
+
+float *kind_base(ne_ctx *c, int kind) {
+  switch (kind) {
+    case NE_PARAM: return c->P;
+    case NE_GRAD: return c->G;
+    case NE_ADAM_M: return c->M;
+    case NE_ADAM_V: return c->Vm;
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------ lifetime ----
+
+extern "C" ne_ctx *ne_create(const ne_config *cfg) {
+  if (validate(cfg)) return nullptr;
+  ne_ctx *c = new ne_ctx();
+  c->c = *cfg;
+  c->D = cfg->dim; c->H = cfg->hidden; c->NH = cfg->n_heads; c->NKV = cfg->kv_heads; c->HD = cfg->head_dim;
+  c->L = cfg->n_layers; c->V = cfg->vocab; c->S = cfg->seq; c->B = cfg->batch; c->T = c->B * c->S;
+  c->Q = c->NH * c->HD; c->KV = c->NKV * c->HD; c->QKV = c->Q + 2 * c->KV;
+  layout_params(c);
+  const size_t T = c->T, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, NH = c->NH, NKV = c->NKV;
+  Plan pl;
+  pl.add(&c->P, c->n_params);
+  pl.add(&c->G, c->n_params);
+  pl.add(&c->M, c->n_params);
+  pl.add(&c->Vm, c->n_params);
+  pl.add(&c->Pb, c->n_params);
+  c->act.resize(c->L);
+  for (int l = 0; l < c->L; l++) {
+    LayerAct &a = c->act[l];
+    pl.add(&a.x_in, T * D); pl.add(&a.r1, T); pl.add(&a.xn, T * D);
+    pl.add(&a.qkv, T * QKV); pl.add(&a.qr, T * Q); pl.add(&a.kr, T * KV);
+    pl.add(&a.rq, T * NH); pl.add(&a.rk, T * NKV);
+    pl.add(&a.attn, T * Q); pl.add(&a.lse, T * NH);
+    pl.add(&a.x2, T * D); pl.add(&a.r2, T); pl.add(&a.x2n, T * D);
+    pl.add(&a.h13, T * 2 * H); pl.add(&a.gate, T * H);
+  }
+  pl.add(&c->xL, T * D); pl.add(&c->rf, T); pl.add(&c->xf, T * D);
+  pl.add(&c->dx, T * D); pl.add(&c->dx2, T * D); pl.add(&c->dtmp, T * D);
+  pl.add(&c->dq, T * Q); pl.add(&c->dk, T * KV); pl.add(&c->delta, T * NH);
+  pl.add(&c->dbf, T * D); pl.add(&c->dh13, T * 2 * H); pl.add(&c->dattn, T * Q); pl.add(&c->dqkv, T * QKV);
+  pl.add(&c->dlogits, T * (size_t)c->V);
+  pl.add(&c->ce_part, T * (size_t)(c->V / 64) * 2);
+  pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
+  pl.add(&c->tok_in, T); pl.add(&c->tok_tgt, T);
+  pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
+  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4);
+
+  int rc = 0;
+  if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
+  if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
+  pl.assign((char *)c->arena);
+  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 2 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
+  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_scalar, 4 * sizeof(float), 0), "hipHostMalloc"))) goto fail;
+  // zero weights, gains 1; zero grads and moments
+  if ((rc = ne_hip_status(hipMemsetAsync(c->P, 0, c->n_params * 4, c->st), "memset"))) goto fail;
+  if ((rc = ne_hip_status(hipMemsetAsync(c->G, 0, c->n_params * 4, c->st), "memset"))) goto fail;
+  if ((rc = ne_hip_status(hipMemsetAsync(c->M, 0, c->n_params * 4, c->st), "memset"))) goto fail;
+  if ((rc = ne_hip_status(hipMemsetAsync(c->Vm, 0, c->n_params * 4, c->st), "memset"))) goto fail;
+  if ((rc = launch_fill_f32(c->P + c->n_decay, 1.f, c->n_params - c->n_decay, c->st))) goto fail;
+  if ((rc = launch_f32_to_bf16(c->P, c->Pb, c->n_params, c->st))) goto fail;
+  {
+    // RoPE tables [S, HD/2]: angle = pos * theta^(-2i/HD), evaluated in double
+    const int half = c->HD / 2;
+    std::vector<float> cs((size_t)c->S * half), sn((size_t)c->S * half);
+    for (int p = 0; p < c->S; p++)
+      for (int i = 0; i < half; i++) {
+        const double freq = 1.0 / pow((double)cfg->rope_theta, 2.0 * i / c->HD);
+        const double ang = p * freq;
+        cs[(size_t)p * half + i] = (float)cos(ang);
+        sn[(size_t)p * half + i] = (float)sin(ang);
+      }
+    if ((rc = ne_hip_status(hipMemcpy(c->cosb, cs.data(), cs.size() * 4, hipMemcpyHostToDevice), "rope"))) goto fail;
+    if ((rc = ne_hip_status(hipMemcpy(c->sinb, sn.data(), sn.size() * 4, hipMemcpyHostToDevice), "rope"))) goto fail;
+  }
+  if (cfg->decode_batch > 0 && cfg->decode_ctx > 0)
+    if ((rc = decode_alloc(c))) goto fail;
+  if ((rc = ne_hip_status(hipStreamSynchronize(c->st), "create sync"))) goto fail;
+  return c;
+fail:
+  ne_destroy(c);
+  return nullptr;
+}
+
+extern "C" void ne_destroy(ne_ctx *c) {
+  if (!c) return;
+  if (c->st) hipStreamSynchronize(c->st);
+  decode_free(c);
+  for (auto &r : c->prof.pending) {
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  for (auto e : c->prof.pool) hipEventDestroy(e);
+  if (c->arena) hipFree(c->arena);
+  if (c->h_tok) hipHostFree(c->h_tok);
+  if (c->h_scalar) hipHostFree(c->h_scalar);
+  if (c->st) hipStreamDestroy(c->st);
+  delete c;
+}
+
+extern "C" int ne_sync(ne_ctx *c) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_HIP(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+// ------------------------------------------------------------------------ tensors ----
+
+extern "C" int ne_num_tensors(const ne_ctx *c) { return c ? (int)c->t_off.size() : 0; }
+
+extern "C" int64_t ne_tensor_numel(const ne_ctx *c, int id) {
+  if (!c || id < 0 || id >= (int)c->t_off.size()) return ne_fail(NE_ERR_ARG, "bad tensor id %d", id);
+  return c->t_numel[id];
+}
+
+extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, size_t n) {
+  if (!c || !host) return ne_fail(NE_ERR_ARG, "null argument");
+  if (id < 0 || id >= (int)c->t_off.size()) return ne_fail(NE_ERR_ARG, "bad tensor id %d", id);
+  if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
+  float *base = kind_base(c, kind);
+  if (!base) return ne_fail(NE_ERR_ARG, "bad tensor kind %d", kind);
+  NE_HIP(hipMemcpyAsync(base + c->t_off[id], host, n * 4, hipMemcpyHostToDevice, c->st));
+  if (kind == NE_PARAM) NE_CHECK(launch_f32_to_bf16(c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+extern "C" int ne_get_tensor(ne_ctx *c, int kind, int id, float *host, size_t n) {
+  if (!c || !host) return ne_fail(NE_ERR_ARG, "null argument");
+  if (id < 0 || id >= (int)c->t_off.size()) return ne_fail(NE_ERR_ARG, "bad tensor id %d", id);
+  if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
+  float *base = kind_base(c, kind);
+  if (!base) return ne_fail(NE_ERR_ARG, "bad tensor kind %d", kind);
+  NE_HIP(hipMemcpyAsync(host, base + c->t_off[id], n * 4, hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+extern "C" int ne_get_state(const ne_ctx *c, ne_train_state *st) {
+  if (!c || !st) return ne_fail(NE_ERR_ARG, "null argument");
+  *st = c->state;
+  return 0;
+}
+
+extern "C" int ne_set_state(ne_ctx *c, const ne_train_state *st) {
+  if (!c || !st) return ne_fail(NE_ERR_ARG, "null argument");
+  c->state = *st;
+  return 0;
+}
+
+// ------------------------------------------------------------------- training step ----
+
+extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale, float *loss_out) {
+  if (!c || !tokens) return ne_fail(NE_ERR_ARG, "null argument");
+  const int T = c->T, S = c->S, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, V = c->V;
+  const float alpha = c->c.res_alpha, eps = c->c.norm_eps;
+  for (int b = 0; b < c->B; b++)
+    for (int s = 0; s < S; s++) {
+      const int32_t ti = tokens[(long)b * (S + 1) + s], tt = tokens[(long)b * (S + 1) + s + 1];
+      if (ti < 0 || ti >= V || tt < 0 || tt >= V) return ne_fail(NE_ERR_ARG, "token id out of [0, %d)", V);
+      c->h_tok[(long)b * S + s] = ti;
+      c->h_tok[T + (long)b * S + s] = tt;
+    }
+  NE_HIP(hipMemcpyAsync(c->tok_in, c->h_tok, 2 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
+  const bf16_t *Pb = c->Pb;
+  const float *P = c->P;
+  float *G = c->G;
+  AttnArgs at = {};
+  at.B = c->B; at.S = S; at.NH = c->NH; at.NKV = c->NKV; at.HD = c->HD;
+  at.scale = 1.0f / sqrtf((float)c->HD);
+
+  // ---------------- forward ----------------
+  {
+    ProfScope ps(c, NE_PROF_EMBED);
+    NE_CHECK(launch_embed_fwd(P + c->off_E, c->tok_in, c->act[0].x_in, T, D, c->st));
+  }
+  for (int l = 0; l < c->L; l++) {
+    LayerAct &a = c->act[l];
+    const LayerOff &o = c->lo[l];
+    float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
+    {
+      ProfScope ps(c, NE_PROF_NORM);
+      NE_CHECK(launch_rmsnorm_fwd(a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, c->st));
+    }
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_BF16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
+    {
+      ProfScope ps(c, NE_PROF_ATTN_FWD);
+      NE_CHECK(launch_qk_prep_fwd(a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
+                                  c->c.qk_norm ? P + o.gk : nullptr, a.qr, a.kr, a.rq, a.rk, T, S, c->NH, c->NKV,
+                                  c->HD, eps, c->st));
+      at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
+      at.o = a.attn; at.ldo = Q; at.lse = a.lse;
+      NE_CHECK(launch_attn_fwd(at, c->st));
+    }
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, D, a.x_in, D, alpha));
+    {
+      ProfScope ps(c, NE_PROF_NORM);
+      NE_CHECK(launch_rmsnorm_fwd(a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, c->st));
+    }
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_BF16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
+    {
+      ProfScope ps(c, NE_PROF_NORM);
+      NE_CHECK(launch_swiglu_fwd(a.h13, a.gate, T, H, c->st));
+    }
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, D, a.x2, D, alpha));
+  }
+  {
+    ProfScope ps(c, NE_PROF_NORM);
+    NE_CHECK(launch_rmsnorm_fwd(c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, c->st));
+  }
+  {
+    ProfScope ps(c, NE_PROF_CE);
+    NE_CHECK(ce_forward(c->xf, Pb + c->off_E, c->tok_tgt, T, D, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
+                        c->loss, c->st));
+    NE_CHECK(ce_backward(c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, loss_scale / (float)T, c->dlogits,
+                         c->st));
+  }
+  if (loss_out) NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
+
+  // ---------------- backward ----------------
+  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
+  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_TN, EPI_F32_ACC, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D));
+  {
+    ProfScope ps(c, NE_PROF_NORM);
+    NE_CHECK(launch_rmsnorm_bwd(c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
+                                G + c->off_gfinal, T, D, c->st));
+  }
+  for (int l = c->L - 1; l >= 0; l--) {
+    LayerAct &a = c->act[l];
+    const LayerOff &o = c->lo[l];
+    // FFN: dbf = alpha * dx
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
+                  a.h13, 2 * H));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D));
+    {
+      ProfScope ps(c, NE_PROF_NORM);
+      NE_CHECK(launch_rmsnorm_bwd(c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, T, D,
+                                  c->st));
+    }
+    // attention: dbf = alpha * dx2
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_BF16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q));
+    {
+      ProfScope ps(c, NE_PROF_ATTN_BWD);
+      at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
+      at.o = a.attn; at.ldo = Q; at.lse = a.lse;
+      at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
+      at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = c->dqkv + Q + KV; at.lddv = QKV;
+      NE_CHECK(launch_attn_bwd(at, c->st));
+      NE_CHECK(launch_qk_prep_bwd(c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
+                                  c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
+                                  c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, T, S,
+                                  c->NH, c->NKV, c->HD, c->st));
+    }
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D));
+    {
+      ProfScope ps(c, NE_PROF_NORM);
+      NE_CHECK(launch_rmsnorm_bwd(c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att, T,
+                                  D, c->st));
+    }
+  }
+  {
+    ProfScope ps(c, NE_PROF_EMBED);
+    NE_CHECK(launch_embed_bwd(G + c->off_E, c->tok_in, c->dx, T, D, c->st));
+  }
+  if (loss_out) {
+    NE_HIP(hipStreamSynchronize(c->st));
+    *loss_out = c->h_scalar[0];
+  }
+  return 0;
+}
+
+extern "C" int ne_zero_grads(ne_ctx *c) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  return 0;
+}
+
+extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float eps, float wd, float grad_scale,
+                                 float clip, float *gnorm_out) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  {
+    ProfScope ps(c, NE_PROF_GNORM);
+    NE_CHECK(launch_sumsq(c->G, c->n_params, c->gn_part, 1024, c->st));
+    NE_CHECK(launch_clip_finalize(c->gn_part, 1024, grad_scale, clip, c->gscale, c->gnorm, c->st));
+  }
+  c->state.adam_t += 1;
+  const int t = c->state.adam_t;
+  AdamArgs a = {};
+  a.p = c->P; a.g = c->G; a.m = c->M; a.v = c->Vm; a.pb = c->Pb;
+  a.n = c->n_params; a.n_decay = c->n_decay;
+  a.lr = lr; a.b1 = b1; a.b2 = b2; a.eps = eps; a.wd = wd;
+  a.bc1 = 1.f - powf(b1, (float)t);
+  a.bc2 = 1.f - powf(b2, (float)t);
+  a.gscale = c->gscale; a.zero_grad = 1;
+  {
+    ProfScope ps(c, NE_PROF_ADAM);
+    NE_CHECK(launch_adam(a, c->st));
+  }
+  c->state.lr = lr;
+  if (gnorm_out) {
+    NE_HIP(hipMemcpyAsync(c->h_scalar + 1, c->gnorm, 4, hipMemcpyDeviceToHost, c->st));
+    NE_HIP(hipStreamSynchronize(c->st));
+    *gnorm_out = c->h_scalar[1];
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------------ profiling ----
+
+extern "C" int ne_prof_enable(ne_ctx *c, int on) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(prof_collect(c));
+  c->prof.on = on != 0;
+  return 0;
+}
+
+extern "C" int ne_prof_reset(ne_ctx *c) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(prof_collect(c));
+  for (int i = 0; i < NE_PROF_COUNT; i++) {
+    c->prof.ms[i] = 0;
+    c->prof.cnt[i] = 0;
+  }
+  return 0;
+}
+
+extern "C" int ne_prof_get(ne_ctx *c, int fam, double *ms, int64_t *count) {
+  if (!c || fam < 0 || fam >= NE_PROF_COUNT) return ne_fail(NE_ERR_ARG, "bad profiling family");
+  NE_CHECK(prof_collect(c));
+  if (ms) *ms = c->prof.ms[fam];
+  if (count) *count = c->prof.cnt[fam];
+  return 0;
+}
+
+// ---------------------------------------------------------------------- checkpoints ----
+
+namespace {
+
+size_t ckpt_size(const ne_ctx *c, bool with_qkn) {
+  const size_t D = c->D, H = c->H, Q = c->Q, KV = c->KV, V = c->V;
+  const size_t per_layer = Q * D + 2 * KV * D + D * Q + 3 * H * D + 2 * D;
+  size_t n = c->L * per_layer + D + V * D;
+  size_t sz = sizeof(CkptHdr) + 3 * 4 * n;
+  if (with_qkn) sz += 12 + (size_t)c->L * 6 * c->HD * 4;
+  return sz;
+}
+
+int io_tensor(ne_ctx *c, FILE *f, int id, int kind, bool rd, std::vector<float> &buf) {
+  const size_t n = c->t_numel[id];
+  buf.resize(n);
+  float *dev = kind_base(c, kind) + c->t_off[id];
+  if (rd) {
+    if (fread(buf.data(), 4, n, f) != n) return ne_fail(NE_ERR_FORMAT, "checkpoint truncated at tensor %d", id);
+    NE_HIP(hipMemcpy(dev, buf.data(), n * 4, hipMemcpyHostToDevice));
+  } else {
+    NE_HIP(hipMemcpy(buf.data(), dev, n * 4, hipMemcpyDeviceToHost));
+    if (fwrite(buf.data(), 4, n, f) != n) return ne_fail(NE_ERR_IO, "checkpoint write failed at tensor %d", id);
+  }
+  return 0;
+}
+
+// v4 body order: per layer 9 tensors then their (m, v); rms_final, m, v; embed, m, v.
+int io_body(ne_ctx *c, FILE *f, bool rd, bool qkn) {
+  std::vector<float> buf;
+  for (int l = 0; l < c->L; l++) {
+    for (int j = 0; j < 9; j++) NE_CHECK(io_tensor(c, f, 9 * l + j, NE_PARAM, rd, buf));
+    for (int j = 0; j < 9; j++) {
+      NE_CHECK(io_tensor(c, f, 9 * l + j, NE_ADAM_M, rd, buf));
+      NE_CHECK(io_tensor(c, f, 9 * l + j, NE_ADAM_V, rd, buf));
+    }
+  }
+  for (int id : {9 * c->L, 9 * c->L + 1})
+    for (int kind : {NE_PARAM, NE_ADAM_M, NE_ADAM_V}) NE_CHECK(io_tensor(c, f, id, kind, rd, buf));
+  if (qkn) {
+    int32_t tag[3] = {QKN_TAG, c->L, c->HD};
+    if (rd) {
+      if (fread(tag, 4, 3, f) != 3 || tag[0] != QKN_TAG || tag[1] != c->L || tag[2] != c->HD)
+        return ne_fail(NE_ERR_FORMAT, "checkpoint QK-norm trailer mismatch");
+    } else if (fwrite(tag, 4, 3, f) != 3) {
+      return ne_fail(NE_ERR_IO, "checkpoint write failed");
+    }
+    for (int l = 0; l < c->L; l++)
+      for (int j = 0; j < 2; j++)
+        for (int kind : {NE_PARAM, NE_ADAM_M, NE_ADAM_V})
+          NE_CHECK(io_tensor(c, f, 9 * c->L + 2 + 2 * l + j, kind, rd, buf));
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int ne_load_ckpt_v4(ne_ctx *c, const char *path, ne_train_state *st) {
+  if (!c || !path) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_HIP(hipStreamSynchronize(c->st));
+  FILE *f = fopen(path, "rb");
+  if (!f) return ne_fail(NE_ERR_IO, "cannot open %s", path);
+  CkptHdr h;
+  int rc = 0;
+  if (fread(&h, sizeof h, 1, f) != 1) rc = ne_fail(NE_ERR_FORMAT, "%s: short header", path);
+  else if (h.magic != CKPT_MAGIC || h.version != 4) rc = ne_fail(NE_ERR_FORMAT, "%s: not a v4 checkpoint", path);
+  else if (h.n_layers != c->L || h.vocab_size != c->V || h.dim != c->D || h.hidden_dim != c->H ||
+           h.n_heads != c->NH || h.kv_heads != c->NKV || h.head_dim != c->HD || h.q_dim != c->Q)
+    rc = ne_fail(NE_ERR_FORMAT, "%s: model dims do not match the context", path);
+  if (!rc) {
+    fseek(f, 0, SEEK_END);
+    const size_t sz = (size_t)ftell(f);
+    fseek(f, sizeof h, SEEK_SET);
+    const bool qkn = c->c.qk_norm && sz == ckpt_size(c, true);
+    if (sz != ckpt_size(c, false) && !qkn)
+      rc = ne_fail(NE_ERR_FORMAT, "%s: size %zu, expected %zu", path, sz, ckpt_size(c, c->c.qk_norm));
+    else
+      rc = io_body(c, f, true, qkn);
+  }
+  fclose(f);
+  if (rc) return rc;
+  NE_CHECK(launch_f32_to_bf16(c->P, c->Pb, c->n_params, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  c->state.step = h.step; c->state.total_steps = h.total_steps; c->state.lr = h.lr; c->state.loss = h.loss;
+  c->state.cum_compile = h.cum_compile; c->state.cum_train = h.cum_train; c->state.cum_wall = h.cum_wall;
+  c->state.cum_steps = h.cum_steps; c->state.cum_batches = h.cum_batches; c->state.adam_t = h.adam_t;
+  if (st) *st = c->state;
+  return 0;
+}
+
+extern "C" int ne_save_ckpt_v4(ne_ctx *c, const char *path, const ne_train_state *st) {
+  if (!c || !path) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_HIP(hipStreamSynchronize(c->st));
+  const ne_train_state &s = st ? *st : c->state;
+  CkptHdr h = {};
+  h.magic = CKPT_MAGIC; h.version = 4; h.step = s.step; h.total_steps = s.total_steps;
+  h.n_layers = c->L; h.vocab_size = c->V; h.dim = c->D; h.hidden_dim = c->H; h.n_heads = c->NH; h.seq_len = c->S;
+  h.lr = s.lr; h.loss = s.loss;
+  h.cum_compile = s.cum_compile; h.cum_train = s.cum_train; h.cum_wall = s.cum_wall;
+  h.cum_steps = s.cum_steps; h.cum_batches = s.cum_batches; h.adam_t = s.adam_t;
+  h.kv_heads = c->NKV; h.head_dim = c->HD; h.q_dim = c->Q;
+  FILE *f = fopen(path, "wb");
+  if (!f) return ne_fail(NE_ERR_IO, "cannot create %s", path);
+  int rc = 0;
+  if (fwrite(&h, sizeof h, 1, f) != 1) rc = ne_fail(NE_ERR_IO, "%s: header write failed", path);
+  if (!rc) rc = io_body(c, f, false, c->c.qk_norm != 0);
+  if (fclose(f) != 0 && !rc) rc = ne_fail(NE_ERR_IO, "%s: close failed", path);
+  return rc;
+}
+
+extern "C" int ne_decode(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float temperature, float top_p,
+                         const double *uniforms, int32_t *out_tokens) {
+  if (!c || !prompt || !out_tokens) return ne_fail(NE_ERR_ARG, "null argument");
+  return decode_run(c, prompt, B, P, n_new, temperature, top_p, uniforms, out_tokens);
+}

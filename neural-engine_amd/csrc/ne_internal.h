@@ -1,0 +1,116 @@
+// Internal host-side declarations shared by the kernel files and the orchestrator.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+
+// ---- error plumbing (thread-local last error, negative status codes) ----
+int ne_fail(int code, const char *fmt, ...);
+int ne_hip_status(hipError_t e, const char *what);
+#define NE_HIP(call)                                       \
+  do {                                                     \
+    hipError_t _e = (call);                                \
+    if (_e != hipSuccess) return ne_hip_status(_e, #call); \
+  } while (0)
+#define NE_CHECK(call)      \
+  do {                      \
+    int _r = (call);        \
+    if (_r != 0) return _r; \
+  } while (0)
+
+enum {
+  NE_ERR_ARG = -1,     // invalid argument / unsupported shape
+  NE_ERR_STATE = -2,   // call not valid in the current context state
+  NE_ERR_IO = -3,      // file open/read/write failure
+  NE_ERR_FORMAT = -4,  // checkpoint magic/version/dims/size mismatch
+  NE_ERR_NOMEM = -5,
+};
+
+// ---- GEMM: C[M,N] = epilogue(alpha * A[M,K] . B[K,N]) on bf16 MFMA (k_gemm.hip) ----
+// layout bit 0: A stored M-contiguous ([K,M]); bit 1: B stored N-contiguous ([K,N]).
+enum { GEMM_NT = 0, GEMM_NN = 2, GEMM_TN = 3 };
+enum {
+  EPI_BF16 = 0,        // C bf16
+  EPI_F32 = 1,         // C fp32
+  EPI_F32_ACC = 2,     // C fp32 += result
+  EPI_RESID = 3,       // C fp32 = R fp32 + result
+  EPI_SWIGLU_BWD = 4,  // result is dgate [M,N]; R = h13 bf16 [M,2N]; C = dh13 bf16 [M,2N]
+  EPI_CE_FWD = 5,      // result is logits; writes per-(row, N-tile) max/sumexp + target logit
+  EPI_CE_BWD = 6,      // C bf16 = (exp(logit - lse) - onehot) * scale
+};
+
+struct GemmArgs {
+  int M, N, K;
+  const void *A; long lda;
+  const void *B; long ldb;
+  void *C; long ldc;
+  const void *R; long ldr;   // EPI_RESID: fp32 residual; EPI_SWIGLU_BWD: bf16 h13
+  float alpha;
+  float scale;               // EPI_CE_BWD gradient scale
+  const int32_t *targets;    // [M] (CE epilogues)
+  const float *lse;          // [M] (EPI_CE_BWD)
+  float *part;               // [M, n_tiles, 2] (EPI_CE_FWD): tile max, tile sum exp
+  float *tgt_logit;          // [M] (EPI_CE_FWD)
+  int n_tiles;               // set by the launcher: N / BN
+};
+
+int gemm_launch(int layout, int epi, GemmArgs a, hipStream_t s);
+int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this shape
+
+// ---- embedding / normalisation / elementwise (k_norm.hip) ----
+int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, hipStream_t s);
+int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, hipStream_t s);
+int launch_rmsnorm_fwd(const float *x, const float *g, bf16_t *y, float *r, int T, int D, float eps,
+                       hipStream_t s);
+int launch_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
+                       const float *resid, float *dx, bf16_t *dxb, float bscale, float *dg, int T,
+                       int D, hipStream_t s);
+int launch_swiglu_fwd(const bf16_t *h13, bf16_t *gate, int T, int H, hipStream_t s);
+int launch_qk_prep_fwd(const bf16_t *qkv, long ld, const float *cosb, const float *sinb,
+                       const float *gq, const float *gk, bf16_t *qr, bf16_t *kr, float *rq,
+                       float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s);
+int launch_qk_prep_bwd(const float *dq, const float *dk, const bf16_t *qkv, long ld,
+                       const float *cosb, const float *sinb, const float *gq, const float *gk,
+                       const float *rq, const float *rk, bf16_t *dqkv, float *dgq, float *dgk,
+                       int T, int S, int NH, int NKV, int HD, hipStream_t s);
+
+// ---- attention (k_attn.hip): causal, GQA kv head = q head / (NH/NKV) ----
+struct AttnArgs {
+  const bf16_t *q; long ldq;   // [T, NH*HD] rows of the batch-major token index t = b*S + s
+  const bf16_t *k; long ldk;   // [T, NKV*HD]
+  const bf16_t *v; long ldv;   // [T, NKV*HD]
+  bf16_t *o; long ldo;         // [T, NH*HD]
+  float *lse;                  // [T, NH] natural-log sum exp of scaled scores
+  // backward
+  const bf16_t *dout; long lddo;  // [T, NH*HD]
+  const float *delta;             // [T, NH] rowsum(dO * O)
+  float *dq; long lddq;           // [T, NH*HD] fp32
+  float *dk; long lddk;           // [T, NKV*HD] fp32
+  bf16_t *dv; long lddv;          // [T, NKV*HD] bf16
+  int B, S, NH, NKV, HD;
+  float scale;
+};
+int launch_attn_fwd(const AttnArgs &a, hipStream_t s);
+int launch_attn_bwd(const AttnArgs &a, hipStream_t s);
+
+// ---- cross-entropy reduction (k_ce.hip) ----
+int launch_ce_reduce(const float *part, int n_tiles, const float *tgt_logit, float *lse,
+                     float *loss_rows, float *loss, int T, hipStream_t s);
+
+// ---- optimizer (k_optim.hip) ----
+struct AdamArgs {
+  float *p, *g, *m, *v;
+  bf16_t *pb;           // bf16 shadow of p (may be null)
+  long n, n_decay;      // elements [0, n_decay) get weight decay
+  float lr, b1, b2, eps, wd, bc1, bc2;
+  const float *gscale;  // device scalar: grad_scale * clip factor
+  int zero_grad;        // write g = 0 after the update
+};
+int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s);
+int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
+                         float *gscale_out, float *gnorm_out, hipStream_t s);
+int launch_adam(const AdamArgs &a, hipStream_t s);
+int launch_f32_to_bf16(const float *src, bf16_t *dst, long n, hipStream_t s);
+int launch_fill_f32(float *dst, float v, long n, hipStream_t s);

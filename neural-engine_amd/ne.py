@@ -1,0 +1,242 @@
+"""ctypes binding of libne.so (include/ne.h): the Python harness over the C-ABI.
+
+The library is loaded from this directory; a missing or stale build raises instead of
+falling back to anything else.  Tensor names follow the checkpoint order of the
+reference (TD/train.m:111-129): "layers.{l}.{Wq,Wk,Wv,Wo,W1,W2,W3,rms_att,rms_ffn}",
+"rms_final", "embed", and with QK-norm "layers.{l}.{q_norm,k_norm}".
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libne.so")
+
+NE_PARAM, NE_GRAD, NE_ADAM_M, NE_ADAM_V = 0, 1, 2, 3
+PROF_FAMILIES = ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "norm", "ce", "adam", "gnorm",
+                 "embed", "decode")
+LAYER_TENSORS = ("Wq", "Wk", "Wv", "Wo", "W1", "W2", "W3", "rms_att", "rms_ffn")
+
+# every symbol include/ne.h declares
+EXPORTS = (
+    "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
+    "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_optimizer_step", "ne_zero_grads",
+    "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4", "ne_decode",
+    "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
+    "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
+    "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
+    "ne_k_embed_bwd", "ne_k_swiglu_fwd",
+)
+
+
+class NEError(RuntimeError):
+    pass
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "hidden", "n_heads", "kv_heads", "head_dim",
+                                          "n_layers", "vocab", "seq", "batch", "qk_norm")] + \
+               [(n, C.c_float) for n in ("rope_theta", "res_alpha", "norm_eps")] + \
+               [(n, C.c_int32) for n in ("decode_batch", "decode_ctx")]
+
+
+class TrainState(C.Structure):
+    _fields_ = [("step", C.c_int32), ("total_steps", C.c_int32), ("lr", C.c_float),
+                ("loss", C.c_float), ("cum_compile", C.c_double), ("cum_train", C.c_double),
+                ("cum_wall", C.c_double), ("cum_steps", C.c_int32), ("cum_batches", C.c_int32),
+                ("adam_t", C.c_int32)]
+
+
+_lib = None
+
+P, I, F, D, L = C.c_void_p, C.c_int, C.c_float, C.c_double, C.c_int64
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise NEError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C neural-engine_amd)")
+    h = C.CDLL(LIB_PATH)
+    sig = {
+        "ne_create": (P, [C.POINTER(Config)]),
+        "ne_destroy": (None, [P]),
+        "ne_last_error": (C.c_char_p, []),
+        "ne_sync": (I, [P]),
+        "ne_num_tensors": (I, [P]),
+        "ne_tensor_numel": (L, [P, I]),
+        "ne_set_tensor": (I, [P, I, I, P, C.c_size_t]),
+        "ne_get_tensor": (I, [P, I, I, P, C.c_size_t]),
+        "ne_train_step": (I, [P, P, F, P]),
+        "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
+        "ne_zero_grads": (I, [P]),
+        "ne_get_state": (I, [P, C.POINTER(TrainState)]),
+        "ne_set_state": (I, [P, C.POINTER(TrainState)]),
+        "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
+        "ne_save_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
+        "ne_decode": (I, [P, P, I, I, I, F, F, P, P]),
+        "ne_prof_enable": (I, [P, I]),
+        "ne_prof_reset": (I, [P]),
+        "ne_prof_get": (I, [P, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
+        "ne_k_rmsnorm_fwd": (I, [P, P, P, P, I, I, F, P]),
+        "ne_k_rmsnorm_bwd": (I, [P, P, P, P, P, P, P, F, P, I, I, P]),
+        "ne_k_gemm": (I, [I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
+        "ne_k_qk_prep_fwd": (I, [P, L, P, P, P, P, P, P, P, P, I, I, I, I, I, F, P]),
+        "ne_k_qk_prep_bwd": (I, [P, P, P, L, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
+        "ne_k_attn_fwd": (I, [P, L, P, L, P, L, P, L, P, I, I, I, I, I, F, P]),
+        "ne_k_attn_bwd": (I, [P, L, P, L, P, L, P, L, P, P, L, P, P, L, P, L, P, L, I, I, I, I, I, F, P]),
+        "ne_k_ce_fwd": (I, [P, P, P, I, I, I, P, P, P, P, P, P]),
+        "ne_k_ce_bwd": (I, [P, P, P, P, I, I, I, F, P, P]),
+        "ne_k_adam": (I, [P, P, P, P, P, L, L, F, F, F, F, F, I, P, I, P]),
+        "ne_k_grad_norm": (I, [P, L, F, F, P, P, P, P]),
+        "ne_k_embed_fwd": (I, [P, P, P, I, I, P]),
+        "ne_k_embed_bwd": (I, [P, P, P, I, I, P]),
+        "ne_k_swiglu_fwd": (I, [P, P, I, I, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = h
+    return h
+
+
+def check(rc: int, what: str = ""):
+    if rc != 0:
+        msg = lib().ne_last_error().decode(errors="replace")
+        raise NEError(f"{what} failed ({rc}): {msg}")
+
+
+def tensor_names(n_layers: int, qk_norm: bool):
+    names = [f"layers.{l}.{t}" for l in range(n_layers) for t in LAYER_TENSORS]
+    names += ["rms_final", "embed"]
+    if qk_norm:
+        for l in range(n_layers):
+            names += [f"layers.{l}.q_norm", f"layers.{l}.k_norm"]
+    return names
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Model:
+    """One device-resident model + optimizer state + activation workspace (ne_ctx)."""
+
+    def __init__(self, dim, hidden, n_heads, kv_heads, head_dim, n_layers, vocab, seq, batch=1,
+                 qk_norm=False, rope_theta=10000.0, res_alpha=1.0, norm_eps=1e-5,
+                 decode_batch=0, decode_ctx=0):
+        self.cfg = Config(dim, hidden, n_heads, kv_heads, head_dim, n_layers, vocab, seq, batch,
+                          int(bool(qk_norm)), rope_theta, res_alpha, norm_eps, decode_batch, decode_ctx)
+        self._h = lib().ne_create(C.byref(self.cfg))
+        if not self._h:
+            raise NEError("ne_create failed: " + lib().ne_last_error().decode(errors="replace"))
+        self.names = tensor_names(n_layers, qk_norm)
+        self.ids = {n: i for i, n in enumerate(self.names)}
+        assert lib().ne_num_tensors(self._h) == len(self.names)
+
+    @classmethod
+    def from_oracle(cls, ocfg, batch=1, decode_batch=0, decode_ctx=0):
+        return cls(ocfg.dim, ocfg.hidden, ocfg.n_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.n_layers,
+                   ocfg.vocab, ocfg.seq, batch, ocfg.qk_norm, ocfg.rope_theta, ocfg.res_alpha,
+                   ocfg.eps, decode_batch, decode_ctx)
+
+    def close(self):
+        if self._h:
+            lib().ne_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def numel(self, name):
+        return int(lib().ne_tensor_numel(self._h, self.ids[name]))
+
+    def set(self, name, arr, kind=NE_PARAM):
+        a = np.ascontiguousarray(arr, np.float32).reshape(-1)
+        check(lib().ne_set_tensor(self._h, kind, self.ids[name], _ptr(a), a.size), f"set {name}")
+
+    def get(self, name, kind=NE_PARAM):
+        out = np.empty(self.numel(name), np.float32)
+        check(lib().ne_get_tensor(self._h, kind, self.ids[name], _ptr(out), out.size), f"get {name}")
+        return out
+
+    def set_params(self, P: dict, kind=NE_PARAM):
+        for n in self.names:
+            if n in P:
+                self.set(n, P[n], kind)
+
+    def get_all(self, shapes: dict, kind=NE_PARAM):
+        return {n: self.get(n, kind).reshape(shapes[n]) for n in self.names}
+
+    def train_step(self, tokens: np.ndarray, loss_scale=1.0, want_loss=True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        loss = C.c_float(0.0)
+        check(lib().ne_train_step(self._h, _ptr(t), loss_scale, C.byref(loss) if want_loss else None),
+              "train_step")
+        return float(loss.value) if want_loss else None
+
+    def optimizer_step(self, lr, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_scale=1.0, clip=1.0,
+                       want_norm=True):
+        gn = C.c_float(0.0)
+        check(lib().ne_optimizer_step(self._h, lr, b1, b2, eps, wd, grad_scale, clip,
+                                      C.byref(gn) if want_norm else None), "optimizer_step")
+        return float(gn.value) if want_norm else None
+
+    def zero_grads(self):
+        check(lib().ne_zero_grads(self._h), "zero_grads")
+
+    def sync(self):
+        check(lib().ne_sync(self._h), "sync")
+
+    def state(self):
+        st = TrainState()
+        check(lib().ne_get_state(self._h, C.byref(st)), "get_state")
+        return st
+
+    def set_state(self, st: TrainState):
+        check(lib().ne_set_state(self._h, C.byref(st)), "set_state")
+
+    def save(self, path, st: TrainState | None = None):
+        check(lib().ne_save_ckpt_v4(self._h, str(path).encode(), C.byref(st) if st else None), "save")
+
+    def load(self, path):
+        st = TrainState()
+        check(lib().ne_load_ckpt_v4(self._h, str(path).encode(), C.byref(st)), "load")
+        return st
+
+    def decode(self, prompt: np.ndarray, n_new: int, temperature=0.0, top_p=1.0, uniforms=None):
+        p = np.ascontiguousarray(prompt, np.int32)
+        B, P0 = p.shape
+        out = np.zeros((B, n_new), np.int32)
+        u = None
+        if uniforms is not None:
+            u = np.ascontiguousarray(uniforms, np.float64).reshape(B, n_new)
+        check(lib().ne_decode(self._h, _ptr(p), B, P0, n_new, temperature, top_p,
+                              _ptr(u) if u is not None else None, _ptr(out)), "decode")
+        return out
+
+    def prof_enable(self, on=True):
+        check(lib().ne_prof_enable(self._h, int(on)), "prof_enable")
+
+    def prof_reset(self):
+        check(lib().ne_prof_reset(self._h), "prof_reset")
+
+    def prof(self):
+        out = {}
+        for i, name in enumerate(PROF_FAMILIES):
+            ms, cnt = C.c_double(0), C.c_int64(0)
+            check(lib().ne_prof_get(self._h, i, C.byref(ms), C.byref(cnt)), "prof_get")
+            out[name] = (ms.value, cnt.value)
+        return out

@@ -1,0 +1,310 @@
+"""Kernel-level parity of the HIP kernels through the C-ABI (device pointers) against the
+numpy oracle (oracle/model.py) and float64 numpy restatements of the same op."""
+import math
+
+import numpy as np
+import pytest
+
+from gpu_util import bf16_round, call, dev, host, need_gpu, ptr, rel_l2, torch, zeros
+import ne
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+L = None
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    need_gpu()
+    global L
+    L = ne.lib()
+
+
+# ------------------------------------------------------------------------- GEMM
+
+def _operands(rng, M, N, K, layout):
+    A = bf16_round(rng.standard_normal((M, K)).astype(np.float32))   # logical [M,K]
+    B = bf16_round(rng.standard_normal((K, N)).astype(np.float32))   # logical [K,N]
+    a_store = A if layout in (0, 2) else A.T                          # bit0: A stored [K,M]
+    b_store = B.T if layout in (0, 1) else B                          # bit1: B stored [K,N]
+    lda = a_store.shape[1]
+    ldb = b_store.shape[1]
+    return A, B, dev(a_store, torch.bfloat16), lda, dev(b_store, torch.bfloat16), ldb
+
+
+@pytest.mark.parametrize("layout", [0, 2, 3, 1])
+@pytest.mark.parametrize("shape", [(64, 64, 64), (128, 192, 320), (256, 4096, 1024), (1024, 1024, 256)])
+def test_gemm_f32_layouts(layout, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K + layout)
+    A, B, a, lda, b, ldb = _operands(rng, M, N, K, layout)
+    c = zeros((M, N))
+    call(L.ne_k_gemm, layout, 1, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 0.5, None)
+    ref = 0.5 * (A.astype(np.float64) @ B.astype(np.float64))
+    err = np.abs(host(c) - ref).max() / np.abs(ref).max()
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("epi", [0, 2, 3])
+def test_gemm_epilogues(epi):
+    M, N, K = 256, 512, 256
+    rng = np.random.default_rng(epi)
+    A, B, a, lda, b, ldb = _operands(rng, M, N, K, 0)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    R = rng.standard_normal((M, N)).astype(np.float32)
+    if epi == 0:
+        c = zeros((M, N), torch.bfloat16)
+        call(L.ne_k_gemm, 0, 0, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 1.0, None)
+        assert rel_l2(host(c), ref) < 4e-3
+    elif epi == 2:
+        c = dev(R)
+        call(L.ne_k_gemm, 0, 2, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 2.0, None)
+        assert rel_l2(host(c), R + 2 * ref) < 1e-6
+    else:
+        c = zeros((M, N))
+        r = dev(R)
+        call(L.ne_k_gemm, 0, 3, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, ptr(r), N, 0.25, None)
+        assert rel_l2(host(c), R + 0.25 * ref) < 1e-6
+
+
+def test_gemm_swiglu_backward_epilogue():
+    T, D, H = 128, 256, 320
+    rng = np.random.default_rng(7)
+    dy = bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    W2 = bf16_round(rng.standard_normal((D, H)).astype(np.float32) * 0.05)
+    h13 = bf16_round(rng.standard_normal((T, 2 * H)).astype(np.float32))
+    dh = zeros((T, 2 * H), torch.bfloat16)
+    call(L.ne_k_gemm, 2, 4, T, H, D, ptr(dev(dy, torch.bfloat16)), D, ptr(dev(W2, torch.bfloat16)), H,
+         ptr(dh), 2 * H, ptr(dev(h13, torch.bfloat16)), 2 * H, 1.0, None)
+    dgate = dy.astype(np.float64) @ W2
+    h1, h3 = h13[:, :H].astype(np.float64), h13[:, H:].astype(np.float64)
+    sg = 1 / (1 + np.exp(-h1))
+    ref = np.concatenate([dgate * h3 * sg * (1 + h1 * (1 - sg)), dgate * h1 * sg], axis=1)
+    assert rel_l2(host(dh), ref) < 4e-3
+
+
+# --------------------------------------------------------------------- norms, embed
+
+@pytest.mark.parametrize("T,D", [(64, 128), (256, 768), (512, 1024)])
+def test_rmsnorm_fwd_bwd(T, D):
+    rng = np.random.default_rng(T)
+    x = rng.standard_normal((T, D)).astype(np.float32) * 3
+    g = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    res = rng.standard_normal((T, D)).astype(np.float32)
+    xd, gd = dev(x), dev(g)
+    y = zeros((T, D), torch.bfloat16)
+    r = zeros((T,))
+    call(L.ne_k_rmsnorm_fwd, ptr(xd), ptr(gd), ptr(y), ptr(r), T, D, 1e-5, None)
+    yr, rr = om.rmsnorm(x, g, 1e-5)
+    assert rel_l2(host(y), yr) < 4e-3
+    np.testing.assert_allclose(host(r), rr[:, 0], rtol=1e-6)
+    dx = zeros((T, D))
+    dxb = zeros((T, D), torch.bfloat16)
+    dg = dev(np.full(D, 0.5, np.float32))
+    call(L.ne_k_rmsnorm_bwd, ptr(dev(dy)), ptr(xd), ptr(gd), ptr(r), ptr(dev(res)), ptr(dx), ptr(dxb), 0.5,
+         ptr(dg), T, D, None)
+    dxr, dgr = om.rmsnorm_bwd(dy, x, g, rr)
+    assert rel_l2(host(dx), dxr + res) < 1e-5
+    assert rel_l2(host(dxb), 0.5 * (dxr + res)) < 4e-3
+    assert rel_l2(host(dg), dgr + 0.5) < 1e-5
+
+
+def test_embed_fwd_bwd_with_repeated_ids():
+    V, D, T = 512, 256, 192
+    rng = np.random.default_rng(3)
+    E = rng.standard_normal((V, D)).astype(np.float32)
+    tok = rng.integers(0, 16, T).astype(np.int32)      # many collisions
+    x = zeros((T, D))
+    call(L.ne_k_embed_fwd, ptr(dev(E)), ptr(dev(tok)), ptr(x), T, D, None)
+    np.testing.assert_array_equal(host(x), E[tok])
+    dx = rng.standard_normal((T, D)).astype(np.float32)
+    gE = zeros((V, D))
+    call(L.ne_k_embed_bwd, ptr(gE), ptr(dev(tok)), ptr(dev(dx)), T, D, None)
+    ref = np.zeros((V, D))
+    np.add.at(ref, tok, dx.astype(np.float64))
+    np.testing.assert_allclose(host(gE), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_swiglu_fwd():
+    T, H = 64, 192
+    rng = np.random.default_rng(4)
+    h13 = bf16_round(rng.standard_normal((T, 2 * H)).astype(np.float32) * 2)
+    gate = zeros((T, H), torch.bfloat16)
+    call(L.ne_k_swiglu_fwd, ptr(dev(h13, torch.bfloat16)), ptr(gate), T, H, None)
+    ref = om.silu(h13[:, :H]) * h13[:, H:]
+    assert rel_l2(host(gate), ref) < 4e-3
+
+
+# -------------------------------------------------------------------- RoPE / QK-norm
+
+@pytest.mark.parametrize("HD,qk", [(64, False), (128, True), (64, True)])
+def test_qk_prep_fwd_bwd(HD, qk):
+    B, S, NH, NKV = 2, 64, 4, 2
+    T, Q, KV = B * S, NH * HD, NKV * HD
+    QKV = Q + 2 * KV
+    theta = 1e6 if qk else 1e4
+    rng = np.random.default_rng(HD + qk)
+    qkv = bf16_round(rng.standard_normal((T, QKV)).astype(np.float32))
+    gq = (1 + 0.3 * rng.standard_normal(HD)).astype(np.float32)
+    gk = (1 + 0.3 * rng.standard_normal(HD)).astype(np.float32)
+    cos, sin = om.rope_tables(S, HD, theta)
+    cosd, sind = dev(cos.astype(np.float32)), dev(sin.astype(np.float32))
+    qkvd = dev(qkv, torch.bfloat16)
+    qr, kr = zeros((T, Q), torch.bfloat16), zeros((T, KV), torch.bfloat16)
+    rq, rk = zeros((T, NH)), zeros((T, NKV))
+    gqd, gkd = (dev(gq), dev(gk)) if qk else (None, None)
+    call(L.ne_k_qk_prep_fwd, ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd), ptr(gkd), ptr(qr), ptr(kr), ptr(rq),
+         ptr(rk), T, S, NH, NKV, HD, 1e-5, None)
+    q = qkv[:, :Q].reshape(B, S, NH, HD)
+    k = qkv[:, Q:Q + KV].reshape(B, S, NKV, HD)
+    if qk:
+        q, rqr = om.rmsnorm(q, gq, 1e-5)
+        k, rkr = om.rmsnorm(k, gk, 1e-5)
+        np.testing.assert_allclose(host(rq), rqr.reshape(T, NH), rtol=1e-5)
+    qe = om.rope_apply(q, cos, sin).reshape(T, Q)
+    ke = om.rope_apply(k, cos, sin).reshape(T, KV)
+    assert rel_l2(host(qr), qe) < 4e-3 and rel_l2(host(kr), ke) < 4e-3
+    # backward
+    dq = rng.standard_normal((T, Q)).astype(np.float32)
+    dk = rng.standard_normal((T, KV)).astype(np.float32)
+    dqkv = zeros((T, QKV), torch.bfloat16)
+    dgq, dgk = (zeros((HD,)), zeros((HD,))) if qk else (None, None)
+    call(L.ne_k_qk_prep_bwd, ptr(dev(dq)), ptr(dev(dk)), ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd), ptr(gkd),
+         ptr(rq), ptr(rk), ptr(dqkv), ptr(dgq), ptr(dgk), T, S, NH, NKV, HD, None)
+    dqn = om.rope_bwd(dq.reshape(B, S, NH, HD), cos, sin)
+    dkn = om.rope_bwd(dk.reshape(B, S, NKV, HD), cos, sin)
+    if qk:
+        dqn, dgqr = om.rmsnorm_bwd(dqn, qkv[:, :Q].reshape(B, S, NH, HD), gq, rqr)
+        dkn, dgkr = om.rmsnorm_bwd(dkn, qkv[:, Q:Q + KV].reshape(B, S, NKV, HD), gk, rkr)
+        assert rel_l2(host(dgq), dgqr) < 1e-4 and rel_l2(host(dgk), dgkr) < 1e-4
+    got = host(dqkv)
+    assert rel_l2(got[:, :Q], dqn.reshape(T, Q)) < 4e-3
+    assert rel_l2(got[:, Q:Q + KV], dkn.reshape(T, KV)) < 4e-3
+
+
+# ------------------------------------------------------------------------ attention
+
+def _attn_ref(q, k, v, do, NH, NKV, scale):
+    """float64 causal GQA attention fwd/bwd; q [B,S,NH,HD], k/v [B,S,NKV,HD]."""
+    B, S, _, HD = q.shape
+    r = NH // NKV
+    o = np.zeros_like(q, dtype=np.float64)
+    lse = np.zeros((B, S, NH))
+    dq = np.zeros_like(o)
+    dk = np.zeros((B, S, NKV, HD))
+    dv = np.zeros((B, S, NKV, HD))
+    mask = np.triu(np.ones((S, S), bool), 1)
+    for b in range(B):
+        for h in range(NH):
+            kh = h // r
+            s = scale * (q[b, :, h].astype(np.float64) @ k[b, :, kh].T.astype(np.float64))
+            s[mask] = -np.inf
+            m = s.max(1, keepdims=True)
+            e = np.exp(s - m)
+            l = e.sum(1, keepdims=True)
+            p = e / l
+            lse[b, :, h] = (m + np.log(l))[:, 0]
+            o[b, :, h] = p @ v[b, :, kh]
+            dp = do[b, :, h] @ v[b, :, kh].T
+            ds = p * (dp - (dp * p).sum(1, keepdims=True))
+            dq[b, :, h] = scale * ds @ k[b, :, kh]
+            dk[b, :, kh] += scale * ds.T @ q[b, :, h]
+            dv[b, :, kh] += p.T @ do[b, :, h]
+    return o, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("B,S,NH,NKV,HD", [(1, 64, 2, 2, 64), (2, 128, 4, 2, 64), (1, 256, 4, 2, 128),
+                                           (2, 192, 2, 1, 128)])
+def test_flash_attention_fwd_bwd(B, S, NH, NKV, HD):
+    T = B * S
+    rng = np.random.default_rng(S + HD)
+    # q/k/v as slices of wider rows (strided like the model's qkv buffer)
+    q = bf16_round(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    k = bf16_round(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    v = bf16_round(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    do = bf16_round(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    scale = 1.0 / math.sqrt(HD)
+    ld = NH * HD + 2 * NKV * HD
+    qkv = np.concatenate([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], axis=1)
+    qkvd = dev(qkv, torch.bfloat16)
+    qd = qkvd[:, :NH * HD]
+    kd = qkvd[:, NH * HD:NH * HD + NKV * HD]
+    vd = qkvd[:, NH * HD + NKV * HD:]
+    o = zeros((T, NH * HD), torch.bfloat16)
+    lse = zeros((T, NH))
+    call(L.ne_k_attn_fwd, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse), B, S, NH, NKV, HD,
+         scale, None)
+    o_r, lse_r, dq_r, dk_r, dv_r = _attn_ref(q, k, v, do, NH, NKV, scale)
+    assert rel_l2(host(o), o_r.reshape(T, -1)) < 8e-3
+    np.testing.assert_allclose(host(lse), lse_r.reshape(T, NH), rtol=1e-4, atol=1e-4)
+    delta = zeros((T, NH))
+    dq, dk = zeros((T, NH * HD)), zeros((T, NKV * HD))
+    dqkv = zeros((T, ld), torch.bfloat16)
+    dv = dqkv[:, NH * HD + NKV * HD:]
+    call(L.ne_k_attn_bwd, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse), ptr(dev(do, torch.bfloat16)),
+         NH * HD, ptr(delta), ptr(dq), NH * HD, ptr(dk), NKV * HD, ptr(dv), ld, B, S, NH, NKV, HD, scale, None)
+    assert rel_l2(host(dq), dq_r.reshape(T, -1)) < 2e-2
+    assert rel_l2(host(dk), dk_r.reshape(T, -1)) < 2e-2
+    assert rel_l2(host(dqkv)[:, NH * HD + NKV * HD:], dv_r.reshape(T, -1)) < 2e-2
+    # q and k columns of dqkv untouched
+    assert np.abs(host(dqkv)[:, :NH * HD + NKV * HD]).max() == 0
+
+
+# --------------------------------------------------------------- cross-entropy (LM head)
+
+@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000)])
+def test_fused_ce_fwd_bwd(T, D, V):
+    rng = np.random.default_rng(V)
+    x = bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    E = bf16_round(rng.standard_normal((V, D)).astype(np.float32) * 0.05)
+    tgt = rng.integers(0, V, T).astype(np.int32)
+    xd, Ed, td = dev(x, torch.bfloat16), dev(E, torch.bfloat16), dev(tgt)
+    part = zeros((T * (V // 64) * 2,))
+    tl, lse, rows, loss = zeros((T,)), zeros((T,)), zeros((T,)), zeros((4,))
+    call(L.ne_k_ce_fwd, ptr(xd), ptr(Ed), ptr(td), T, D, V, ptr(part), ptr(tl), ptr(lse), ptr(rows), ptr(loss), None)
+    logits = x.astype(np.float64) @ E.T.astype(np.float64)
+    m = logits.max(1, keepdims=True)
+    lse_r = (m + np.log(np.exp(logits - m).sum(1, keepdims=True)))[:, 0]
+    p_t = np.exp(logits[np.arange(T), tgt] - lse_r)
+    loss_r = np.mean(-np.log(p_t + 1e-10))
+    np.testing.assert_allclose(host(lse), lse_r, rtol=1e-5)
+    assert abs(host(loss)[0] - loss_r) < 1e-4 * abs(loss_r)
+    dl = zeros((T, V), torch.bfloat16)
+    call(L.ne_k_ce_bwd, ptr(xd), ptr(Ed), ptr(td), ptr(lse), T, D, V, 256.0 / T, ptr(dl), None)
+    ref = np.exp(logits - lse_r[:, None])
+    ref[np.arange(T), tgt] -= 1
+    ref *= 256.0 / T
+    assert rel_l2(host(dl), ref) < 4e-3
+
+
+# ------------------------------------------------------------------------ optimizer
+
+def test_adam_matches_oracle_and_grad_norm():
+    n, n_decay = 4096 * 3, 4096 * 2
+    rng = np.random.default_rng(11)
+    p = rng.standard_normal(n).astype(np.float32) * 0.02
+    g = rng.standard_normal(n).astype(np.float32) * 1e-2
+    m = rng.standard_normal(n).astype(np.float32) * 1e-3
+    v = np.abs(rng.standard_normal(n).astype(np.float32)) * 1e-5
+    pd, gd, md, vd = dev(p), dev(g), dev(m), dev(v)
+    pb = zeros((n,), torch.bfloat16)
+    part = zeros((1024,), torch.float64)
+    gs, gn = zeros((1,)), zeros((1,))
+    call(L.ne_k_grad_norm, ptr(gd), n, 0.5, 1.0, ptr(part), ptr(gs), ptr(gn), None)
+    norm = 0.5 * np.linalg.norm(g.astype(np.float64))
+    assert abs(host(gn)[0] - norm) < 1e-5 * norm
+    scale = 0.5 * min(1.0, 1.0 / norm)
+    assert abs(host(gs)[0] - scale) < 1e-6 * scale
+    t = 7
+    call(L.ne_k_adam, ptr(pd), ptr(gd), ptr(md), ptr(vd), ptr(pb), n, n_decay, 3e-4, 0.9, 0.95, 1e-8, 0.1, t,
+         ptr(gs), 1, None)
+    pr, mr, vr = p.copy(), m.copy(), v.copy()
+    ge = g * np.float32(host(gs)[0])
+    om.adam_update(pr[:n_decay], ge[:n_decay], mr[:n_decay], vr[:n_decay], t, 3e-4, 0.9, 0.95, 1e-8, 0.1)
+    om.adam_update(pr[n_decay:], ge[n_decay:], mr[n_decay:], vr[n_decay:], t, 3e-4, 0.9, 0.95, 1e-8, 0.0)
+    np.testing.assert_allclose(host(pd), pr, rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(host(md), mr, rtol=1e-5, atol=1e-12)
+    np.testing.assert_allclose(host(vd), vr, rtol=1e-5, atol=1e-14)
+    assert np.abs(host(gd)).max() == 0
+    np.testing.assert_allclose(host(pb), bf16_round(host(pd)), rtol=0, atol=0)

@@ -1,0 +1,175 @@
+"""Model-level parity through the C-ABI (ne_train_step / ne_optimizer_step / ne_decode /
+checkpoints) against the numpy oracle, at small shapes the oracle runs in seconds."""
+import numpy as np
+import pytest
+
+from gpu_util import need_gpu, rel_l2
+import ne
+from oracle import ckpt, model as om
+
+pytestmark = pytest.mark.gpu
+
+# Tolerances of the step (fp32 master weights, bf16 activations/operands, fp32 accumulation)
+LOSS_RTOL = 1e-3
+GRAD_RL2 = 1e-2
+ADAM_RTOL = 1e-5
+
+CASES = {
+    "ref": dict(qk_norm=False, rope_theta=1e4, res_alpha=1.0),
+    "train_alpha": dict(qk_norm=False, rope_theta=1e4, res_alpha=om.train_alpha(2)),
+    "qwen3": dict(qk_norm=True, rope_theta=1e6, res_alpha=1.0),
+}
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    need_gpu()
+
+
+def shapes(cfg):
+    return dict(om.tensor_list(cfg))
+
+
+def run_step(cfg, P, tok, loss_scale=256.0):
+    m = ne.Model.from_oracle(cfg, batch=tok.shape[0])
+    m.set_params(P)
+    loss = m.train_step(tok, loss_scale)
+    G = m.get_all(shapes(cfg), ne.NE_GRAD)
+    return m, loss, G
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_train_step_matches_oracle(case):
+    cfg = om.tiny(**CASES[case])
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = om.tokens_for_step(cfg, 2, cfg.seq, seed=1)
+    print(f"\n[case {case}] tiny model B=2 S={cfg.seq}", flush=True)
+    m, loss, G = run_step(cfg, P, tok)
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    Go = om.backward(cfg, P, cache)
+    assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
+    worst = max((rel_l2(G[n], Go[n]), n) for n in P)
+    print(f"  loss gpu={loss:.6f} oracle={lo:.6f}; worst grad rel-L2 {worst[0]:.2e} ({worst[1]})")
+    for n in P:
+        assert rel_l2(G[n], Go[n]) <= GRAD_RL2, (n, rel_l2(G[n], Go[n]))
+    m.close()
+
+
+def test_grads_accumulate_and_zero():
+    cfg = om.tiny()
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = om.tokens_for_step(cfg, 1, cfg.seq, seed=2)
+    m = ne.Model.from_oracle(cfg, batch=1)
+    m.set_params(P)
+    m.train_step(tok, 1.0)
+    g1 = m.get("layers.1.W2", ne.NE_GRAD)
+    m.train_step(tok, 1.0)
+    g2 = m.get("layers.1.W2", ne.NE_GRAD)
+    assert rel_l2(g2, 2 * g1) < 1e-5
+    m.zero_grads()
+    assert np.abs(m.get("layers.1.W2", ne.NE_GRAD)).max() == 0
+    m.close()
+
+
+@pytest.mark.parametrize("clip", [1.0, 1e-3])
+def test_optimizer_step_matches_oracle(clip):
+    """Same grads in -> AdamW out within 1e-5 (isolates the update from bf16 gradients)."""
+    cfg = om.tiny(qk_norm=True)
+    rng = np.random.default_rng(5)
+    P = om.init_params(cfg, seed=3, std=0.02)
+    G = {k: (rng.standard_normal(v.shape) * 1e-2 * 256).astype(np.float32) for k, v in P.items()}
+    M = {k: (rng.standard_normal(v.shape) * 1e-3).astype(np.float32) for k, v in P.items()}
+    V = {k: (np.abs(rng.standard_normal(v.shape)) * 1e-5).astype(np.float32) for k, v in P.items()}
+    m = ne.Model.from_oracle(cfg)
+    m.set_params(P)
+    m.set_params(G, ne.NE_GRAD)
+    m.set_params(M, ne.NE_ADAM_M)
+    m.set_params(V, ne.NE_ADAM_V)
+    st = m.state()
+    st.adam_t = 4
+    m.set_state(st)
+    gn = m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=clip)
+    Po = {k: v.copy() for k, v in P.items()}
+    Go = {k: v.copy() for k, v in G.items()}
+    gno = om.optimizer_step(Po, Go, M, V, 5, 3e-4, grad_scale=1 / 256, clip=clip)
+    assert abs(gn - gno) < 1e-5 * gno
+    sh = shapes(cfg)
+    Pg = m.get_all(sh)
+    for n in P:
+        np.testing.assert_allclose(Pg[n], Po[n], rtol=ADAM_RTOL, atol=1e-10, err_msg=n)
+    Mg = m.get_all(sh, ne.NE_ADAM_M)
+    for n in P:
+        np.testing.assert_allclose(Mg[n], M[n], rtol=ADAM_RTOL, atol=1e-12, err_msg=n)
+    assert max(np.abs(m.get(n, ne.NE_GRAD)).max() for n in P) == 0
+    assert m.state().adam_t == 5
+    m.close()
+
+
+def _bf16_params(cfg, seed=0, std=0.02):
+    return {k: om.round_bf16(v) for k, v in om.init_params(cfg, seed=seed, std=std).items()}
+
+
+@pytest.mark.parametrize("case", ["ref", "qwen3"])
+def test_decode_greedy_matches_oracle(case):
+    cfg = om.tiny(**CASES[case], vocab=1024)
+    P = _bf16_params(cfg, std=0.05)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, (3, 8)).astype(np.int32)
+    m = ne.Model.from_oracle(cfg, decode_batch=3, decode_ctx=64)
+    m.set_params(P)
+    got = m.decode(prompt, 24)
+    want, margins, _ = om.decode(cfg, P, prompt, 24, return_logits=True)
+    print(f"\n  min top-2 margin {margins.min():.3e}")
+    np.testing.assert_array_equal(got, want)
+    m.close()
+
+
+def test_decode_sampling_matches_oracle():
+    cfg = om.tiny(**CASES["qwen3"], vocab=1024)
+    P = _bf16_params(cfg, std=0.3)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, (2, 5)).astype(np.int32)
+    u = np.random.RandomState(3).random_sample((2, 16))
+    m = ne.Model.from_oracle(cfg, decode_batch=2, decode_ctx=32)
+    m.set_params(P)
+    for temp, top_p in ((0.6, 1.0), (0.8, 0.9)):
+        got = m.decode(prompt, 16, temperature=temp, top_p=top_p, uniforms=u)
+        want = om.decode(cfg, P, prompt, 16, temperature=temp, top_p=top_p, uniforms=u)
+        np.testing.assert_array_equal(got, want, err_msg=f"temp={temp} top_p={top_p}")
+    m.close()
+
+
+def test_checkpoint_roundtrip_with_oracle_reader(tmp_path):
+    cfg = om.tiny(qk_norm=True, n_layers=1)
+    P = om.init_params(cfg, seed=4, std=0.02)
+    rng = np.random.default_rng(0)
+    M = {k: rng.standard_normal(v.shape).astype(np.float32) for k, v in P.items()}
+    V = {k: rng.standard_normal(v.shape).astype(np.float32) for k, v in P.items()}
+    m = ne.Model.from_oracle(cfg)
+    m.set_params(P)
+    m.set_params(M, ne.NE_ADAM_M)
+    m.set_params(V, ne.NE_ADAM_V)
+    st = ne.TrainState(step=100, total_steps=1000, lr=2e-4, loss=5.5, adam_t=10, cum_steps=100)
+    path = tmp_path / "c.bin"
+    m.save(path, st)
+    assert path.stat().st_size == ckpt.expected_size(cfg)
+    h, P2, M2, V2 = ckpt.read(path)
+    assert h["step"] == 100 and h["adam_t"] == 10 and abs(h["loss"] - 5.5) < 1e-6
+    for n in P:
+        np.testing.assert_array_equal(P2[n], P[n])
+        np.testing.assert_array_equal(M2[n], M[n])
+        np.testing.assert_array_equal(V2[n], V[n])
+    # oracle-written file loads back into a fresh context
+    path2 = tmp_path / "d.bin"
+    ckpt.write(path2, cfg, P2, V2, M2, step=3, adam_t=2)
+    m2 = ne.Model.from_oracle(cfg)
+    st2 = m2.load(path2)
+    assert st2.step == 3 and st2.adam_t == 2
+    for n in P:
+        np.testing.assert_array_equal(m2.get(n).reshape(P[n].shape), P[n])
+        np.testing.assert_array_equal(m2.get(n, ne.NE_ADAM_M).reshape(P[n].shape), V[n])
+    # truncated file is rejected with a size error
+    raw = path2.read_bytes()
+    (tmp_path / "t.bin").write_bytes(raw[:-4])
+    with pytest.raises(ne.NEError, match="size"):
+        m2.load(tmp_path / "t.bin")
+    m.close()
+    m2.close()

@@ -1,0 +1,56 @@
+"""CPU-side checks of the C-ABI library: it loads, exports every symbol ne.h declares,
+rejects bad configurations without a GPU, and the tensor naming matches the oracle."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import ne
+from oracle import model as om
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    src = open(os.path.join(ROOT, "include", "ne.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(ne_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_symbols_listed_in_binding():
+    assert header_symbols() == sorted(ne.EXPORTS)
+
+
+def test_library_exports_every_header_symbol():
+    h = ctypes.CDLL(ne.LIB_PATH)
+    for name in header_symbols():
+        assert hasattr(h, name), name
+    ne.lib()  # signatures bind
+
+
+def test_invalid_config_rejected_without_device():
+    cfg = ne.Config(dim=100, hidden=256, n_heads=4, kv_heads=2, head_dim=64, n_layers=1, vocab=512,
+                    seq=64, batch=1, qk_norm=0, rope_theta=1e4, res_alpha=1.0, norm_eps=1e-5,
+                    decode_batch=0, decode_ctx=0)
+    assert not ne.lib().ne_create(ctypes.byref(cfg))
+    assert b"multiples of 64" in ne.lib().ne_last_error()
+    cfg.dim, cfg.head_dim = 128, 96
+    assert not ne.lib().ne_create(ctypes.byref(cfg))
+    assert b"head_dim" in ne.lib().ne_last_error()
+
+
+def test_kernel_entry_points_validate_shapes_before_launch():
+    # a GEMM with M not a multiple of 64 must be refused on the host
+    rc = ne.lib().ne_k_gemm(0, 0, 65, 64, 64, None, 64, None, 64, None, 64, None, 0, 1.0, None)
+    assert rc == -1 and b"multiples of 64" in ne.lib().ne_last_error()
+    rc = ne.lib().ne_k_attn_fwd(None, 64, None, 64, None, 64, None, 64, None, 1, 100, 4, 2, 64, 0.125, None)
+    assert rc == -1 and b"multiple of 64" in ne.lib().ne_last_error()
+    rc = ne.lib().ne_k_adam(None, None, None, None, None, 8, 8, 1e-3, 0.9, 0.95, 1e-8, 0.1, 0, None, 1, None)
+    assert rc == -1
+
+
+@pytest.mark.parametrize("qk", [False, True])
+def test_tensor_names_match_oracle_order(qk):
+    cfg = om.tiny(qk_norm=qk)
+    assert ne.tensor_names(cfg.n_layers, qk) == [n for n, _ in om.tensor_list(cfg)]
