@@ -45,7 +45,13 @@ typedef struct ne_config {
   float norm_eps;       /* 1e-5 */
   int32_t decode_batch; /* max sequences of ne_decode (0: no decode buffers) */
   int32_t decode_ctx;   /* max prompt + generated tokens of ne_decode */
+  int32_t dtype;        /* 16-bit format of activations and the weight shadow: NE_FP16 or NE_BF16 */
 } ne_config;
+
+/* 16-bit formats.  NE_FP16 (IEEE half: 10-bit mantissa, the reference's own ANE format) is
+ * the training default; its backward runs at an internal power-of-two gradient scale with
+ * overflow detection (see ne_optimizer_step).  NE_BF16 trades precision for range. */
+enum { NE_BF16 = 0, NE_FP16 = 1 };
 
 /* Counters of the v4 checkpoint header (TD/config.h:82-91 CkptHdr). */
 typedef struct ne_train_state {
@@ -60,7 +66,7 @@ enum { NE_PARAM = 0, NE_GRAD = 1, NE_ADAM_M = 2, NE_ADAM_V = 3 };
 
 /* ---------------------------------------------------------------- context ---- */
 
-/* Allocate device-resident fp32 master weights, grads, Adam m/v, the bf16 weight shadow and
+/* Allocate device-resident fp32 master weights, grads, Adam m/v, the 16-bit weight shadow and
  * all activation/workspace buffers.  Replaces ane_init (TD/config.h:99-107), the per-layer
  * host allocations (TD/config.h:110-176, TD/train.m:199-210), kernel compilation
  * (TD/train.m:25-94, TD/io.h:135-171) and IOSurface/request setup (TD/train.m:304-329).
@@ -80,7 +86,7 @@ int ne_sync(ne_ctx *ctx);
 int ne_num_tensors(const ne_ctx *ctx);
 int64_t ne_tensor_numel(const ne_ctx *ctx, int tensor_id);
 /* Copy fp32 host data in/out of one tensor (row-major, reference layout).  Setting a
- * parameter also refreshes its bf16 shadow.  Replaces the per-layer stage_* / transpose
+ * parameter also refreshes its 16-bit shadow.  Replaces the per-layer stage_* / transpose
  * restaging of TD/io.h:263-409 and TD/train.m:261-274 (weights never leave the device
  * during training). */
 int ne_set_tensor(ne_ctx *ctx, int kind, int tensor_id, const float *host, size_t n);
@@ -99,13 +105,19 @@ int ne_train_step(ne_ctx *ctx, const int32_t *tokens, float loss_scale, float *l
 
 /* Scale grads by grad_scale, global L2 norm, clip to `clip` (if > 0), AdamW with
  * bias-corrected moments (t = ++adam_t), weight decay wd on matrices and the embedding
- * (0 on the RMSNorm / QK-norm gains), refresh the bf16 shadow, zero the grads.  gnorm_out
- * (may be NULL; non-NULL synchronises) receives the pre-clip norm.  Replaces
- * TD/train.m:782-903 and adam_update (TD/cpu_ops.h:266-303). */
+ * (0 on the RMSNorm / QK-norm gains), refresh the 16-bit shadow, zero the grads.  gnorm_out
+ * (may be NULL) receives the pre-clip norm.  If any 16-bit value of the accumulated
+ * micro-steps overflowed, the update is skipped (weights, moments and adam_t unchanged,
+ * grads zeroed), the internal gradient scale is halved and 1 is returned; otherwise 0.
+ * Synchronises.  Replaces TD/train.m:782-903 and adam_update (TD/cpu_ops.h:266-303). */
 int ne_optimizer_step(ne_ctx *ctx, float lr, float b1, float b2, float eps, float wd,
                       float grad_scale, float clip, float *gnorm_out);
 /* Zero all gradients.  Replaces layer_grads_zero (TD/config.h:164-170). */
 int ne_zero_grads(ne_ctx *ctx);
+/* Internal gradient scale of the 16-bit backward and the number of skipped (overflowed)
+ * optimizer steps.  No reference counterpart (the ANE path had a fixed loss scale 256,
+ * TD/train.m:180). */
+int ne_grad_scale_info(const ne_ctx *ctx, float *scale, int32_t *skipped_steps);
 int ne_get_state(const ne_ctx *ctx, ne_train_state *st);
 int ne_set_state(ne_ctx *ctx, const ne_train_state *st);
 
@@ -126,7 +138,7 @@ int ne_save_ckpt_v4(ne_ctx *ctx, const char *path, const ne_train_state *st);
  * temperature < 1e-6 selects greedy argmax; otherwise softmax(logits/temperature), an
  * optional top-p mask (top_p < 1) and inverse-CDF sampling in vocabulary order with
  * uniforms[b*n_new + j] in [0,1) (the draw of numpy's RandomState.choice, generate.py:215).
- * Uses the bf16 weight shadow with fp32 activations and an fp32 KV cache.  Requires
+ * Uses the 16-bit weight shadow with fp32 activations and an fp32 KV cache.  Requires
  * B <= decode_batch and P + n_new <= decode_ctx. */
 int ne_decode(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temperature,
               float top_p, const double *uniforms, int32_t *out_tokens);
@@ -144,76 +156,80 @@ int ne_prof_reset(ne_ctx *ctx);
 int ne_prof_get(ne_ctx *ctx, int family, double *ms, int64_t *count);
 
 /* ------------------------------------------------------ kernel-level entry points ---- */
-/* Device-pointer entry points of the individual kernels (bf16 = uint16 bit patterns),
- * for testing and for callers composing their own step.  stream: a hipStream_t or NULL.
- * They launch asynchronously and return the launch status. */
+/* Device-pointer entry points of the individual kernels, for testing and for callers
+ * composing their own step.  16-bit buffers hold NE_FP16 or NE_BF16 bit patterns as
+ * selected by dtype.  stream: a hipStream_t or NULL.  They launch asynchronously and return
+ * the launch status. */
 
-/* y[T,D] bf16 = x*r*g, r[T] = (mean(x^2)+eps)^-1/2.  TD/cpu_ops.h:20-60 rmsnorm. */
-int ne_k_rmsnorm_fwd(const float *x, const float *g, void *y, float *r, int T, int D, float eps,
-                     void *stream);
-/* Exact RMSNorm backward + residual (may be NULL) + gain-grad accumulation into dg; dxb
- * (may be NULL) receives bf16(bscale*dx).  TD/cpu_ops.h:108-261 rmsnorm_bwd(_add). */
-int ne_k_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
-                     const float *resid, float *dx, void *dxb, float bscale, float *dg, int T,
-                     int D, void *stream);
-/* C = epi(alpha * A.B) on bf16 MFMA.  layout 0: A[M,K] B[N,K] (forward, weights [out,in]);
- * 2: A[M,K] B[K,N] (input gradient); 3: A[K,M] B[K,N] (weight gradient).  epi 0: C bf16,
+/* y[T,D] 16-bit = x*r*g, r[T] = (mean(x^2)+eps)^-1/2.  TD/cpu_ops.h:20-60 rmsnorm. */
+int ne_k_rmsnorm_fwd(int dtype, const float *x, const float *g, void *y, float *r, int T, int D,
+                     float eps, void *stream);
+/* Exact RMSNorm backward + residual (may be NULL); dg += dg_scale * sum_t dy*x*r; dxb (may
+ * be NULL) receives 16-bit(bscale*dx).  TD/cpu_ops.h:108-261 rmsnorm_bwd(_add). */
+int ne_k_rmsnorm_bwd(int dtype, const float *dy, const float *x, const float *g, const float *r,
+                     const float *resid, float *dx, void *dxb, float bscale, float *dg,
+                     float dg_scale, int T, int D, void *stream);
+/* C = epi(alpha * A.B) on 16-bit MFMA.  layout 0: A[M,K] B[N,K] (forward, weights [out,in]);
+ * 2: A[M,K] B[K,N] (input gradient); 3: A[K,M] B[K,N] (weight gradient).  epi 0: C 16-bit,
  * 1: C fp32, 2: C fp32 +=, 3: C fp32 = R fp32 + result, 4: SwiGLU backward (result =
- * dgate, R = h13 bf16 [M,2N], C = dh13 bf16 [M,2N]).  M, N, K multiples of 64.
+ * dgate, R = h13 16-bit [M,2N], C = dh13 16-bit [M,2N]).  M, N, K multiples of 64.
  * Replaces the matmuls of TD/mil_dynamic.h:14-35, 57-234, 238-306, 320-576 and the
  * cblas_sgemm calls of TD/train.m:500-524, 554-738. */
-int ne_k_gemm(int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
+int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
               const void *B, int64_t ldb, void *C, int64_t ldc, const void *R, int64_t ldr,
               float alpha, void *stream);
 /* Per-head QK-RMSNorm (gq/gk NULL: off) + interleaved RoPE of the q and k column blocks of
- * qkv [T, ld] bf16 at positions t % S with fp32 tables cos/sin [S, HD/2]; writes qr, kr
- * bf16 and the norm factors rq [T,NH], rk [T,NKV].  TD/mil_dynamic.h:133-169. */
-int ne_k_qk_prep_fwd(const void *qkv, int64_t ld, const float *cosb, const float *sinb,
-                     const float *gq, const float *gk, void *qr, void *kr, float *rq, float *rk,
-                     int T, int S, int NH, int NKV, int HD, float eps, void *stream);
+ * qkv [T, ld] at positions t % S with fp32 tables cos/sin [S, HD/2]; writes qr, kr and the
+ * norm factors rq [T,NH], rk [T,NKV].  TD/mil_dynamic.h:133-169. */
+int ne_k_qk_prep_fwd(int dtype, const void *qkv, int64_t ld, const float *cosb,
+                     const float *sinb, const float *gq, const float *gk, void *qr, void *kr,
+                     float *rq, float *rk, int T, int S, int NH, int NKV, int HD, float eps,
+                     void *stream);
 /* Backward of ne_k_qk_prep_fwd: dq [T,NH*HD], dk [T,NKV*HD] fp32 -> q/k column blocks of
- * dqkv bf16; gain grads accumulate into dgq/dgk.  TD/cpu_ops.h:510-537. */
-int ne_k_qk_prep_bwd(const float *dq, const float *dk, const void *qkv, int64_t ld,
+ * dqkv; gain grads (times dg_scale) accumulate into dgq/dgk.  TD/cpu_ops.h:510-537. */
+int ne_k_qk_prep_bwd(int dtype, const float *dq, const float *dk, const void *qkv, int64_t ld,
                      const float *cosb, const float *sinb, const float *gq, const float *gk,
                      const float *rq, const float *rk, void *dqkv, float *dgq, float *dgk,
-                     int T, int S, int NH, int NKV, int HD, void *stream);
-/* Causal GQA flash attention forward: o [T,NH*HD] bf16 and lse [T,NH] fp32 (natural log of
- * the row sum of exp(scale*q.k)).  Rows are t = b*S + s.  TD/mil_dynamic.h:171-223. */
-int ne_k_attn_fwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
-                  int64_t ldv, void *o, int64_t ldo, float *lse, int B, int S, int NH, int NKV,
-                  int HD, float scale, void *stream);
-/* Backward: dq [T,NH*HD] fp32, dk [T,NKV*HD] fp32, dv bf16 (GQA-reduced); delta [T,NH] is
+                     float dg_scale, int T, int S, int NH, int NKV, int HD, void *stream);
+/* Causal GQA flash attention forward: o [T,NH*HD] and lse [T,NH] fp32 (natural log of the
+ * row sum of exp(scale*q.k)).  Rows are t = b*S + s.  TD/mil_dynamic.h:171-223. */
+int ne_k_attn_fwd(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
+                  const void *v, int64_t ldv, void *o, int64_t ldo, float *lse, int B, int S,
+                  int NH, int NKV, int HD, float scale, void *stream);
+/* Backward: dq [T,NH*HD] fp32, dk [T,NKV*HD] fp32, dv 16-bit (GQA-reduced); delta [T,NH] is
  * scratch.  TD/mil_dynamic.h:583-707, TD/cpu_ops.h:585-605. */
-int ne_k_attn_bwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
-                  int64_t ldv, const void *o, int64_t ldo, const float *lse, const void *dout,
-                  int64_t lddo, float *delta, float *dq, int64_t lddq, float *dk, int64_t lddk,
-                  void *dv, int64_t lddv, int B, int S, int NH, int NKV, int HD, float scale,
-                  void *stream);
+int ne_k_attn_bwd(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
+                  const void *v, int64_t ldv, const void *o, int64_t ldo, const float *lse,
+                  const void *dout, int64_t lddo, float *delta, float *dq, int64_t lddq,
+                  float *dk, int64_t lddk, void *dv, int64_t lddv, int B, int S, int NH, int NKV,
+                  int HD, float scale, void *stream);
 /* Fused LM-head + softmax cross-entropy (TD/train.m:493-524, TD/cpu_ops.h:348-382):
  * logits = x[T,D] . E[V,D]^T are produced tile by tile and never stored.  Forward writes
  * lse[T] and loss[0] = mean(-log(p_tgt + 1e-10)); part is scratch [T, V/64*2] floats
  * and tgt_logit/loss_rows scratch [T]. */
-int ne_k_ce_fwd(const void *x, const void *E, const int32_t *targets, int T, int D, int V,
-                float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D,
+                int V, float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                 void *stream);
-/* Backward: dlogits bf16 [T,V] = (softmax - onehot) * scale, recomputing the logits. */
-int ne_k_ce_bwd(const void *x, const void *E, const int32_t *targets, const float *lse, int T,
-                int D, int V, float scale, void *dlogits, void *stream);
+/* Backward: dlogits 16-bit [T,V] = (softmax - onehot) * scale, recomputing the logits. */
+int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_t *targets,
+                const float *lse, int T, int D, int V, float scale, void *dlogits, void *stream);
 /* In-place AdamW over n fp32 elements; elements [0, n_decay) get weight decay.  The grad is
- * multiplied by *gscale (device scalar).  pb (may be NULL) receives the bf16 weights; the
+ * multiplied by *gscale (device scalar).  pb (may be NULL) receives the 16-bit weights; the
  * grad is zeroed when zero_grad.  TD/cpu_ops.h:266-303. */
-int ne_k_adam(float *p, float *g, float *m, float *v, void *pb, int64_t n, int64_t n_decay,
-              float lr, float b1, float b2, float eps, float wd, int t, const float *gscale,
-              int zero_grad, void *stream);
+int ne_k_adam(int dtype, float *p, float *g, float *m, float *v, void *pb, int64_t n,
+              int64_t n_decay, float lr, float b1, float b2, float eps, float wd, int t,
+              const float *gscale, int zero_grad, void *stream);
 /* Global grad norm and clip factor: gscale[0] = grad_scale * min(1, clip/norm),
  * gnorm[0] = grad_scale * ||g||.  partials: scratch of 1024 doubles.  TD/train.m:785-849. */
 int ne_k_grad_norm(const float *g, int64_t n, float grad_scale, float clip, double *partials,
                    float *gscale, float *gnorm, void *stream);
-/* x[T,D] fp32 = E[tok[t]] (TD/cpu_ops.h:433-439); gE[tok[t]] += dx[t] (TD/cpu_ops.h:441-447). */
+/* x[T,D] fp32 = E[tok[t]] (TD/cpu_ops.h:433-439); gE[tok[t]] += scale*dx[t]
+ * (TD/cpu_ops.h:441-447). */
 int ne_k_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, void *stream);
-int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, void *stream);
-/* gate[T,H] bf16 = silu(h1)*h3 with h13 = [h1 | h3] rows [T,2H] (TD/mil_dynamic.h:276-281). */
-int ne_k_swiglu_fwd(const void *h13, void *gate, int T, int H, void *stream);
+int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D,
+                   void *stream);
+/* gate[T,H] = silu(h1)*h3 with h13 = [h1 | h3] rows [T,2H] (TD/mil_dynamic.h:276-281). */
+int ne_k_swiglu_fwd(int dtype, const void *h13, void *gate, int T, int H, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,30 +1,71 @@
-// Shared device helpers for the gfx950 kernels: bf16 storage, MFMA operand vectors,
-// 64-lane wavefront reductions.  Activations/weights are stored as raw uint16 bf16 bit
-// patterns and bit-cast to __bf16 vectors only at the MFMA boundary.
+// Shared device helpers for the gfx950 kernels: 16-bit storage types, MFMA operand
+// vectors, 64-lane wavefront reductions.
+//
+// Activations and the weight shadow are 16-bit, stored as raw uint16 bit patterns and
+// bit-cast to the MFMA operand vectors at the instruction boundary.  The 16-bit format is
+// a per-context choice: IEEE fp16 (default for training: 10-bit mantissa, 8x finer than
+// bf16, same MFMA rate on gfx950; gradients carry a power-of-two scale to stay in range)
+// or bf16.  Kernels are templated on a format tag (H16F / H16B).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-typedef uint16_t bf16_t;
+typedef uint16_t h16_t;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define NE_WAVE 64
 
-__device__ __forceinline__ float bf2f(bf16_t h) {
-  return __uint_as_float(((uint32_t)h) << 16);
-}
+// bf16 format tag
+struct H16B {
+  static constexpr int id = 0;
+  typedef bf16x8 v8;
+  __device__ static __forceinline__ float f(h16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+  // round to nearest even (finite inputs)
+  __device__ static __forceinline__ h16_t h(float x) {
+    uint32_t u = __float_as_uint(x);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (h16_t)(u >> 16);
+  }
+  __device__ static __forceinline__ bool bad(h16_t v) { return (v & 0x7F80u) == 0x7F80u; }
+  __device__ static __forceinline__ v8 op(const u16x8 &v) { return __builtin_bit_cast(v8, v); }
+  __device__ static __forceinline__ f32x16 mfma32(const v8 &a, const v8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ f32x4 mfma16(const v8 &a, const v8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
 
-// fp32 -> bf16, round to nearest even (finite inputs).
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+// IEEE fp16 format tag
+struct H16F {
+  static constexpr int id = 1;
+  typedef f16x8 v8;
+  __device__ static __forceinline__ float f(h16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+  __device__ static __forceinline__ h16_t h(float x) { return __builtin_bit_cast(h16_t, (_Float16)x); }
+  // inf or nan after conversion (|x| beyond the fp16 range)
+  __device__ static __forceinline__ bool bad(h16_t v) { return (v & 0x7C00u) == 0x7C00u; }
+  __device__ static __forceinline__ v8 op(const u16x8 &v) { return __builtin_bit_cast(v8, v); }
+  __device__ static __forceinline__ f32x16 mfma32(const v8 &a, const v8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ f32x4 mfma16(const v8 &a, const v8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Dispatch a templated launcher on the runtime format id: DISPATCH_H16(dt, fn<HT>(args)).
+#define DISPATCH_H16(dt, ...)            \
+  ((dt) == 1 ? [&] { using HT = H16F; return __VA_ARGS__; }() \
+             : [&] { using HT = H16B; return __VA_ARGS__; }())
+
+// Raise a device overflow flag (non-finite 16-bit result) once per thread.
+__device__ __forceinline__ void flag_overflow(int *ovf, bool bad) {
+  if (ovf && bad) *ovf = 1;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -45,7 +86,7 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
-// Reduction over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
+// Reductions over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
 __device__ __forceinline__ float quad16_sum(float v) {
   v += __shfl_xor(v, 16, 64);
   v += __shfl_xor(v, 32, 64);
@@ -55,18 +96,4 @@ __device__ __forceinline__ float quad16_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, 64));
   v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
-}
-
-__device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x16 mfma32(const bf16x8 &a, const bf16x8 &b, const f32x16 &c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(const u16x8 &v) {
-  return __builtin_bit_cast(bf16x8, v);
-}
-__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 &v) {
-  return __builtin_bit_cast(bf16x8, v);
 }

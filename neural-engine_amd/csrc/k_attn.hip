@@ -1,4 +1,4 @@
-// Causal flash attention forward / backward on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
+// Causal flash attention forward / backward on 16-bit MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
 //
 // Replaces the score/softmax/PV part of gen_sdpa_fwd_dynamic (TD/mil_dynamic.h:171-223,
 // full S x S scores plus a -65504 mask blob, TD/mil_dynamic.h:716-725) and the two
@@ -22,33 +22,36 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr int BLK = 64;  // queries per q tile and keys per kv tile
 
-__device__ __forceinline__ bf16x8 ld8(const bf16_t *p) { return as_bf16x8(*(const u16x8 *)p); }
+template <typename HT>
+__device__ __forceinline__ typename HT::v8 ld8(const h16_t *p) { return HT::op(*(const u16x8 *)p); }
 
 // 8 K-values from a transposed LDS tile: columns c0..c0+3 and c1..c1+3 of one row.
-__device__ __forceinline__ bf16x8 ld_pair4(const bf16_t *row, int c0, int c1) {
+template <typename HT>
+__device__ __forceinline__ typename HT::v8 ld_pair4(const h16_t *row, int c0, int c1) {
   const u16x4 x = *(const u16x4 *)(row + c0);
   const u16x4 y = *(const u16x4 *)(row + c1);
   u16x8 r;
   r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3];
   r[4] = y[0]; r[5] = y[1]; r[6] = y[2]; r[7] = y[3];
-  return as_bf16x8(r);
+  return HT::op(r);
 }
 
-__device__ __forceinline__ bf16x8 pack_acc(const f32x4 &x, const f32x4 &y) {
+template <typename HT>
+__device__ __forceinline__ typename HT::v8 pack_acc(const f32x4 &x, const f32x4 &y) {
   u16x8 r;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    r[i] = f2bf(x[i]);
-    r[4 + i] = f2bf(y[i]);
+    r[i] = HT::h(x[i]);
+    r[4 + i] = HT::h(y[i]);
   }
-  return as_bf16x8(r);
+  return HT::op(r);
 }
 
 // Stage a 64-row x HD tile of rows t0.. (column offset col) into LDS row-major
 // (pitch RP) and/or transposed (pitch TP).
 template <int HD, int RP, int TP, bool ROW, bool TRN>
-__device__ __forceinline__ void stage_tile(const bf16_t *__restrict__ src, long ld, long t0, int col,
-                                           bf16_t *rows, bf16_t *trn) {
+__device__ __forceinline__ void stage_tile(const h16_t *__restrict__ src, long ld, long t0, int col,
+                                           h16_t *rows, h16_t *trn) {
   for (int c = threadIdx.x; c < BLK * HD / 8; c += 256) {
     const int r = c / (HD / 8), d8 = c % (HD / 8);
     const u16x8 v = *(const u16x8 *)(src + (t0 + r) * ld + col + d8 * 8);
@@ -60,11 +63,11 @@ __device__ __forceinline__ void stage_tile(const bf16_t *__restrict__ src, long 
   }
 }
 
-template <int HD>
+template <typename HT, int HD>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[BLK * RP];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[HD * TP];
+  __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
+  __shared__ __attribute__((aligned(16))) h16_t Vt[HD * TP];
   const int nqb = a.S / BLK;
   const int qb = nqb - 1 - blockIdx.x;  // longest rows first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -74,9 +77,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const long tb = (long)b * a.S;
   const int qi = qb * BLK + w * 16 + c16;  // this lane's query (position in sequence)
   const long tq = tb + qi;
-  bf16x8 qf[NK];
+  typename HT::v8 qf[NK];
 #pragma unroll
-  for (int kk = 0; kk < NK; kk++) qf[kk] = ld8(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
+  for (int kk = 0; kk < NK; kk++) qf[kk] = ld8<HT>(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
   f32x4 acc[ND];
 #pragma unroll
   for (int d = 0; d < ND; d++) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       s[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < NK; kk++)
-        s[nb] = mfma16(ld8(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], s[nb]);
+        s[nb] = HT::mfma16(ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], s[nb]);
     }
     // s[nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi)
     float mx = -INFINITY;
@@ -125,10 +128,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     for (int d = 0; d < ND; d++) acc[d] *= alpha;
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const bf16x8 pb = pack_acc(s[2 * c], s[2 * c + 1]);
+      const typename HT::v8 pb = pack_acc<HT>(s[2 * c], s[2 * c + 1]);
 #pragma unroll
       for (int d = 0; d < ND; d++)
-        acc[d] = mfma16(ld_pair4(Vt + (d * 16 + c16) * TP, 2 * c * 16 + g * 4, (2 * c + 1) * 16 + g * 4), pb, acc[d]);
+        acc[d] = HT::mfma16(ld_pair4<HT>(Vt + (d * 16 + c16) * TP, 2 * c * 16 + g * 4, (2 * c + 1) * 16 + g * 4), pb, acc[d]);
     }
   }
   const float l_tot = quad16_sum(l_i);
@@ -137,14 +140,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   for (int d = 0; d < ND; d++) {
     u16x4 o;
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = f2bf(acc[d][i] * inv);
+    for (int i = 0; i < 4; i++) o[i] = HT::h(acc[d][i] * inv);
     *(u16x4 *)(a.o + tq * a.ldo + h * HD + d * 16 + g * 4) = o;
   }
   if (g == 0) a.lse[tq * a.NH + h] = (m_i + log2f(l_tot)) * LN2;
 }
 
 // delta[t, h] = sum_d dO[t,h,d] * O[t,h,d]
-template <int HD>
+template <typename HT, int HD>
 __global__ void attn_delta_kernel(AttnArgs a, long rows) {
   constexpr int L = HD / 8;  // lanes per row
   const long gid = blockIdx.x * 256L + threadIdx.x;
@@ -157,20 +160,20 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
     const u16x8 o = *(const u16x8 *)(a.o + t * a.ldo + h * HD + j * 8);
     const u16x8 d = *(const u16x8 *)(a.dout + t * a.lddo + h * HD + j * 8);
 #pragma unroll
-    for (int e = 0; e < 8; e++) s += bf2f(o[e]) * bf2f(d[e]);
+    for (int e = 0; e < 8; e++) s += HT::f(o[e]) * HT::f(d[e]);
   }
 #pragma unroll
   for (int off = 1; off < L; off <<= 1) s += __shfl_xor(s, off, 64);
-  if (row < rows && j == 0) ((float *)a.delta)[row] = s;
+  if (row < rows && j == 0) a.delta[row] = s;
 }
 
-template <int HD>
+template <typename HT, int HD>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) bf16_t dOs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) bf16_t Qt[HD * TP];
-  __shared__ __attribute__((aligned(16))) bf16_t dOt[HD * TP];
+  __shared__ __attribute__((aligned(16))) h16_t Qs[BLK * RP];
+  __shared__ __attribute__((aligned(16))) h16_t dOs[BLK * RP];
+  __shared__ __attribute__((aligned(16))) h16_t Qt[HD * TP];
+  __shared__ __attribute__((aligned(16))) h16_t dOt[HD * TP];
   __shared__ float lse_s[BLK], dl_s[BLK];
   const int nqb = a.S / BLK;
   const int kb = blockIdx.x;  // smallest kb has the most query tiles: launched first
@@ -181,11 +184,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const long tb = (long)b * a.S;
   const int ki = kb * BLK + w * 16 + c16;  // this lane's key (as MFMA column)
   const long tk = tb + ki;
-  bf16x8 kf[NK], vf[NK];
+  typename HT::v8 kf[NK], vf[NK];
 #pragma unroll
   for (int kk = 0; kk < NK; kk++) {
-    kf[kk] = ld8(a.k + tk * a.ldk + kvh * HD + kk * 32 + g * 8);
-    vf[kk] = ld8(a.v + tk * a.ldv + kvh * HD + kk * 32 + g * 8);
+    kf[kk] = ld8<HT>(a.k + tk * a.ldk + kvh * HD + kk * 32 + g * 8);
+    vf[kk] = ld8<HT>(a.v + tk * a.ldv + kvh * HD + kk * 32 + g * 8);
   }
   f32x4 dk[ND], dv[ND];
 #pragma unroll
@@ -210,8 +213,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NK; kk++) {
-          sp[mb] = mfma16(ld8(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8), kf[kk], sp[mb]);
-          dp[mb] = mfma16(ld8(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8), vf[kk], dp[mb]);
+          sp[mb] = HT::mfma16(ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8), kf[kk], sp[mb]);
+          dp[mb] = HT::mfma16(ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8), vf[kk], dp[mb]);
         }
       }
       // sp[mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki)
@@ -227,35 +230,40 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         }
 #pragma unroll
       for (int c = 0; c < 2; c++) {
-        const bf16x8 pb = pack_acc(sp[2 * c], sp[2 * c + 1]);
-        const bf16x8 sb = pack_acc(dp[2 * c], dp[2 * c + 1]);
+        const typename HT::v8 pb = pack_acc<HT>(sp[2 * c], sp[2 * c + 1]);
+        const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
         const int c0 = 2 * c * 16 + g * 4, c1 = (2 * c + 1) * 16 + g * 4;
 #pragma unroll
         for (int d = 0; d < ND; d++) {
-          dv[d] = mfma16(ld_pair4(dOt + (d * 16 + c16) * TP, c0, c1), pb, dv[d]);
-          dk[d] = mfma16(ld_pair4(Qt + (d * 16 + c16) * TP, c0, c1), sb, dk[d]);
+          dv[d] = HT::mfma16(ld_pair4<HT>(dOt + (d * 16 + c16) * TP, c0, c1), pb, dv[d]);
+          dk[d] = HT::mfma16(ld_pair4<HT>(Qt + (d * 16 + c16) * TP, c0, c1), sb, dk[d]);
         }
       }
     }
   }
   // dv[d][i] = dV[key ki][dim d*16 + 4g + i]
+  bool bad = false;
 #pragma unroll
   for (int d = 0; d < ND; d++) {
     *(float4 *)(a.dk + tk * a.lddk + kvh * HD + d * 16 + g * 4) =
         make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
     u16x4 o;
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = f2bf(dv[d][i]);
+    for (int i = 0; i < 4; i++) {
+      o[i] = HT::h(dv[d][i]);
+      bad |= HT::bad(o[i]);
+    }
     *(u16x4 *)(a.dv + tk * a.lddv + kvh * HD + d * 16 + g * 4) = o;
   }
+  flag_overflow(a.ovf, bad);
 }
 
-template <int HD>
+template <typename HT, int HD>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[BLK * RP];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) bf16_t Kt[HD * TP];
+  __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
+  __shared__ __attribute__((aligned(16))) h16_t Vs[BLK * RP];
+  __shared__ __attribute__((aligned(16))) h16_t Kt[HD * TP];
   const int nqb = a.S / BLK;
   const int qb = nqb - 1 - blockIdx.x;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -265,11 +273,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const long tb = (long)b * a.S;
   const int qi = qb * BLK + w * 16 + c16;
   const long tq = tb + qi;
-  bf16x8 qf[NK], df[NK];
+  typename HT::v8 qf[NK], df[NK];
 #pragma unroll
   for (int kk = 0; kk < NK; kk++) {
-    qf[kk] = ld8(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
-    df[kk] = ld8(a.dout + tq * a.lddo + h * HD + kk * 32 + g * 8);
+    qf[kk] = ld8<HT>(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
+    df[kk] = ld8<HT>(a.dout + tq * a.lddo + h * HD + kk * 32 + g * 8);
   }
   const float lse2 = a.lse[tq * a.NH + h] * LOG2E;
   const float dl = a.delta[tq * a.NH + h];
@@ -289,8 +297,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       sp[nb] = dp[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < NK; kk++) {
-        sp[nb] = mfma16(ld8(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], sp[nb]);
-        dp[nb] = mfma16(ld8(Vs + (nb * 16 + c16) * RP + kk * 32 + g * 8), df[kk], dp[nb]);
+        sp[nb] = HT::mfma16(ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], sp[nb]);
+        dp[nb] = HT::mfma16(ld8<HT>(Vs + (nb * 16 + c16) * RP + kk * 32 + g * 8), df[kk], dp[nb]);
       }
     }
     // sp[nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi)
@@ -304,10 +312,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       }
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const bf16x8 sb = pack_acc(dp[2 * c], dp[2 * c + 1]);
+      const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
       const int c0 = 2 * c * 16 + g * 4, c1 = (2 * c + 1) * 16 + g * 4;
 #pragma unroll
-      for (int d = 0; d < ND; d++) dq[d] = mfma16(ld_pair4(Kt + (d * 16 + c16) * TP, c0, c1), sb, dq[d]);
+      for (int d = 0; d < ND; d++) dq[d] = HT::mfma16(ld_pair4<HT>(Kt + (d * 16 + c16) * TP, c0, c1), sb, dq[d]);
     }
   }
   // dq[d][i] = dQ[query qi][dim d*16 + 4g + i]
@@ -326,28 +334,42 @@ int check(const AttnArgs &a) {
 
 }  // namespace
 
-int launch_attn_fwd(const AttnArgs &a, hipStream_t s) {
-  NE_CHECK(check(a));
+namespace {
+
+template <typename HT>
+int fwd_t(const AttnArgs &a, hipStream_t s) {
   dim3 grid(a.S / BLK, a.NH, a.B);
-  if (a.HD == 128) hipLaunchKernelGGL(attn_fwd_kernel<128>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(256), 0, s, a);
+  if (a.HD == 128) hipLaunchKernelGGL((attn_fwd_kernel<HT, 128>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((attn_fwd_kernel<HT, 64>), grid, dim3(256), 0, s, a);
   return ne_hip_status(hipGetLastError(), "attn_fwd");
 }
 
-int launch_attn_bwd(const AttnArgs &a, hipStream_t s) {
-  NE_CHECK(check(a));
+template <typename HT>
+int bwd_t(const AttnArgs &a, hipStream_t s) {
   const long rows = (long)a.B * a.S * a.NH;
   const long thr = rows * (a.HD / 8);
-  if (a.HD == 128) hipLaunchKernelGGL(attn_delta_kernel<128>, dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
-  else hipLaunchKernelGGL(attn_delta_kernel<64>, dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
+  if (a.HD == 128) hipLaunchKernelGGL((attn_delta_kernel<HT, 128>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
+  else hipLaunchKernelGGL((attn_delta_kernel<HT, 64>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   NE_HIP(hipGetLastError());
   dim3 gkv(a.S / BLK, a.NKV, a.B), gq(a.S / BLK, a.NH, a.B);
   if (a.HD == 128) {
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<128>, gkv, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<128>, gq, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, 128>), gkv, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, 128>), gq, dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<64>, gkv, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, gq, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, 64>), gkv, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, 64>), gq, dim3(256), 0, s, a);
   }
   return ne_hip_status(hipGetLastError(), "attn_bwd");
+}
+
+}  // namespace
+
+int launch_attn_fwd(int dt, const AttnArgs &a, hipStream_t s) {
+  NE_CHECK(check(a));
+  return DISPATCH_H16(dt, fwd_t<HT>(a, s));
+}
+
+int launch_attn_bwd(int dt, const AttnArgs &a, hipStream_t s) {
+  NE_CHECK(check(a));
+  return DISPATCH_H16(dt, bwd_t<HT>(a, s));
 }

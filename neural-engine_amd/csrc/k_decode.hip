@@ -3,11 +3,11 @@
 // Per generated position every layer runs: RMSNorm -> fused QKV GEMV -> (QK-norm) RoPE +
 // KV-cache append -> GQA attention over the cache -> Wo GEMV + residual -> RMSNorm ->
 // W1|W3 GEMV -> SwiGLU -> W2 GEMV + residual; then the final norm, the tied LM-head GEMV
-// and greedy / temperature / top-p sampling on device.  Weights are the bf16 shadow;
+// and greedy / temperature / top-p sampling on device.  Weights are the 16-bit shadow;
 // activations, the KV cache and all accumulation are fp32.
 //
 // The GEMVs run on v_mfma_f32_16x16x4_f32: a wave multiplies 16 weight rows by up to 16
-// (or 32) sequences, each lane loading 8 consecutive bf16 weights per 32-wide K chunk, so
+// (or 32) sequences, each lane loading 8 consecutive 16-bit weights per 32-wide K chunk, so
 // every weight byte is read once per step whatever the batch.  The four waves of a block
 // split K and reduce through LDS (deterministic).
 #include <math.h>
@@ -34,8 +34,8 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
 }
 
 // out[b, n] = (resid ? resid[b,n] : 0) + alpha * sum_k W[n,k] x[b,k]
-template <int NB>
-__global__ __launch_bounds__(256) void gemv_kernel(const bf16_t *__restrict__ W, long ldw,
+template <typename HT, int NB>
+__global__ __launch_bounds__(256) void gemv_kernel(const h16_t *__restrict__ W, long ldw,
                                                    const float *__restrict__ x, int K,
                                                    float *out, long ldo, const float *resid, float alpha) {
   __shared__ f32x4 red[4][NB][64];
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16_t *__restrict__ W,
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16_t *wr = W + row * ldw;
+  const h16_t *wr = W + row * ldw;
   for (int k0 = kbeg; k0 < kbeg + ks; k0 += 32) {
     const u16x8 wv = *(const u16x8 *)(wr + k0 + g * 8);
 #pragma unroll
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16_t *__restrict__ W,
       const float4 xa = xr[0], xb = xr[1];
       const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc[nb] = mfma_f32(bf2f(wv[j]), xs[j], acc[nb]);
+      for (int j = 0; j < 8; j++) acc[nb] = mfma_f32(HT::f(wv[j]), xs[j], acc[nb]);
     }
   }
 #pragma unroll
@@ -79,11 +79,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16_t *__restrict__ W,
   }
 }
 
-__global__ void dec_embed_kernel(const bf16_t *__restrict__ E, const int32_t *__restrict__ tok, float *x, int D,
+template <typename HT>
+__global__ void dec_embed_kernel(const h16_t *__restrict__ E, const int32_t *__restrict__ tok, float *x, int D,
                                  int B) {
   const int b = blockIdx.x;
   for (int i = threadIdx.x; i < D; i += blockDim.x)
-    x[(long)b * D + i] = (b < B) ? bf2f(E[(long)tok[b] * D + i]) : 0.f;
+    x[(long)b * D + i] = (b < B) ? HT::f(E[(long)tok[b] * D + i]) : 0.f;
 }
 
 // generate.py:81-84: (x / rms) * w, rms = sqrt(mean(x^2) + eps); one block per sequence
@@ -327,12 +328,14 @@ __global__ void set_tokens_kernel(const int32_t *__restrict__ prompt, int P, int
   if (b < B) tok[b] = prompt[(long)b * P + pos];
 }
 
-int gemv(ne_ctx *c, const bf16_t *W, int N, int K, const float *x, float *out, const float *resid, float alpha) {
+int gemv(ne_ctx *c, const h16_t *W, int N, int K, const float *x, float *out, const float *resid, float alpha) {
   Dec *d = (Dec *)c->dec;
   if (N % 16 || K % 128) return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%16, K%%128)", N, K);
-  if (d->Bp == 16) hipLaunchKernelGGL(gemv_kernel<1>, dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
-  else hipLaunchKernelGGL(gemv_kernel<2>, dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
-  return ne_hip_status(hipGetLastError(), "decode gemv");
+  return DISPATCH_H16(c->dt, [&] {
+    if (d->Bp == 16) hipLaunchKernelGGL((gemv_kernel<HT, 1>), dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
+    else hipLaunchKernelGGL((gemv_kernel<HT, 2>), dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
+    return ne_hip_status(hipGetLastError(), "decode gemv");
+  }());
 }
 
 }  // namespace
@@ -406,13 +409,14 @@ int decode_run(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float 
     NE_HIP(hipMemcpyAsync(d->unif, u.data(), u.size() * 8, hipMemcpyHostToDevice, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
   }
-  const bf16_t *Pb = c->Pb;
+  const h16_t *Pb = c->Pb;
   const float *Pf = c->P;
   int rc = 0;
   int step = 0;
   for (int pos = 0; pos < P + n_new - 1 && !rc; pos++) {
     if (pos < P) hipLaunchKernelGGL(set_tokens_kernel, dim3(1), dim3(64), 0, c->st, dprompt, P, pos, d->tok, B);
-    hipLaunchKernelGGL(dec_embed_kernel, dim3(d->Bp), dim3(256), 0, c->st, Pb + c->off_E, d->tok, d->x, D, B);
+    if (c->dt == NE_FP16) hipLaunchKernelGGL(dec_embed_kernel<H16F>, dim3(d->Bp), dim3(256), 0, c->st, Pb + c->off_E, d->tok, d->x, D, B);
+    else hipLaunchKernelGGL(dec_embed_kernel<H16B>, dim3(d->Bp), dim3(256), 0, c->st, Pb + c->off_E, d->tok, d->x, D, B);
     for (int l = 0; l < c->L && !rc; l++) {
       const LayerOff &o = c->lo[l];
       const size_t kvl = (size_t)l * d->Bp * NKV * d->ctx * HD;

@@ -1,7 +1,7 @@
 // bf16 MFMA GEMM for gfx950 with LDS-staged tiles and fused epilogues.
 //
-// C[M,N] = epi(alpha * sum_k A[m,k] B[k,n]).  Operands are bf16 with fp32 accumulation
-// on v_mfma_f32_32x32x16_bf16.  Each operand may be K-contiguous (activation rows,
+// C[M,N] = epi(alpha * sum_k A[m,k] B[k,n]).  Operands are 16-bit (fp16 or bf16) with fp32
+// accumulation on v_mfma_f32_32x32x16_{f16,bf16}.  Each operand may be K-contiguous (activation rows,
 // weight rows [N,K]) or M/N-contiguous (the dY^T and X of a weight-gradient GEMM);
 // both are staged into LDS K-contiguous so every MFMA operand is one 16-byte LDS read.
 // M/N-contiguous tiles are transposed in registers in 4x8 blocks on the way into LDS.
@@ -25,7 +25,7 @@ struct Stage {
   static constexpr int NV = KC ? PER : PER * 4;
   u16x8 v[NV];
 
-  __device__ __forceinline__ void load(const bf16_t *p, long ld, int r0, int k0, int tid) {
+  __device__ __forceinline__ void load(const h16_t *p, long ld, int r0, int k0, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       int c = tid + i * NTHREADS;
@@ -44,7 +44,7 @@ struct Stage {
   }
 
   template <int PITCH>
-  __device__ __forceinline__ void store(bf16_t *lds, int tid) {
+  __device__ __forceinline__ void store(h16_t *lds, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       int c = tid + i * NTHREADS;
@@ -71,21 +71,21 @@ struct Stage {
 
 __device__ __forceinline__ float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
+template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
   constexpr int PITCH = BK + 8;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
   static_assert(WM * WN == 4, "4 waves");
   static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2][(BM + BN) * PITCH];
+  __shared__ __attribute__((aligned(16))) h16_t lds[2][(BM + BN) * PITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  const bf16_t *A = (const bf16_t *)g.A;
-  const bf16_t *B = (const bf16_t *)g.B;
+  const h16_t *A = (const h16_t *)g.A;
+  const h16_t *B = (const h16_t *)g.B;
 
   Stage<BM, BK, AKC> sa;
   Stage<BN, BK, BKC> sb;
@@ -110,21 +110,21 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
       sa.load(A, g.lda, m0, (kt + 1) * BK, tid);
       sb.load(B, g.ldb, n0, (kt + 1) * BK, tid);
     }
-    const bf16_t *As = lds[cur];
-    const bf16_t *Bs = lds[cur] + BM * PITCH;
+    const h16_t *As = lds[cur];
+    const h16_t *Bs = lds[cur] + BM * PITCH;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
-      bf16x8 a[FM], b[FN];
+      typename HT::v8 a[FM], b[FN];
 #pragma unroll
       for (int i = 0; i < FM; i++)
-        a[i] = as_bf16x8(*(const u16x8 *)(As + (wm * TM + i * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+        a[i] = HT::op(*(const u16x8 *)(As + (wm * TM + i * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
 #pragma unroll
       for (int j = 0; j < FN; j++)
-        b[j] = as_bf16x8(*(const u16x8 *)(Bs + (wn * TN + j * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+        b[j] = HT::op(*(const u16x8 *)(Bs + (wn * TN + j * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < FN; j++) acc[i][j] = HT::mfma32(a[i], b[j], acc[i][j]);
     }
     if (kt + 1 < nk) {
       sa.template store<PITCH>(lds[cur ^ 1], tid);
@@ -183,6 +183,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
     return;
   }
 
+  bool bad = false;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
 #pragma unroll
@@ -192,8 +193,10 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
       for (int e = 0; e < 16; e++) {
         const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         const float v = acc[i][j][e] * alpha;
-        if constexpr (EPI == EPI_BF16) {
-          ((bf16_t *)g.C)[(long)row * g.ldc + col] = f2bf(v);
+        if constexpr (EPI == EPI_H16) {
+          const h16_t o = HT::h(v);
+          bad |= HT::bad(o);
+          ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
         } else if constexpr (EPI == EPI_F32) {
           ((float *)g.C)[(long)row * g.ldc + col] = v;
         } else if constexpr (EPI == EPI_F32_ACC) {
@@ -201,50 +204,56 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
         } else if constexpr (EPI == EPI_RESID) {
           ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
         } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-          const bf16_t *h = (const bf16_t *)g.R + (long)row * g.ldr;
-          const float h1 = bf2f(h[col]), h3 = bf2f(h[g.N + col]);
+          const h16_t *h = (const h16_t *)g.R + (long)row * g.ldr;
+          const float h1 = HT::f(h[col]), h3 = HT::f(h[g.N + col]);
           const float sg = fast_sigmoid(h1);
-          bf16_t *d = (bf16_t *)g.C + (long)row * g.ldc;
-          d[col] = f2bf(v * h3 * sg * (1.f + h1 * (1.f - sg)));
-          d[g.N + col] = f2bf(v * h1 * sg);
+          h16_t *d = (h16_t *)g.C + (long)row * g.ldc;
+          const h16_t o1 = HT::h(v * h3 * sg * (1.f + h1 * (1.f - sg)));
+          const h16_t o3 = HT::h(v * h1 * sg);
+          bad |= HT::bad(o1) | HT::bad(o3);
+          d[col] = o1;
+          d[g.N + col] = o3;
         } else if constexpr (EPI == EPI_CE_BWD) {
           float p = __expf(v - g.lse[row]);
           if (col == g.targets[row]) p -= 1.f;
-          ((bf16_t *)g.C)[(long)row * g.ldc + col] = f2bf(p * g.scale);
+          const h16_t o = HT::h(p * g.scale);
+          bad |= HT::bad(o);
+          ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
         }
       }
     }
   }
+  flag_overflow(g.ovf, bad);
 }
 
 }  // namespace
 
 namespace {
 
-template <int BM, int BN, int WM, int WN, bool AKC, bool BKC, int EPI>
+template <typename HT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int EPI>
 int launch_t(GemmArgs g, hipStream_t s) {
   g.n_tiles = g.N / BN;
   dim3 grid(g.N / BN, g.M / BM);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(NTHREADS), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(NTHREADS), 0, s, g);
   return ne_hip_status(hipGetLastError(), "gemm launch");
 }
 
-template <bool AKC, bool BKC, int EPI>
+template <typename HT, bool AKC, bool BKC, int EPI>
 int launch_e(GemmArgs g, hipStream_t s) {
-  if (gemm_tile_n(g.M, g.N, g.K, EPI) == 128) return launch_t<128, 128, 2, 2, AKC, BKC, EPI>(g, s);
-  return launch_t<64, 64, 2, 2, AKC, BKC, EPI>(g, s);
+  if (gemm_tile_n(g.M, g.N, g.K, EPI) == 128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
+  return launch_t<HT, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
 }
 
-template <bool AKC, bool BKC>
+template <typename HT, bool AKC, bool BKC>
 int launch_l(int epi, GemmArgs g, hipStream_t s) {
   switch (epi) {
-    case EPI_BF16: return launch_e<AKC, BKC, EPI_BF16>(g, s);
-    case EPI_F32: return launch_e<AKC, BKC, EPI_F32>(g, s);
-    case EPI_F32_ACC: return launch_e<AKC, BKC, EPI_F32_ACC>(g, s);
-    case EPI_RESID: return launch_e<AKC, BKC, EPI_RESID>(g, s);
-    case EPI_SWIGLU_BWD: return launch_e<AKC, BKC, EPI_SWIGLU_BWD>(g, s);
-    case EPI_CE_FWD: return launch_e<AKC, BKC, EPI_CE_FWD>(g, s);
-    case EPI_CE_BWD: return launch_e<AKC, BKC, EPI_CE_BWD>(g, s);
+    case EPI_H16: return launch_e<HT, AKC, BKC, EPI_H16>(g, s);
+    case EPI_F32: return launch_e<HT, AKC, BKC, EPI_F32>(g, s);
+    case EPI_F32_ACC: return launch_e<HT, AKC, BKC, EPI_F32_ACC>(g, s);
+    case EPI_RESID: return launch_e<HT, AKC, BKC, EPI_RESID>(g, s);
+    case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, s);
+    case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, s);
+    case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, s);
   }
   return ne_fail(NE_ERR_ARG, "gemm: unknown epilogue %d", epi);
 }
@@ -258,16 +267,26 @@ int gemm_tile_n(int M, int N, int K, int epi) {
   return 64;
 }
 
-int gemm_launch(int layout, int epi, GemmArgs g, hipStream_t s) {
+namespace {
+
+template <typename HT>
+int launch_dt(int layout, int epi, GemmArgs g, hipStream_t s) {
+  switch (layout) {
+    case 0: return launch_l<HT, true, true>(epi, g, s);
+    case 1: return launch_l<HT, false, true>(epi, g, s);
+    case 2: return launch_l<HT, true, false>(epi, g, s);
+    case 3: return launch_l<HT, false, false>(epi, g, s);
+  }
+  return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
+}
+
+}  // namespace
+
+int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
     return ne_fail(NE_ERR_ARG, "gemm: M=%d N=%d K=%d must be positive multiples of 64", g.M, g.N, g.K);
   if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
     return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
-  switch (layout) {
-    case 0: return launch_l<true, true>(epi, g, s);
-    case 1: return launch_l<false, true>(epi, g, s);
-    case 2: return launch_l<true, false>(epi, g, s);
-    case 3: return launch_l<false, false>(epi, g, s);
-  }
-  return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
+  if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
+  return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, s));
 }

@@ -1,6 +1,6 @@
 // Embedding gather/scatter, RMSNorm fwd/bwd, SwiGLU gate, and the RoPE + QK-RMSNorm
 // prologue/epilogue of attention.  All HBM-bound: one wavefront per token row,
-// float4 / 8-byte vector accesses, fp32 arithmetic.
+// float4 / 8-byte vector accesses, fp32 arithmetic, 16-bit (fp16/bf16) GEMM operands out.
 #include "common.h"
 #include "ne_internal.h"
 
@@ -17,21 +17,22 @@ __global__ void embed_fwd_kernel(const float *__restrict__ E, const int32_t *__r
   for (int i = lane; i < D / 4; i += 64) dst[i] = src[i];
 }
 
-// gE[tok[t], :] += dx[t, :]   (TD/cpu_ops.h:441-447 embed_backward)
+// gE[tok[t], :] += scale * dx[t, :]   (TD/cpu_ops.h:441-447 embed_backward)
 __global__ void embed_bwd_kernel(float *__restrict__ gE, const int32_t *__restrict__ tok,
-                                 const float *__restrict__ dx, int T, int D) {
+                                 const float *__restrict__ dx, float scale, int T, int D) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
   float *dst = gE + (long)tok[row] * D;
   const float *src = dx + (long)row * D;
-  for (int i = lane; i < D; i += 64) atomicAdd(dst + i, src[i]);
+  for (int i = lane; i < D; i += 64) atomicAdd(dst + i, scale * src[i]);
 }
 
 // y = x * r * g, r = (mean(x^2) + eps)^-1/2   (TD/cpu_ops.h:20-60 rmsnorm)
+template <typename HT>
 __global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
-                                   bf16_t *__restrict__ y, float *__restrict__ rr, int T, int D,
-                                   float eps) {
+                                   h16_t *__restrict__ y, float *__restrict__ rr, int T, int D,
+                                   float eps, int *ovf) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= T) return;
@@ -46,26 +47,32 @@ __global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__r
   if (lane == 0) rr[row] = r;
   u16x4 *yr = (u16x4 *)(y + (long)row * D);
   const float4 *gv = (const float4 *)g;
+  bool bad = false;
   for (int i = lane; i < D / 4; i += 64) {
     float4 v = xr[i], w = gv[i];
     u16x4 o;
-    o[0] = f2bf(v.x * r * w.x);
-    o[1] = f2bf(v.y * r * w.y);
-    o[2] = f2bf(v.z * r * w.z);
-    o[3] = f2bf(v.w * r * w.w);
+    o[0] = HT::h(v.x * r * w.x);
+    o[1] = HT::h(v.y * r * w.y);
+    o[2] = HT::h(v.z * r * w.z);
+    o[3] = HT::h(v.w * r * w.w);
+    bad |= HT::bad(o[0]) | HT::bad(o[1]) | HT::bad(o[2]) | HT::bad(o[3]);
     yr[i] = o;
   }
+  flag_overflow(ovf, bad);
 }
 
 // Exact RMSNorm backward with fused residual add and gain-gradient accumulation:
 //   dx = r*g*dy - x*r^3*sum(dy*x*g)/D (+ resid);  dg += sum_t dy*x*r
-//   dxb = bf16(bscale * dx)  (the alpha-scaled operand of the next GEMM)
+//   dxb = 16-bit(bscale * dx)  (the alpha-scaled operand of the next GEMM); the gain
+//   gradient is accumulated times dg_scale (removes the backward's internal scale)
 // Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).
 constexpr int RMSB_MAXV = 8;  // float4 per lane: D <= 2048
+template <typename HT>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const float *__restrict__ dy, const float *__restrict__ x, const float *__restrict__ g,
     const float *__restrict__ rr, const float *__restrict__ resid, float *__restrict__ dx,
-    bf16_t *__restrict__ dxb, float bscale, float *__restrict__ dg, int T, int D, int rows_per_block) {
+    h16_t *__restrict__ dxb, float bscale, float *__restrict__ dg, float dg_scale, int T, int D,
+    int rows_per_block, int *ovf) {
   __shared__ float red[4][2048];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int D4 = D / 4;
@@ -76,6 +83,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
   const float invD = 1.0f / (float)D;
   const int r0 = blockIdx.x * rows_per_block;
   const int r1 = min(T, r0 + rows_per_block);
+  bool bad = false;
   for (int row = r0 + wave; row < r1; row += 4) {
     const float4 *dyr = (const float4 *)(dy + (long)row * D);
     const float4 *xr = (const float4 *)(x + (long)row * D);
@@ -115,10 +123,11 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
         dxr[i] = o;
         if (dbr) {
           u16x4 b;
-          b[0] = f2bf(o.x * bscale);
-          b[1] = f2bf(o.y * bscale);
-          b[2] = f2bf(o.z * bscale);
-          b[3] = f2bf(o.w * bscale);
+          b[0] = HT::h(o.x * bscale);
+          b[1] = HT::h(o.y * bscale);
+          b[2] = HT::h(o.z * bscale);
+          b[3] = HT::h(o.w * bscale);
+          bad |= HT::bad(b[0]) | HT::bad(b[1]) | HT::bad(b[2]) | HT::bad(b[3]);
           dbr[i] = b;
         }
         acc[j].x += dyv[j].x * xv[j].x * r;
@@ -128,6 +137,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
       }
     }
   }
+  flag_overflow(ovf, bad);
   // reduce the 4 waves' gain gradients, one atomic per channel per block
 #pragma unroll
   for (int j = 0; j < RMSB_MAXV; j++) {
@@ -141,12 +151,14 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
   }
   __syncthreads();
   for (int i = threadIdx.x; i < D; i += 256)
-    atomicAdd(dg + i, red[0][i] + red[1][i] + red[2][i] + red[3][i]);
+    atomicAdd(dg + i, dg_scale * (red[0][i] + red[1][i] + red[2][i] + red[3][i]));
 }
 
 // gate = silu(h1) * h3, h13 = [h1 | h3] per row   (TD/mil_dynamic.h:276-281)
-__global__ void swiglu_fwd_kernel(const bf16_t *__restrict__ h13, bf16_t *__restrict__ gate, int T,
-                                  int H) {
+template <typename HT>
+__global__ void swiglu_fwd_kernel(const h16_t *__restrict__ h13, h16_t *__restrict__ gate, int T,
+                                  int H, int *ovf) {
+  bool bad = false;
   const long n4 = (long)T * H / 4;
   for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
     const long e = i * 4;
@@ -156,11 +168,13 @@ __global__ void swiglu_fwd_kernel(const bf16_t *__restrict__ h13, bf16_t *__rest
     u16x4 o;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const float h1 = bf2f(a[j]), h3 = bf2f(b[j]);
-      o[j] = f2bf(h1 / (1.f + __expf(-h1)) * h3);
+      const float h1 = HT::f(a[j]), h3 = HT::f(b[j]);
+      o[j] = HT::h(h1 / (1.f + __expf(-h1)) * h3);
+      bad |= HT::bad(o[j]);
     }
     *(u16x4 *)(gate + e) = o;
   }
+  flag_overflow(ovf, bad);
 }
 
 // Per (token, head, pair): optional per-head RMSNorm with gain g[HD], then interleaved
@@ -168,11 +182,11 @@ __global__ void swiglu_fwd_kernel(const bf16_t *__restrict__ h13, bf16_t *__rest
 // Head slots 0..NH-1 are q heads (qkv columns h*HD), NH..NH+NKV-1 are k heads
 // (columns NH*HD + (h-NH)*HD).  Replaces the RoPE of gen_sdpa_fwd_dynamic
 // (TD/mil_dynamic.h:133-169).
-template <bool QKN>
-__global__ void qk_prep_fwd_kernel(const bf16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
+template <typename HT, bool QKN>
+__global__ void qk_prep_fwd_kernel(const h16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
                                    const float *__restrict__ sinb, const float *__restrict__ gq,
-                                   const float *__restrict__ gk, bf16_t *__restrict__ qr,
-                                   bf16_t *__restrict__ kr, float *__restrict__ rq, float *__restrict__ rk,
+                                   const float *__restrict__ gk, h16_t *__restrict__ qr,
+                                   h16_t *__restrict__ kr, float *__restrict__ rq, float *__restrict__ rk,
                                    int T, int S, int NH, int NKV, int HD, float eps) {
   const int half = HD / 2;
   const long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
@@ -186,7 +200,7 @@ __global__ void qk_prep_fwd_kernel(const bf16_t *__restrict__ qkv, long ld, cons
   const int hh = isq ? h : h - NH;
   const long col = (isq ? 0 : (long)NH * HD) + (long)hh * HD + 2 * i;
   const uint32_t pr = *(const uint32_t *)(qkv + t * ld + col);
-  float x0 = bf2f((bf16_t)(pr & 0xFFFF)), x1 = bf2f((bf16_t)(pr >> 16));
+  float x0 = HT::f((h16_t)(pr & 0xFFFF)), x1 = HT::f((h16_t)(pr >> 16));
   if (QKN) {
     float ss = x0 * x0 + x1 * x1;
     for (int o = 1; o < half; o <<= 1) ss += __shfl_xor(ss, o, 64);
@@ -202,7 +216,7 @@ __global__ void qk_prep_fwd_kernel(const bf16_t *__restrict__ qkv, long ld, cons
   const int pos = t % S;
   const float c = cosb[pos * half + i], s = sinb[pos * half + i];
   const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-  const uint32_t out = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+  const uint32_t out = (uint32_t)HT::h(y0) | ((uint32_t)HT::h(y1) << 16);
   if (isq) *(uint32_t *)(qr + t * (long)NH * HD + (long)hh * HD + 2 * i) = out;
   else *(uint32_t *)(kr + t * (long)NKV * HD + (long)hh * HD + 2 * i) = out;
 }
@@ -210,13 +224,14 @@ __global__ void qk_prep_fwd_kernel(const bf16_t *__restrict__ qkv, long ld, cons
 // Backward of qk_prep: inverse rotation (TD/cpu_ops.h:510-537), then the exact
 // per-head RMSNorm backward; gain gradients reduced per block, one atomic per channel.
 // Block = 256 threads = 256/(HD/2) token rows of one head slot; grid.y = head slot.
-template <bool QKN>
+template <typename HT, bool QKN>
 __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
-    const float *__restrict__ dq, const float *__restrict__ dk, const bf16_t *__restrict__ qkv, long ld,
+    const float *__restrict__ dq, const float *__restrict__ dk, const h16_t *__restrict__ qkv, long ld,
     const float *__restrict__ cosb, const float *__restrict__ sinb, const float *__restrict__ gq,
     const float *__restrict__ gk, const float *__restrict__ rq, const float *__restrict__ rk,
-    bf16_t *__restrict__ dqkv, float *__restrict__ dgq, float *__restrict__ dgk, int T, int S, int NH,
-    int NKV, int HD, int tok_per_block) {
+    h16_t *__restrict__ dqkv, float *__restrict__ dgq, float *__restrict__ dgk, float dg_scale, int T,
+    int S, int NH, int NKV, int HD, int tok_per_block, int *ovf) {
+  bool bad = false;
   __shared__ float red[256 * 2];
   const int half = HD / 2;
   const int i = threadIdx.x % half;
@@ -243,7 +258,7 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
     float d1 = dd.y * c - dd.x * s;
     if (QKN) {
       const uint32_t pr = *(const uint32_t *)(qkv + t * ld + col);
-      const float x0 = bf2f((bf16_t)(pr & 0xFFFF)), x1 = bf2f((bf16_t)(pr >> 16));
+      const float x0 = HT::f((h16_t)(pr & 0xFFFF)), x1 = HT::f((h16_t)(pr >> 16));
       const float r = isq ? rq[t * NH + hh] : rk[t * NKV + hh];
       float dot = d0 * x0 * g0 + d1 * x1 * g1;
       for (int o = 1; o < half; o <<= 1) dot += __shfl_xor(dot, o, 64);
@@ -253,8 +268,11 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
       d0 = r * g0 * d0 - x0 * cc;
       d1 = r * g1 * d1 - x1 * cc;
     }
-    *(uint32_t *)(dqkv + t * ld + col) = (uint32_t)f2bf(d0) | ((uint32_t)f2bf(d1) << 16);
+    const h16_t o0 = HT::h(d0), o1 = HT::h(d1);
+    bad |= HT::bad(o0) | HT::bad(o1);
+    *(uint32_t *)(dqkv + t * ld + col) = (uint32_t)o0 | ((uint32_t)o1 << 16);
   }
+  flag_overflow(ovf, bad);
   if (QKN) {
     red[threadIdx.x * 2] = a0;
     red[threadIdx.x * 2 + 1] = a1;
@@ -266,8 +284,8 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
         s1 += red[(k * half + i) * 2 + 1];
       }
       float *dg = isq ? dgq : dgk;
-      atomicAdd(dg + 2 * i, s0);
-      atomicAdd(dg + 2 * i + 1, s1);
+      atomicAdd(dg + 2 * i, dg_scale * s0);
+      atomicAdd(dg + 2 * i + 1, dg_scale * s1);
     }
   }
 }
@@ -280,55 +298,65 @@ int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D,
   return ne_hip_status(hipGetLastError(), "embed_fwd");
 }
 
-int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, hipStream_t s) {
-  hipLaunchKernelGGL(embed_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, dx, T, D);
+int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D, hipStream_t s) {
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, dx, scale, T, D);
   return ne_hip_status(hipGetLastError(), "embed_bwd");
 }
 
-int launch_rmsnorm_fwd(const float *x, const float *g, bf16_t *y, float *r, int T, int D, float eps,
-                       hipStream_t s) {
+int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D, float eps,
+                       int *ovf, hipStream_t s) {
   if (D % 4) return ne_fail(NE_ERR_ARG, "rmsnorm: D %% 4 != 0");
-  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, g, y, r, T, D, eps);
-  return ne_hip_status(hipGetLastError(), "rmsnorm_fwd");
+  return DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(rmsnorm_fwd_kernel<HT>, dim3((T + 3) / 4), dim3(256), 0, s, x, g, y, r, T, D, eps, ovf);
+    return ne_hip_status(hipGetLastError(), "rmsnorm_fwd");
+  }());
 }
 
-int launch_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
-                       const float *resid, float *dx, bf16_t *dxb, float bscale, float *dg, int T,
-                       int D, hipStream_t s) {
+int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
+                       const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
+                       int D, int *ovf, hipStream_t s) {
   if (D % 4 || D > 2048) return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
   const int rows = 64;
-  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((T + rows - 1) / rows), dim3(256), 0, s, dy, x, g, r,
-                     resid, dx, dxb, bscale, dg, T, D, rows);
-  return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
+  return DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3((T + rows - 1) / rows), dim3(256), 0, s, dy, x, g, r, resid,
+                       dx, dxb, bscale, dg, dg_scale, T, D, rows, ovf);
+    return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
+  }());
 }
 
-int launch_swiglu_fwd(const bf16_t *h13, bf16_t *gate, int T, int H, hipStream_t s) {
+int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s) {
   if (H % 4) return ne_fail(NE_ERR_ARG, "swiglu: H %% 4 != 0");
   const long n4 = (long)T * H / 4;
   const int blocks = (int)std::min<long>((n4 + 255) / 256, 8192);
-  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(blocks), dim3(256), 0, s, h13, gate, T, H);
-  return ne_hip_status(hipGetLastError(), "swiglu_fwd");
+  return DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(swiglu_fwd_kernel<HT>, dim3(blocks), dim3(256), 0, s, h13, gate, T, H, ovf);
+    return ne_hip_status(hipGetLastError(), "swiglu_fwd");
+  }());
 }
 
-int launch_qk_prep_fwd(const bf16_t *qkv, long ld, const float *cosb, const float *sinb,
-                       const float *gq, const float *gk, bf16_t *qr, bf16_t *kr, float *rq,
+int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
+                       const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq,
                        float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
   const long total = (long)T * (NH + NKV) * (HD / 2);
   const int blocks = (int)((total + 255) / 256);
-  if (gq) hipLaunchKernelGGL(qk_prep_fwd_kernel<true>, dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
-  else hipLaunchKernelGGL(qk_prep_fwd_kernel<false>, dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
-  return ne_hip_status(hipGetLastError(), "qk_prep_fwd");
+  return DISPATCH_H16(dt, [&] {
+    if (gq) hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, true>), dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
+    else hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, false>), dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
+    return ne_hip_status(hipGetLastError(), "qk_prep_fwd");
+  }());
 }
 
-int launch_qk_prep_bwd(const float *dq, const float *dk, const bf16_t *qkv, long ld,
+int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
-                       const float *rq, const float *rk, bf16_t *dqkv, float *dgq, float *dgk,
-                       int T, int S, int NH, int NKV, int HD, hipStream_t s) {
+                       const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk, float dg_scale,
+                       int T, int S, int NH, int NKV, int HD, int *ovf, hipStream_t s) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
   const int tpb = 256;
   dim3 grid((T + tpb - 1) / tpb, NH + NKV);
-  if (gq) hipLaunchKernelGGL(qk_prep_bwd_kernel<true>, grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, T, S, NH, NKV, HD, tpb);
-  else hipLaunchKernelGGL(qk_prep_bwd_kernel<false>, grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, T, S, NH, NKV, HD, tpb);
-  return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
+  return DISPATCH_H16(dt, [&] {
+    if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf);
+    else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf);
+    return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
+  }());
 }

@@ -2,9 +2,10 @@
 //
 // Replaces TD/train.m:782-849 (grad scale, global L2 norm, clip) and
 // TD/cpu_ops.h:266-303 adam_update called per tensor (TD/train.m:861-897), plus the
-// fp16 weight restaging of TD/train.m:872-895: here the update writes the bf16 shadow
+// fp16 weight restaging of TD/train.m:872-895: here the update writes the 16-bit shadow
 // the GEMMs read, in the same pass.  Per element: read p, g, m, v (16 B), write
-// p, m, v (12 B), bf16 shadow (2 B), zeroed g (4 B) = 34 B.
+// p, m, v (12 B), 16-bit shadow (2 B), zeroed g (4 B) = 34 B.  A step whose backward
+// overflowed the 16-bit range (device flag) leaves p, m, v untouched and only zeroes g.
 #include "common.h"
 #include "ne_internal.h"
 
@@ -43,14 +44,19 @@ __global__ void clip_finalize_kernel(const double *__restrict__ partials, int np
   }
 }
 
-template <bool SHADOW>
+template <typename HT, bool SHADOW>
 __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
   const float gs = a.gscale[0];
+  const bool skip = a.skip && a.skip[0];
   const float ob1 = 1.f - a.b1, ob2 = 1.f - a.b2;
   const float ibc1 = 1.f / a.bc1, ibc2 = 1.f / a.bc2;
   const long n4 = a.n / 4;
   float4 *p4 = (float4 *)a.p, *g4 = (float4 *)a.g, *m4 = (float4 *)a.m, *v4 = (float4 *)a.v;
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    if (skip) {
+      if (a.zero_grad) g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      continue;
+    }
     float4 p = p4[i], g = g4[i], m = m4[i], v = v4[i];
     const float wd = (i * 4 < a.n_decay) ? a.wd : 0.f;
     float pe[4] = {p.x, p.y, p.z, p.w}, ge[4] = {g.x, g.y, g.z, g.w};
@@ -69,17 +75,18 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
     if (a.zero_grad) g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (SHADOW) {
       u16x4 b;
-      b[0] = f2bf(pe[0]);
-      b[1] = f2bf(pe[1]);
-      b[2] = f2bf(pe[2]);
-      b[3] = f2bf(pe[3]);
+      b[0] = HT::h(pe[0]);
+      b[1] = HT::h(pe[1]);
+      b[2] = HT::h(pe[2]);
+      b[3] = HT::h(pe[3]);
       ((u16x4 *)a.pb)[i] = b;
     }
   }
 }
 
-__global__ void f32_to_bf16_kernel(const float *__restrict__ src, bf16_t *__restrict__ dst, long n) {
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = f2bf(src[i]);
+template <typename HT>
+__global__ void f32_to_h16_kernel(const float *__restrict__ src, h16_t *__restrict__ dst, long n) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = HT::h(src[i]);
 }
 
 __global__ void fill_f32_kernel(float *__restrict__ dst, float v, long n) {
@@ -102,17 +109,21 @@ int launch_clip_finalize(const double *partials, int nparts, float grad_scale, f
   return ne_hip_status(hipGetLastError(), "clip_finalize");
 }
 
-int launch_adam(const AdamArgs &a, hipStream_t s) {
+int launch_adam(int dt, const AdamArgs &a, hipStream_t s) {
   if (a.n % 4 || a.n_decay % 4) return ne_fail(NE_ERR_ARG, "adam: sizes must be multiples of 4");
   const int grid = grid_for(a.n / 4);
-  if (a.pb) hipLaunchKernelGGL(adam_kernel<true>, dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(adam_kernel<false>, dim3(grid), dim3(256), 0, s, a);
-  return ne_hip_status(hipGetLastError(), "adam");
+  return DISPATCH_H16(dt, [&] {
+    if (a.pb) hipLaunchKernelGGL((adam_kernel<HT, true>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((adam_kernel<HT, false>), dim3(grid), dim3(256), 0, s, a);
+    return ne_hip_status(hipGetLastError(), "adam");
+  }());
 }
 
-int launch_f32_to_bf16(const float *src, bf16_t *dst, long n, hipStream_t s) {
-  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
-  return ne_hip_status(hipGetLastError(), "f32_to_bf16");
+int launch_f32_to_h16(int dt, const float *src, h16_t *dst, long n, hipStream_t s) {
+  return DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(f32_to_h16_kernel<HT>, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
+    return ne_hip_status(hipGetLastError(), "f32_to_h16");
+  }());
 }
 
 int launch_fill_f32(float *dst, float v, long n, hipStream_t s) {

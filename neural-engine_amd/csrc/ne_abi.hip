@@ -1,4 +1,5 @@
 // Error plumbing and the kernel-level C-ABI entry points (device pointers).
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -24,120 +25,133 @@ int ne_hip_status(hipError_t e, const char *what) {
 extern "C" const char *ne_last_error(void) { return g_err; }
 
 #define S(stream) ((hipStream_t)(stream))
+#define CHECK_DT(dt) \
+  if ((dt) != NE_BF16 && (dt) != NE_FP16) return ne_fail(NE_ERR_ARG, "unknown 16-bit format %d", (dt))
 
-extern "C" int ne_k_rmsnorm_fwd(const float *x, const float *g, void *y, float *r, int T, int D, float eps,
-                                void *stream) {
-  return launch_rmsnorm_fwd(x, g, (bf16_t *)y, r, T, D, eps, S(stream));
+extern "C" int ne_k_rmsnorm_fwd(int dtype, const float *x, const float *g, void *y, float *r, int T, int D,
+                                float eps, void *stream) {
+  CHECK_DT(dtype);
+  return launch_rmsnorm_fwd(dtype, x, g, (h16_t *)y, r, T, D, eps, nullptr, S(stream));
 }
 
-extern "C" int ne_k_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
-                                const float *resid, float *dx, void *dxb, float bscale, float *dg, int T,
-                                int D, void *stream) {
-  return launch_rmsnorm_bwd(dy, x, g, r, resid, dx, (bf16_t *)dxb, bscale, dg, T, D, S(stream));
+extern "C" int ne_k_rmsnorm_bwd(int dtype, const float *dy, const float *x, const float *g, const float *r,
+                                const float *resid, float *dx, void *dxb, float bscale, float *dg,
+                                float dg_scale, int T, int D, void *stream) {
+  CHECK_DT(dtype);
+  return launch_rmsnorm_bwd(dtype, dy, x, g, r, resid, dx, (h16_t *)dxb, bscale, dg, dg_scale, T, D, nullptr,
+                            S(stream));
 }
 
-extern "C" int ne_k_gemm(int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
+extern "C" int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
                          const void *B, int64_t ldb, void *C, int64_t ldc, const void *R, int64_t ldr,
                          float alpha, void *stream) {
+  CHECK_DT(dtype);
   if (epi == EPI_CE_FWD || epi == EPI_CE_BWD || epi < 0 || epi > EPI_CE_BWD)
     return ne_fail(NE_ERR_ARG, "ne_k_gemm: epilogue %d not available here (use ne_k_ce_*)", epi);
   GemmArgs g = {};
   g.M = M; g.N = N; g.K = K;
   g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.R = R; g.ldr = ldr;
   g.alpha = alpha;
-  return gemm_launch(layout, epi, g, S(stream));
+  return gemm_launch(dtype, layout, epi, g, S(stream));
 }
 
-extern "C" int ne_k_qk_prep_fwd(const void *qkv, int64_t ld, const float *cosb, const float *sinb,
+extern "C" int ne_k_qk_prep_fwd(int dtype, const void *qkv, int64_t ld, const float *cosb, const float *sinb,
                                 const float *gq, const float *gk, void *qr, void *kr, float *rq, float *rk,
                                 int T, int S, int NH, int NKV, int HD, float eps, void *stream) {
-  return launch_qk_prep_fwd((const bf16_t *)qkv, ld, cosb, sinb, gq, gk, (bf16_t *)qr, (bf16_t *)kr, rq, rk,
+  CHECK_DT(dtype);
+  return launch_qk_prep_fwd(dtype, (const h16_t *)qkv, ld, cosb, sinb, gq, gk, (h16_t *)qr, (h16_t *)kr, rq, rk,
                             T, S, NH, NKV, HD, eps, S(stream));
 }
 
-extern "C" int ne_k_qk_prep_bwd(const float *dq, const float *dk, const void *qkv, int64_t ld,
+extern "C" int ne_k_qk_prep_bwd(int dtype, const float *dq, const float *dk, const void *qkv, int64_t ld,
                                 const float *cosb, const float *sinb, const float *gq, const float *gk,
                                 const float *rq, const float *rk, void *dqkv, float *dgq, float *dgk,
-                                int T, int S, int NH, int NKV, int HD, void *stream) {
-  return launch_qk_prep_bwd(dq, dk, (const bf16_t *)qkv, ld, cosb, sinb, gq, gk, rq, rk, (bf16_t *)dqkv, dgq,
-                            dgk, T, S, NH, NKV, HD, S(stream));
+                                float dg_scale, int T, int S, int NH, int NKV, int HD, void *stream) {
+  CHECK_DT(dtype);
+  return launch_qk_prep_bwd(dtype, dq, dk, (const h16_t *)qkv, ld, cosb, sinb, gq, gk, rq, rk, (h16_t *)dqkv,
+                            dgq, dgk, dg_scale, T, S, NH, NKV, HD, nullptr, S(stream));
 }
 
 static AttnArgs attn_args(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,
                           int B, int S, int NH, int NKV, int HD, float scale) {
   AttnArgs a = {};
-  a.q = (const bf16_t *)q; a.ldq = ldq;
-  a.k = (const bf16_t *)k; a.ldk = ldk;
-  a.v = (const bf16_t *)v; a.ldv = ldv;
+  a.q = (const h16_t *)q; a.ldq = ldq;
+  a.k = (const h16_t *)k; a.ldk = ldk;
+  a.v = (const h16_t *)v; a.ldv = ldv;
   a.B = B; a.S = S; a.NH = NH; a.NKV = NKV; a.HD = HD; a.scale = scale;
   return a;
 }
 
-extern "C" int ne_k_attn_fwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+extern "C" int ne_k_attn_fwd(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
                              int64_t ldv, void *o, int64_t ldo, float *lse, int B, int S, int NH, int NKV,
                              int HD, float scale, void *stream) {
+  CHECK_DT(dtype);
   AttnArgs a = attn_args(q, ldq, k, ldk, v, ldv, B, S, NH, NKV, HD, scale);
-  a.o = (bf16_t *)o; a.ldo = ldo; a.lse = lse;
-  return launch_attn_fwd(a, S(stream));
+  a.o = (h16_t *)o; a.ldo = ldo; a.lse = lse;
+  return launch_attn_fwd(dtype, a, S(stream));
 }
 
-extern "C" int ne_k_attn_bwd(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
+extern "C" int ne_k_attn_bwd(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v,
                              int64_t ldv, const void *o, int64_t ldo, const float *lse, const void *dout,
                              int64_t lddo, float *delta, float *dq, int64_t lddq, float *dk, int64_t lddk,
                              void *dv, int64_t lddv, int B, int S, int NH, int NKV, int HD, float scale,
                              void *stream) {
+  CHECK_DT(dtype);
   AttnArgs a = attn_args(q, ldq, k, ldk, v, ldv, B, S, NH, NKV, HD, scale);
-  a.o = (bf16_t *)o; a.ldo = ldo; a.lse = (float *)lse;
-  a.dout = (const bf16_t *)dout; a.lddo = lddo; a.delta = delta;
-  a.dq = dq; a.lddq = lddq; a.dk = dk; a.lddk = lddk; a.dv = (bf16_t *)dv; a.lddv = lddv;
-  return launch_attn_bwd(a, S(stream));
+  a.o = (h16_t *)o; a.ldo = ldo; a.lse = (float *)lse;
+  a.dout = (const h16_t *)dout; a.lddo = lddo; a.delta = delta;
+  a.dq = dq; a.lddq = lddq; a.dk = dk; a.lddk = lddk; a.dv = (h16_t *)dv; a.lddv = lddv;
+  return launch_attn_bwd(dtype, a, S(stream));
 }
 
-int ce_forward(const void *x, const void *E, const int32_t *targets, int T, int D, int V, float *part,
+int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, float *part,
                float *tgt_logit, float *lse, float *loss_rows, float *loss, hipStream_t s) {
   GemmArgs g = {};
   g.M = T; g.N = V; g.K = D;
   g.A = x; g.lda = D; g.B = E; g.ldb = D;
   g.alpha = 1.f;
   g.targets = targets; g.part = part; g.tgt_logit = tgt_logit;
-  NE_CHECK(gemm_launch(GEMM_NT, EPI_CE_FWD, g, s));
+  NE_CHECK(gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s));
   return launch_ce_reduce(part, V / gemm_tile_n(T, V, D, EPI_CE_FWD), tgt_logit, lse, loss_rows, loss, T, s);
 }
 
-int ce_backward(const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D, int V,
-                float scale, void *dlogits, hipStream_t s) {
+int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D,
+                int V, float scale, void *dlogits, int *ovf, hipStream_t s) {
   GemmArgs g = {};
   g.M = T; g.N = V; g.K = D;
   g.A = x; g.lda = D; g.B = E; g.ldb = D;
   g.C = dlogits; g.ldc = V;
   g.alpha = 1.f; g.scale = scale;
-  g.targets = targets; g.lse = lse;
-  return gemm_launch(GEMM_NT, EPI_CE_BWD, g, s);
+  g.targets = targets; g.lse = lse; g.ovf = ovf;
+  return gemm_launch(dt, GEMM_NT, EPI_CE_BWD, g, s);
 }
 
-extern "C" int ne_k_ce_fwd(const void *x, const void *E, const int32_t *targets, int T, int D, int V,
+extern "C" int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
                            float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                            void *stream) {
-  return ce_forward(x, E, targets, T, D, V, part, tgt_logit, lse, loss_rows, loss, S(stream));
+  CHECK_DT(dtype);
+  return ce_forward(dtype, x, E, targets, T, D, V, part, tgt_logit, lse, loss_rows, loss, S(stream));
 }
 
-extern "C" int ne_k_ce_bwd(const void *x, const void *E, const int32_t *targets, const float *lse, int T,
-                           int D, int V, float scale, void *dlogits, void *stream) {
-  return ce_backward(x, E, targets, lse, T, D, V, scale, dlogits, S(stream));
+extern "C" int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_t *targets, const float *lse,
+                           int T, int D, int V, float scale, void *dlogits, void *stream) {
+  CHECK_DT(dtype);
+  return ce_backward(dtype, x, E, targets, lse, T, D, V, scale, dlogits, nullptr, S(stream));
 }
 
-extern "C" int ne_k_adam(float *p, float *g, float *m, float *v, void *pb, int64_t n, int64_t n_decay,
-                         float lr, float b1, float b2, float eps, float wd, int t, const float *gscale,
-                         int zero_grad, void *stream) {
+extern "C" int ne_k_adam(int dtype, float *p, float *g, float *m, float *v, void *pb, int64_t n,
+                         int64_t n_decay, float lr, float b1, float b2, float eps, float wd, int t,
+                         const float *gscale, int zero_grad, void *stream) {
+  CHECK_DT(dtype);
   if (t < 1) return ne_fail(NE_ERR_ARG, "adam: step t=%d must be >= 1", t);
   AdamArgs a = {};
-  a.p = p; a.g = g; a.m = m; a.v = v; a.pb = (bf16_t *)pb;
+  a.p = p; a.g = g; a.m = m; a.v = v; a.pb = (h16_t *)pb;
   a.n = n; a.n_decay = n_decay;
   a.lr = lr; a.b1 = b1; a.b2 = b2; a.eps = eps; a.wd = wd;
   a.bc1 = 1.f - powf(b1, (float)t);
   a.bc2 = 1.f - powf(b2, (float)t);
   a.gscale = gscale; a.zero_grad = zero_grad;
-  return launch_adam(a, S(stream));
+  return launch_adam(dtype, a, S(stream));
 }
 
 extern "C" int ne_k_grad_norm(const float *g, int64_t n, float grad_scale, float clip, double *partials,
@@ -150,10 +164,12 @@ extern "C" int ne_k_embed_fwd(const float *E, const int32_t *tok, float *x, int 
   return launch_embed_fwd(E, tok, x, T, D, S(stream));
 }
 
-extern "C" int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, void *stream) {
-  return launch_embed_bwd(gE, tok, dx, T, D, S(stream));
+extern "C" int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D,
+                              void *stream) {
+  return launch_embed_bwd(gE, tok, dx, scale, T, D, S(stream));
 }
 
-extern "C" int ne_k_swiglu_fwd(const void *h13, void *gate, int T, int H, void *stream) {
-  return launch_swiglu_fwd((const bf16_t *)h13, (bf16_t *)gate, T, H, S(stream));
+extern "C" int ne_k_swiglu_fwd(int dtype, const void *h13, void *gate, int T, int H, void *stream) {
+  CHECK_DT(dtype);
+  return launch_swiglu_fwd(dtype, (const h16_t *)h13, (h16_t *)gate, T, H, nullptr, S(stream));
 }

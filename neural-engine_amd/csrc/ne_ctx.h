@@ -27,7 +27,7 @@ struct Prof {
 
 struct LayerAct {
   float *x_in, *r1, *x2, *r2, *rq, *rk, *lse;
-  bf16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
+  h16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
 };
 
 struct LayerOff {
@@ -37,24 +37,29 @@ struct LayerOff {
 struct ne_ctx {
   ne_config c;
   int D, H, NH, NKV, HD, L, V, S, B, T, Q, KV, QKV;
+  int dt;                 // 16-bit format (NE_BF16 / NE_FP16)
+  float gs = 1024.f;      // internal gradient scale: dlogits = (p - onehot) * gs
+  int32_t skipped = 0;    // optimizer steps skipped after a 16-bit overflow
+  int good_steps = 0;     // consecutive non-overflowing optimizer steps
   hipStream_t st = nullptr;
   long n_params = 0, n_decay = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
-  bf16_t *Pb = nullptr;
+  h16_t *Pb = nullptr;
   std::vector<LayerOff> lo;
   long off_E = 0, off_gfinal = 0;
   std::vector<long> t_off, t_numel;  // per tensor id
   void *arena = nullptr;
   std::vector<LayerAct> act;
   float *xL, *rf;
-  bf16_t *xf;
+  h16_t *xf;
   float *dx, *dx2, *dtmp, *dq, *dk, *delta;
-  bf16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
+  h16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
   float *ce_part, *ce_tgt, *ce_lse, *ce_rows, *loss;
   int32_t *tok_in, *tok_tgt;
   float *cosb, *sinb;
   double *gn_part;
   float *gscale, *gnorm;
+  int *ovf;               // device flag: a 16-bit value of this accumulation window overflowed
   int32_t *h_tok = nullptr;  // pinned [2T]
   float *h_scalar = nullptr; // pinned [4]
   ne_train_state state = {};

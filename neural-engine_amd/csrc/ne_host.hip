@@ -3,7 +3,7 @@
 // k_*.hip on the context's single stream.
 //
 // Device memory (all resident, nothing round-trips through the host during a step):
-//   flat fp32 buffers P (master weights), G (grads), M, V (Adam) and the bf16 shadow Pb
+//   flat fp32 buffers P (master weights), G (grads), M, V (Adam) and the 16-bit shadow Pb
 //   of P, one element order for all five:
 //     per layer: Wqkv [Q+2KV, D] (= Wq;Wk;Wv rows), Wo [D,Q], W13 [2H, D] (= W1;W3 rows),
 //                W2 [D,H]
@@ -111,7 +111,8 @@ int gemm(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, const voi
   g.M = M; g.N = N; g.K = K;
   g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.R = R; g.ldr = ldr;
   g.alpha = alpha;
-  return gemm_launch(layout, epi, g, c->st);
+  g.ovf = c->ovf;
+  return gemm_launch(c->dt, layout, epi, g, c->st);
 }
 
 int validate(const ne_config *c) {
@@ -126,6 +127,7 @@ int validate(const ne_config *c) {
     return ne_fail(NE_ERR_ARG, "config: dim, hidden and vocab must be multiples of 64");
   if (c->dim > 2048) return ne_fail(NE_ERR_ARG, "config: dim > 2048 unsupported");
   if (c->decode_batch < 0 || c->decode_ctx < 0) return ne_fail(NE_ERR_ARG, "config: negative decode sizes");
+  if (c->dtype != NE_BF16 && c->dtype != NE_FP16) return ne_fail(NE_ERR_ARG, "config: dtype must be NE_BF16 or NE_FP16");
   return 0;
 }
 
@@ -201,6 +203,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   c->D = cfg->dim; c->H = cfg->hidden; c->NH = cfg->n_heads; c->NKV = cfg->kv_heads; c->HD = cfg->head_dim;
   c->L = cfg->n_layers; c->V = cfg->vocab; c->S = cfg->seq; c->B = cfg->batch; c->T = c->B * c->S;
   c->Q = c->NH * c->HD; c->KV = c->NKV * c->HD; c->QKV = c->Q + 2 * c->KV;
+  c->dt = cfg->dtype;
   layout_params(c);
   const size_t T = c->T, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, NH = c->NH, NKV = c->NKV;
   Plan pl;
@@ -228,7 +231,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
   pl.add(&c->tok_in, T); pl.add(&c->tok_tgt, T);
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
-  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4);
+  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 4);
 
   int rc = 0;
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
@@ -242,7 +245,8 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if ((rc = ne_hip_status(hipMemsetAsync(c->M, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = ne_hip_status(hipMemsetAsync(c->Vm, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = launch_fill_f32(c->P + c->n_decay, 1.f, c->n_params - c->n_decay, c->st))) goto fail;
-  if ((rc = launch_f32_to_bf16(c->P, c->Pb, c->n_params, c->st))) goto fail;
+  if ((rc = ne_hip_status(hipMemsetAsync(c->ovf, 0, 16, c->st), "memset"))) goto fail;
+  if ((rc = launch_f32_to_h16(c->dt, c->P, c->Pb, c->n_params, c->st))) goto fail;
   {
     // RoPE tables [S, HD/2]: angle = pos * theta^(-2i/HD), evaluated in double
     const int half = c->HD / 2;
@@ -304,7 +308,7 @@ extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, siz
   float *base = kind_base(c, kind);
   if (!base) return ne_fail(NE_ERR_ARG, "bad tensor kind %d", kind);
   NE_HIP(hipMemcpyAsync(base + c->t_off[id], host, n * 4, hipMemcpyHostToDevice, c->st));
-  if (kind == NE_PARAM) NE_CHECK(launch_f32_to_bf16(c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
+  if (kind == NE_PARAM) NE_CHECK(launch_f32_to_h16(c->dt, c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   return 0;
 }
@@ -346,12 +350,20 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
       c->h_tok[T + (long)b * S + s] = tt;
     }
   NE_HIP(hipMemcpyAsync(c->tok_in, c->h_tok, 2 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
-  const bf16_t *Pb = c->Pb;
+  const h16_t *Pb = c->Pb;
   const float *P = c->P;
   float *G = c->G;
   AttnArgs at = {};
   at.B = c->B; at.S = S; at.NH = c->NH; at.NKV = c->NKV; at.HD = c->HD;
   at.scale = 1.0f / sqrtf((float)c->HD);
+
+  // The backward runs at an internal power-of-two scale gs (dlogits = (p - onehot) * gs) that
+  // keeps 16-bit gradients in range; fp32 sinks (weight / gain / embedding grads) take
+  // u = (loss_scale / T) / gs, so G accumulates d(loss * loss_scale)/dw exactly as the
+  // reference's loss_scale convention (TD/train.m:180, TD/cpu_ops.h:348-382).
+  const int dt = c->dt;
+  const float u = loss_scale / (float)T / c->gs;
+  int *ovf = c->ovf;
 
   // ---------------- forward ----------------
   {
@@ -364,50 +376,49 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
     float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_BF16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
     {
       ProfScope ps(c, NE_PROF_ATTN_FWD);
-      NE_CHECK(launch_qk_prep_fwd(a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
+      NE_CHECK(launch_qk_prep_fwd(dt, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.qr, a.kr, a.rq, a.rk, T, S, c->NH, c->NKV,
                                   c->HD, eps, c->st));
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
-      NE_CHECK(launch_attn_fwd(at, c->st));
+      NE_CHECK(launch_attn_fwd(dt, at, c->st));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, D, a.x_in, D, alpha));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_BF16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_swiglu_fwd(a.h13, a.gate, T, H, c->st));
+      NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf, c->st));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, D, a.x2, D, alpha));
   }
   {
     ProfScope ps(c, NE_PROF_NORM);
-    NE_CHECK(launch_rmsnorm_fwd(c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, c->st));
+    NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf, c->st));
   }
   {
     ProfScope ps(c, NE_PROF_CE);
-    NE_CHECK(ce_forward(c->xf, Pb + c->off_E, c->tok_tgt, T, D, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
+    NE_CHECK(ce_forward(dt, c->xf, Pb + c->off_E, c->tok_tgt, T, D, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
                         c->loss, c->st));
-    NE_CHECK(ce_backward(c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, loss_scale / (float)T, c->dlogits,
-                         c->st));
+    NE_CHECK(ce_backward(dt, c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, c->gs, c->dlogits, ovf, c->st));
   }
   if (loss_out) NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
 
-  // ---------------- backward ----------------
+  // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
   NE_CHECK(gemm(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
-  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_TN, EPI_F32_ACC, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D));
+  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_TN, EPI_F32_ACC, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
   {
     ProfScope ps(c, NE_PROF_NORM);
-    NE_CHECK(launch_rmsnorm_bwd(c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, T, D, c->st));
+    NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
+                                G + c->off_gfinal, u, T, D, ovf, c->st));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
@@ -415,40 +426,43 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
     // FFN: dbf = alpha * dx
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
                   a.h13, 2 * H));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H, nullptr, 0, u));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp, D));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D,
+                  nullptr, 0, u));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_bwd(c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, T, D,
-                                  c->st));
+      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
+                                  T, D, ovf, c->st));
     }
     // attention: dbf = alpha * dx2
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_BF16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q, nullptr, 0, u));
     {
       ProfScope ps(c, NE_PROF_ATTN_BWD);
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
       at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = c->dqkv + Q + KV; at.lddv = QKV;
-      NE_CHECK(launch_attn_bwd(at, c->st));
-      NE_CHECK(launch_qk_prep_bwd(c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
+      at.ovf = ovf;
+      NE_CHECK(launch_attn_bwd(dt, at, c->st));
+      NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
-                                  c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, T, S,
-                                  c->NH, c->NKV, c->HD, c->st));
+                                  c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
+                                  c->NH, c->NKV, c->HD, ovf, c->st));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
+                  0, u));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_bwd(c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att, T,
-                                  D, c->st));
+      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att,
+                                  u, T, D, ovf, c->st));
     }
   }
   {
     ProfScope ps(c, NE_PROF_EMBED);
-    NE_CHECK(launch_embed_bwd(G + c->off_E, c->tok_in, c->dx, T, D, c->st));
+    NE_CHECK(launch_embed_bwd(G + c->off_E, c->tok_in, c->dx, u, T, D, c->st));
   }
   if (loss_out) {
     NE_HIP(hipStreamSynchronize(c->st));
@@ -460,6 +474,7 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
 extern "C" int ne_zero_grads(ne_ctx *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
+  NE_HIP(hipMemsetAsync(c->ovf, 0, 4, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   return 0;
 }
@@ -467,6 +482,21 @@ extern "C" int ne_zero_grads(ne_ctx *c) {
 extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float eps, float wd, float grad_scale,
                                  float clip, float *gnorm_out) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  // overflow check of the accumulation window (dynamic gradient scaling)
+  NE_HIP(hipMemcpyAsync(c->h_scalar + 2, c->ovf, 4, hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  int32_t flag;
+  memcpy(&flag, c->h_scalar + 2, 4);
+  if (flag) {
+    NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
+    NE_HIP(hipMemsetAsync(c->ovf, 0, 4, c->st));
+    NE_HIP(hipStreamSynchronize(c->st));
+    c->gs = c->gs * 0.5f;
+    c->skipped += 1;
+    c->good_steps = 0;
+    if (gnorm_out) *gnorm_out = NAN;
+    return 1;
+  }
   {
     ProfScope ps(c, NE_PROF_GNORM);
     NE_CHECK(launch_sumsq(c->G, c->n_params, c->gn_part, 1024, c->st));
@@ -483,14 +513,26 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   a.gscale = c->gscale; a.zero_grad = 1;
   {
     ProfScope ps(c, NE_PROF_ADAM);
-    NE_CHECK(launch_adam(a, c->st));
+    NE_CHECK(launch_adam(c->dt, a, c->st));
   }
   c->state.lr = lr;
+  // grow the internal scale after a long overflow-free run (bounded)
+  if (++c->good_steps >= 1000 && c->gs < 65536.f) {
+    c->gs *= 2.f;
+    c->good_steps = 0;
+  }
   if (gnorm_out) {
     NE_HIP(hipMemcpyAsync(c->h_scalar + 1, c->gnorm, 4, hipMemcpyDeviceToHost, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
     *gnorm_out = c->h_scalar[1];
   }
+  return 0;
+}
+
+extern "C" int ne_grad_scale_info(const ne_ctx *c, float *scale, int32_t *skipped) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  if (scale) *scale = c->gs;
+  if (skipped) *skipped = c->skipped;
   return 0;
 }
 
@@ -602,7 +644,7 @@ extern "C" int ne_load_ckpt_v4(ne_ctx *c, const char *path, ne_train_state *st) 
   }
   fclose(f);
   if (rc) return rc;
-  NE_CHECK(launch_f32_to_bf16(c->P, c->Pb, c->n_params, c->st));
+  NE_CHECK(launch_f32_to_h16(c->dt, c->P, c->Pb, c->n_params, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   c->state.step = h.step; c->state.total_steps = h.total_steps; c->state.lr = h.lr; c->state.loss = h.loss;
   c->state.cum_compile = h.cum_compile; c->state.cum_train = h.cum_train; c->state.cum_wall = h.cum_wall;

@@ -1,10 +1,12 @@
 // Internal host-side declarations shared by the kernel files and the orchestrator.
+// `dt` selects the 16-bit format (0 bf16, 1 fp16); `ovf` (nullable) is a device int set
+// to 1 when a 16-bit result is not finite.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
-typedef uint16_t bf16_t;
+typedef uint16_t h16_t;
 
 // ---- error plumbing (thread-local last error, negative status codes) ----
 int ne_fail(int code, const char *fmt, ...);
@@ -28,17 +30,17 @@ enum {
   NE_ERR_NOMEM = -5,
 };
 
-// ---- GEMM: C[M,N] = epilogue(alpha * A[M,K] . B[K,N]) on bf16 MFMA (k_gemm.hip) ----
+// ---- GEMM: C[M,N] = epilogue(alpha * A[M,K] . B[K,N]) on 16-bit MFMA (k_gemm.hip) ----
 // layout bit 0: A stored M-contiguous ([K,M]); bit 1: B stored N-contiguous ([K,N]).
 enum { GEMM_NT = 0, GEMM_NN = 2, GEMM_TN = 3 };
 enum {
-  EPI_BF16 = 0,        // C bf16
+  EPI_H16 = 0,         // C 16-bit
   EPI_F32 = 1,         // C fp32
   EPI_F32_ACC = 2,     // C fp32 += result
   EPI_RESID = 3,       // C fp32 = R fp32 + result
-  EPI_SWIGLU_BWD = 4,  // result is dgate [M,N]; R = h13 bf16 [M,2N]; C = dh13 bf16 [M,2N]
+  EPI_SWIGLU_BWD = 4,  // result is dgate [M,N]; R = h13 16-bit [M,2N]; C = dh13 16-bit [M,2N]
   EPI_CE_FWD = 5,      // result is logits; writes per-(row, N-tile) max/sumexp + target logit
-  EPI_CE_BWD = 6,      // C bf16 = (exp(logit - lse) - onehot) * scale
+  EPI_CE_BWD = 6,      // C 16-bit = (exp(logit - lse) - onehot) * scale
 };
 
 struct GemmArgs {
@@ -46,71 +48,81 @@ struct GemmArgs {
   const void *A; long lda;
   const void *B; long ldb;
   void *C; long ldc;
-  const void *R; long ldr;   // EPI_RESID: fp32 residual; EPI_SWIGLU_BWD: bf16 h13
+  const void *R; long ldr;   // EPI_RESID: fp32 residual; EPI_SWIGLU_BWD: 16-bit h13
   float alpha;
   float scale;               // EPI_CE_BWD gradient scale
   const int32_t *targets;    // [M] (CE epilogues)
   const float *lse;          // [M] (EPI_CE_BWD)
   float *part;               // [M, n_tiles, 2] (EPI_CE_FWD): tile max, tile sum exp
   float *tgt_logit;          // [M] (EPI_CE_FWD)
+  int *ovf;                  // 16-bit outputs: overflow flag (nullable)
   int n_tiles;               // set by the launcher: N / BN
 };
 
-int gemm_launch(int layout, int epi, GemmArgs a, hipStream_t s);
+int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s);
 int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this shape
 
 // ---- embedding / normalisation / elementwise (k_norm.hip) ----
 int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, hipStream_t s);
-int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, int T, int D, hipStream_t s);
-int launch_rmsnorm_fwd(const float *x, const float *g, bf16_t *y, float *r, int T, int D, float eps,
-                       hipStream_t s);
-int launch_rmsnorm_bwd(const float *dy, const float *x, const float *g, const float *r,
-                       const float *resid, float *dx, bf16_t *dxb, float bscale, float *dg, int T,
-                       int D, hipStream_t s);
-int launch_swiglu_fwd(const bf16_t *h13, bf16_t *gate, int T, int H, hipStream_t s);
-int launch_qk_prep_fwd(const bf16_t *qkv, long ld, const float *cosb, const float *sinb,
-                       const float *gq, const float *gk, bf16_t *qr, bf16_t *kr, float *rq,
-                       float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s);
-int launch_qk_prep_bwd(const float *dq, const float *dk, const bf16_t *qkv, long ld,
+int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D,
+                     hipStream_t s);
+int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D,
+                       float eps, int *ovf, hipStream_t s);
+int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
+                       const float *resid, float *dx, h16_t *dxb, float bscale, float *dg,
+                       float dg_scale, int T, int D, int *ovf, hipStream_t s);
+int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s);
+int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
+                       const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq, float *rk,
+                       int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s);
+int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
-                       const float *rq, const float *rk, bf16_t *dqkv, float *dgq, float *dgk,
-                       int T, int S, int NH, int NKV, int HD, hipStream_t s);
+                       const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk,
+                       float dg_scale, int T, int S, int NH, int NKV, int HD, int *ovf,
+                       hipStream_t s);
 
 // ---- attention (k_attn.hip): causal, GQA kv head = q head / (NH/NKV) ----
 struct AttnArgs {
-  const bf16_t *q; long ldq;   // [T, NH*HD] rows of the batch-major token index t = b*S + s
-  const bf16_t *k; long ldk;   // [T, NKV*HD]
-  const bf16_t *v; long ldv;   // [T, NKV*HD]
-  bf16_t *o; long ldo;         // [T, NH*HD]
-  float *lse;                  // [T, NH] natural-log sum exp of scaled scores
+  const h16_t *q; long ldq;   // [T, NH*HD] rows of the batch-major token index t = b*S + s
+  const h16_t *k; long ldk;   // [T, NKV*HD]
+  const h16_t *v; long ldv;   // [T, NKV*HD]
+  h16_t *o; long ldo;         // [T, NH*HD]
+  float *lse;                 // [T, NH] natural-log sum exp of scaled scores
   // backward
-  const bf16_t *dout; long lddo;  // [T, NH*HD]
-  const float *delta;             // [T, NH] rowsum(dO * O)
-  float *dq; long lddq;           // [T, NH*HD] fp32
-  float *dk; long lddk;           // [T, NKV*HD] fp32
-  bf16_t *dv; long lddv;          // [T, NKV*HD] bf16
+  const h16_t *dout; long lddo;  // [T, NH*HD]
+  float *delta;                  // [T, NH] rowsum(dO * O) (scratch)
+  float *dq; long lddq;          // [T, NH*HD] fp32
+  float *dk; long lddk;          // [T, NKV*HD] fp32
+  h16_t *dv; long lddv;          // [T, NKV*HD] 16-bit
+  int *ovf;
   int B, S, NH, NKV, HD;
   float scale;
 };
-int launch_attn_fwd(const AttnArgs &a, hipStream_t s);
-int launch_attn_bwd(const AttnArgs &a, hipStream_t s);
+int launch_attn_fwd(int dt, const AttnArgs &a, hipStream_t s);
+int launch_attn_bwd(int dt, const AttnArgs &a, hipStream_t s);
 
-// ---- cross-entropy reduction (k_ce.hip) ----
+// ---- cross-entropy (k_ce.hip over the EPI_CE_* GEMM epilogues) ----
 int launch_ce_reduce(const float *part, int n_tiles, const float *tgt_logit, float *lse,
                      float *loss_rows, float *loss, int T, hipStream_t s);
+int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
+               float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+               hipStream_t s);
+int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse,
+                int T, int D, int V, float scale, void *dlogits, int *ovf, hipStream_t s);
 
 // ---- optimizer (k_optim.hip) ----
 struct AdamArgs {
   float *p, *g, *m, *v;
-  bf16_t *pb;           // bf16 shadow of p (may be null)
+  h16_t *pb;            // 16-bit shadow of p (may be null)
   long n, n_decay;      // elements [0, n_decay) get weight decay
   float lr, b1, b2, eps, wd, bc1, bc2;
   const float *gscale;  // device scalar: grad_scale * clip factor
+  const int *skip;      // device flag: when set, leave p/m/v untouched (overflowed step)
   int zero_grad;        // write g = 0 after the update
 };
 int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s);
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
                          float *gscale_out, float *gnorm_out, hipStream_t s);
-int launch_adam(const AdamArgs &a, hipStream_t s);
-int launch_f32_to_bf16(const float *src, bf16_t *dst, long n, hipStream_t s);
+int launch_adam(int dt, const AdamArgs &a, hipStream_t s);
+int launch_f32_to_h16(int dt, const float *src, h16_t *dst, long n, hipStream_t s);
 int launch_fill_f32(float *dst, float v, long n, hipStream_t s);

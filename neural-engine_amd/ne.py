@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libne.so")
 
 NE_PARAM, NE_GRAD, NE_ADAM_M, NE_ADAM_V = 0, 1, 2, 3
+NE_BF16, NE_FP16 = 0, 1
 PROF_FAMILIES = ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "norm", "ce", "adam", "gnorm",
                  "embed", "decode")
 LAYER_TENSORS = ("Wq", "Wk", "Wv", "Wo", "W1", "W2", "W3", "rms_att", "rms_ffn")
@@ -24,7 +25,8 @@ LAYER_TENSORS = ("Wq", "Wk", "Wv", "Wo", "W1", "W2", "W3", "rms_att", "rms_ffn")
 EXPORTS = (
     "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
     "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_optimizer_step", "ne_zero_grads",
-    "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4", "ne_decode",
+    "ne_grad_scale_info", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
+    "ne_decode",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
@@ -40,7 +42,7 @@ class Config(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("dim", "hidden", "n_heads", "kv_heads", "head_dim",
                                           "n_layers", "vocab", "seq", "batch", "qk_norm")] + \
                [(n, C.c_float) for n in ("rope_theta", "res_alpha", "norm_eps")] + \
-               [(n, C.c_int32) for n in ("decode_batch", "decode_ctx")]
+               [(n, C.c_int32) for n in ("decode_batch", "decode_ctx", "dtype")]
 
 
 class TrainState(C.Structure):
@@ -74,6 +76,7 @@ def lib():
         "ne_train_step": (I, [P, P, F, P]),
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
+        "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
         "ne_get_state": (I, [P, C.POINTER(TrainState)]),
         "ne_set_state": (I, [P, C.POINTER(TrainState)]),
         "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
@@ -82,20 +85,20 @@ def lib():
         "ne_prof_enable": (I, [P, I]),
         "ne_prof_reset": (I, [P]),
         "ne_prof_get": (I, [P, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
-        "ne_k_rmsnorm_fwd": (I, [P, P, P, P, I, I, F, P]),
-        "ne_k_rmsnorm_bwd": (I, [P, P, P, P, P, P, P, F, P, I, I, P]),
-        "ne_k_gemm": (I, [I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
-        "ne_k_qk_prep_fwd": (I, [P, L, P, P, P, P, P, P, P, P, I, I, I, I, I, F, P]),
-        "ne_k_qk_prep_bwd": (I, [P, P, P, L, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
-        "ne_k_attn_fwd": (I, [P, L, P, L, P, L, P, L, P, I, I, I, I, I, F, P]),
-        "ne_k_attn_bwd": (I, [P, L, P, L, P, L, P, L, P, P, L, P, P, L, P, L, P, L, I, I, I, I, I, F, P]),
-        "ne_k_ce_fwd": (I, [P, P, P, I, I, I, P, P, P, P, P, P]),
-        "ne_k_ce_bwd": (I, [P, P, P, P, I, I, I, F, P, P]),
-        "ne_k_adam": (I, [P, P, P, P, P, L, L, F, F, F, F, F, I, P, I, P]),
+        "ne_k_rmsnorm_fwd": (I, [I, P, P, P, P, I, I, F, P]),
+        "ne_k_rmsnorm_bwd": (I, [I, P, P, P, P, P, P, P, F, P, F, I, I, P]),
+        "ne_k_gemm": (I, [I, I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
+        "ne_k_qk_prep_fwd": (I, [I, P, L, P, P, P, P, P, P, P, P, I, I, I, I, I, F, P]),
+        "ne_k_qk_prep_bwd": (I, [I, P, P, P, L, P, P, P, P, P, P, P, P, P, F, I, I, I, I, I, P]),
+        "ne_k_attn_fwd": (I, [I, P, L, P, L, P, L, P, L, P, I, I, I, I, I, F, P]),
+        "ne_k_attn_bwd": (I, [I, P, L, P, L, P, L, P, L, P, P, L, P, P, L, P, L, P, L, I, I, I, I, I, F, P]),
+        "ne_k_ce_fwd": (I, [I, P, P, P, I, I, I, P, P, P, P, P, P]),
+        "ne_k_ce_bwd": (I, [I, P, P, P, P, I, I, I, F, P, P]),
+        "ne_k_adam": (I, [I, P, P, P, P, P, L, L, F, F, F, F, F, I, P, I, P]),
         "ne_k_grad_norm": (I, [P, L, F, F, P, P, P, P]),
         "ne_k_embed_fwd": (I, [P, P, P, I, I, P]),
-        "ne_k_embed_bwd": (I, [P, P, P, I, I, P]),
-        "ne_k_swiglu_fwd": (I, [P, P, I, I, P]),
+        "ne_k_embed_bwd": (I, [P, P, P, F, I, I, P]),
+        "ne_k_swiglu_fwd": (I, [I, P, P, I, I, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(h, name)
@@ -129,9 +132,10 @@ class Model:
 
     def __init__(self, dim, hidden, n_heads, kv_heads, head_dim, n_layers, vocab, seq, batch=1,
                  qk_norm=False, rope_theta=10000.0, res_alpha=1.0, norm_eps=1e-5,
-                 decode_batch=0, decode_ctx=0):
+                 decode_batch=0, decode_ctx=0, dtype=NE_FP16):
         self.cfg = Config(dim, hidden, n_heads, kv_heads, head_dim, n_layers, vocab, seq, batch,
-                          int(bool(qk_norm)), rope_theta, res_alpha, norm_eps, decode_batch, decode_ctx)
+                          int(bool(qk_norm)), rope_theta, res_alpha, norm_eps, decode_batch, decode_ctx,
+                          dtype)
         self._h = lib().ne_create(C.byref(self.cfg))
         if not self._h:
             raise NEError("ne_create failed: " + lib().ne_last_error().decode(errors="replace"))
@@ -140,10 +144,10 @@ class Model:
         assert lib().ne_num_tensors(self._h) == len(self.names)
 
     @classmethod
-    def from_oracle(cls, ocfg, batch=1, decode_batch=0, decode_ctx=0):
+    def from_oracle(cls, ocfg, batch=1, decode_batch=0, decode_ctx=0, dtype=NE_FP16):
         return cls(ocfg.dim, ocfg.hidden, ocfg.n_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.n_layers,
                    ocfg.vocab, ocfg.seq, batch, ocfg.qk_norm, ocfg.rope_theta, ocfg.res_alpha,
-                   ocfg.eps, decode_batch, decode_ctx)
+                   ocfg.eps, decode_batch, decode_ctx, dtype)
 
     def close(self):
         if self._h:
@@ -189,10 +193,18 @@ class Model:
 
     def optimizer_step(self, lr, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_scale=1.0, clip=1.0,
                        want_norm=True):
+        """Returns the pre-clip grad norm (NaN when the step was skipped after an overflow)."""
         gn = C.c_float(0.0)
-        check(lib().ne_optimizer_step(self._h, lr, b1, b2, eps, wd, grad_scale, clip,
-                                      C.byref(gn) if want_norm else None), "optimizer_step")
+        rc = lib().ne_optimizer_step(self._h, lr, b1, b2, eps, wd, grad_scale, clip,
+                                     C.byref(gn) if want_norm else None)
+        if rc not in (0, 1):
+            check(rc, "optimizer_step")
         return float(gn.value) if want_norm else None
+
+    def grad_scale_info(self):
+        sc, sk = C.c_float(0), C.c_int32(0)
+        check(lib().ne_grad_scale_info(self._h, C.byref(sc), C.byref(sk)), "grad_scale_info")
+        return float(sc.value), int(sk.value)
 
     def zero_grads(self):
         check(lib().ne_zero_grads(self._h), "zero_grads")

@@ -14,15 +14,31 @@ def need_gpu():
         pytest.skip("no GPU")
 
 
+# Device tensors created by dev()/zeros() stay referenced until the test ends, so a
+# pointer taken from a temporary (ptr(dev(x)) inside an argument list) is never freed
+# and recycled by torch's caching allocator before the kernel reads it.
+KEEP = []
+
+
 def dev(a, dtype=None):
     t = torch.as_tensor(np.ascontiguousarray(a))
     if dtype is not None:
         t = t.to(dtype)
-    return t.cuda().contiguous()
+    t = t.cuda().contiguous()
+    KEEP.append(t)
+    return t
 
 
 def zeros(shape, dtype=torch.float32):
-    return torch.zeros(shape, dtype=dtype, device="cuda")
+    t = torch.zeros(shape, dtype=dtype, device="cuda")
+    KEEP.append(t)
+    return t
+
+
+@pytest.fixture(autouse=True)
+def _release_device_tensors():
+    yield
+    KEEP.clear()
 
 
 def ptr(t):
@@ -49,3 +65,10 @@ def rel_l2(a, b):
 
 def bf16_round(a):
     return torch.as_tensor(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+# 16-bit formats of the library: (ne dtype id, torch dtype, rounding, unit roundoff)
+FMT = {
+    "fp16": (ne.NE_FP16, torch.float16, lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32), 2.0 ** -11),
+    "bf16": (ne.NE_BF16, torch.bfloat16, bf16_round, 2.0 ** -8),
+}

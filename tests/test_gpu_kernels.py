@@ -1,16 +1,19 @@
 """Kernel-level parity of the HIP kernels through the C-ABI (device pointers) against the
-numpy oracle (oracle/model.py) and float64 numpy restatements of the same op."""
+numpy oracle (oracle/model.py) and float64 numpy restatements of the same op, in both
+16-bit formats.  Tolerances scale with the format's unit roundoff u (fp16 2^-11, bf16 2^-8):
+a single rounding of the output gives rel-L2 ~ u/sqrt(3)."""
 import math
 
 import numpy as np
 import pytest
 
-from gpu_util import bf16_round, call, dev, host, need_gpu, ptr, rel_l2, torch, zeros
+from gpu_util import FMT, _release_device_tensors, call, dev, host, need_gpu, ptr, rel_l2, torch, zeros  # noqa: F401
 import ne
 from oracle import model as om
 
 pytestmark = pytest.mark.gpu
 L = None
+FMTS = ["fp16", "bf16"]
 
 
 @pytest.fixture(autouse=True)
@@ -22,92 +25,98 @@ def _gpu():
 
 # ------------------------------------------------------------------------- GEMM
 
-def _operands(rng, M, N, K, layout):
-    A = bf16_round(rng.standard_normal((M, K)).astype(np.float32))   # logical [M,K]
-    B = bf16_round(rng.standard_normal((K, N)).astype(np.float32))   # logical [K,N]
-    a_store = A if layout in (0, 2) else A.T                          # bit0: A stored [K,M]
-    b_store = B.T if layout in (0, 1) else B                          # bit1: B stored [K,N]
-    lda = a_store.shape[1]
-    ldb = b_store.shape[1]
-    return A, B, dev(a_store, torch.bfloat16), lda, dev(b_store, torch.bfloat16), ldb
+def _operands(rng, M, N, K, layout, fmt):
+    dt, tdt, rnd, _ = FMT[fmt]
+    A = rnd(rng.standard_normal((M, K)).astype(np.float32))   # logical [M,K]
+    B = rnd(rng.standard_normal((K, N)).astype(np.float32))   # logical [K,N]
+    a_store = A if layout in (0, 2) else A.T                  # bit0: A stored [K,M]
+    b_store = B.T if layout in (0, 1) else B                  # bit1: B stored [K,N]
+    return A, B, dev(a_store, tdt), a_store.shape[1], dev(b_store, tdt), b_store.shape[1]
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("layout", [0, 2, 3, 1])
 @pytest.mark.parametrize("shape", [(64, 64, 64), (128, 192, 320), (256, 4096, 1024), (1024, 1024, 256)])
-def test_gemm_f32_layouts(layout, shape):
+def test_gemm_f32_layouts(fmt, layout, shape):
     M, N, K = shape
     rng = np.random.default_rng(M + N + K + layout)
-    A, B, a, lda, b, ldb = _operands(rng, M, N, K, layout)
+    A, B, a, lda, b, ldb = _operands(rng, M, N, K, layout, fmt)
     c = zeros((M, N))
-    call(L.ne_k_gemm, layout, 1, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 0.5, None)
+    call(L.ne_k_gemm, FMT[fmt][0], layout, 1, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 0.5, None)
     ref = 0.5 * (A.astype(np.float64) @ B.astype(np.float64))
     err = np.abs(host(c) - ref).max() / np.abs(ref).max()
     assert err < 1e-5, err
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("epi", [0, 2, 3])
-def test_gemm_epilogues(epi):
+def test_gemm_epilogues(fmt, epi):
     M, N, K = 256, 512, 256
+    dt, tdt, _, u = FMT[fmt]
     rng = np.random.default_rng(epi)
-    A, B, a, lda, b, ldb = _operands(rng, M, N, K, 0)
+    A, B, a, lda, b, ldb = _operands(rng, M, N, K, 0, fmt)
     ref = A.astype(np.float64) @ B.astype(np.float64)
     R = rng.standard_normal((M, N)).astype(np.float32)
     if epi == 0:
-        c = zeros((M, N), torch.bfloat16)
-        call(L.ne_k_gemm, 0, 0, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 1.0, None)
-        assert rel_l2(host(c), ref) < 4e-3
+        c = zeros((M, N), tdt)
+        call(L.ne_k_gemm, dt, 0, 0, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 1.0, None)
+        assert rel_l2(host(c), ref) < u
     elif epi == 2:
         c = dev(R)
-        call(L.ne_k_gemm, 0, 2, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 2.0, None)
+        call(L.ne_k_gemm, dt, 0, 2, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 2.0, None)
         assert rel_l2(host(c), R + 2 * ref) < 1e-6
     else:
         c = zeros((M, N))
         r = dev(R)
-        call(L.ne_k_gemm, 0, 3, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, ptr(r), N, 0.25, None)
+        call(L.ne_k_gemm, dt, 0, 3, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, ptr(r), N, 0.25, None)
         assert rel_l2(host(c), R + 0.25 * ref) < 1e-6
 
 
-def test_gemm_swiglu_backward_epilogue():
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemm_swiglu_backward_epilogue(fmt):
     T, D, H = 128, 256, 320
+    dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(7)
-    dy = bf16_round(rng.standard_normal((T, D)).astype(np.float32))
-    W2 = bf16_round(rng.standard_normal((D, H)).astype(np.float32) * 0.05)
-    h13 = bf16_round(rng.standard_normal((T, 2 * H)).astype(np.float32))
-    dh = zeros((T, 2 * H), torch.bfloat16)
-    call(L.ne_k_gemm, 2, 4, T, H, D, ptr(dev(dy, torch.bfloat16)), D, ptr(dev(W2, torch.bfloat16)), H,
-         ptr(dh), 2 * H, ptr(dev(h13, torch.bfloat16)), 2 * H, 1.0, None)
+    dy = rnd(rng.standard_normal((T, D)).astype(np.float32))
+    W2 = rnd(rng.standard_normal((D, H)).astype(np.float32) * 0.05)
+    h13 = rnd(rng.standard_normal((T, 2 * H)).astype(np.float32))
+    dh = zeros((T, 2 * H), tdt)
+    call(L.ne_k_gemm, dt, 2, 4, T, H, D, ptr(dev(dy, tdt)), D, ptr(dev(W2, tdt)), H, ptr(dh), 2 * H,
+         ptr(dev(h13, tdt)), 2 * H, 1.0, None)
     dgate = dy.astype(np.float64) @ W2
     h1, h3 = h13[:, :H].astype(np.float64), h13[:, H:].astype(np.float64)
     sg = 1 / (1 + np.exp(-h1))
     ref = np.concatenate([dgate * h3 * sg * (1 + h1 * (1 - sg)), dgate * h1 * sg], axis=1)
-    assert rel_l2(host(dh), ref) < 4e-3
+    assert rel_l2(host(dh), ref) < u
 
 
 # --------------------------------------------------------------------- norms, embed
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,D", [(64, 128), (256, 768), (512, 1024)])
-def test_rmsnorm_fwd_bwd(T, D):
+def test_rmsnorm_fwd_bwd(fmt, T, D):
+    dt, tdt, _, u = FMT[fmt]
     rng = np.random.default_rng(T)
     x = rng.standard_normal((T, D)).astype(np.float32) * 3
     g = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
     dy = rng.standard_normal((T, D)).astype(np.float32)
     res = rng.standard_normal((T, D)).astype(np.float32)
     xd, gd = dev(x), dev(g)
-    y = zeros((T, D), torch.bfloat16)
+    y = zeros((T, D), tdt)
     r = zeros((T,))
-    call(L.ne_k_rmsnorm_fwd, ptr(xd), ptr(gd), ptr(y), ptr(r), T, D, 1e-5, None)
+    call(L.ne_k_rmsnorm_fwd, dt, ptr(xd), ptr(gd), ptr(y), ptr(r), T, D, 1e-5, None)
     yr, rr = om.rmsnorm(x, g, 1e-5)
-    assert rel_l2(host(y), yr) < 4e-3
+    assert rel_l2(host(y), yr) < u
     np.testing.assert_allclose(host(r), rr[:, 0], rtol=1e-6)
     dx = zeros((T, D))
-    dxb = zeros((T, D), torch.bfloat16)
+    dxb = zeros((T, D), tdt)
     dg = dev(np.full(D, 0.5, np.float32))
-    call(L.ne_k_rmsnorm_bwd, ptr(dev(dy)), ptr(xd), ptr(gd), ptr(r), ptr(dev(res)), ptr(dx), ptr(dxb), 0.5,
-         ptr(dg), T, D, None)
+    call(L.ne_k_rmsnorm_bwd, dt, ptr(dev(dy)), ptr(xd), ptr(gd), ptr(r), ptr(dev(res)), ptr(dx), ptr(dxb), 0.5,
+         ptr(dg), 0.25, T, D, None)
     dxr, dgr = om.rmsnorm_bwd(dy, x, g, rr)
     assert rel_l2(host(dx), dxr + res) < 1e-5
-    assert rel_l2(host(dxb), 0.5 * (dxr + res)) < 4e-3
-    assert rel_l2(host(dg), dgr + 0.5) < 1e-5
+    assert rel_l2(host(dxb), 0.5 * (dxr + res)) < u
+    assert rel_l2(host(dg), 0.25 * dgr + 0.5) < 1e-5
 
 
 def test_embed_fwd_bwd_with_repeated_ids():
@@ -120,42 +129,46 @@ def test_embed_fwd_bwd_with_repeated_ids():
     np.testing.assert_array_equal(host(x), E[tok])
     dx = rng.standard_normal((T, D)).astype(np.float32)
     gE = zeros((V, D))
-    call(L.ne_k_embed_bwd, ptr(gE), ptr(dev(tok)), ptr(dev(dx)), T, D, None)
+    call(L.ne_k_embed_bwd, ptr(gE), ptr(dev(tok)), ptr(dev(dx)), 0.5, T, D, None)
     ref = np.zeros((V, D))
-    np.add.at(ref, tok, dx.astype(np.float64))
+    np.add.at(ref, tok, 0.5 * dx.astype(np.float64))
     np.testing.assert_allclose(host(gE), ref, rtol=1e-5, atol=1e-5)
 
 
-def test_swiglu_fwd():
+@pytest.mark.parametrize("fmt", FMTS)
+def test_swiglu_fwd(fmt):
     T, H = 64, 192
+    dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(4)
-    h13 = bf16_round(rng.standard_normal((T, 2 * H)).astype(np.float32) * 2)
-    gate = zeros((T, H), torch.bfloat16)
-    call(L.ne_k_swiglu_fwd, ptr(dev(h13, torch.bfloat16)), ptr(gate), T, H, None)
+    h13 = rnd(rng.standard_normal((T, 2 * H)).astype(np.float32) * 2)
+    gate = zeros((T, H), tdt)
+    call(L.ne_k_swiglu_fwd, dt, ptr(dev(h13, tdt)), ptr(gate), T, H, None)
     ref = om.silu(h13[:, :H]) * h13[:, H:]
-    assert rel_l2(host(gate), ref) < 4e-3
+    assert rel_l2(host(gate), ref) < u
 
 
 # -------------------------------------------------------------------- RoPE / QK-norm
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("HD,qk", [(64, False), (128, True), (64, True)])
-def test_qk_prep_fwd_bwd(HD, qk):
+def test_qk_prep_fwd_bwd(fmt, HD, qk):
+    dt, tdt, rnd, u = FMT[fmt]
     B, S, NH, NKV = 2, 64, 4, 2
     T, Q, KV = B * S, NH * HD, NKV * HD
     QKV = Q + 2 * KV
     theta = 1e6 if qk else 1e4
     rng = np.random.default_rng(HD + qk)
-    qkv = bf16_round(rng.standard_normal((T, QKV)).astype(np.float32))
+    qkv = rnd(rng.standard_normal((T, QKV)).astype(np.float32))
     gq = (1 + 0.3 * rng.standard_normal(HD)).astype(np.float32)
     gk = (1 + 0.3 * rng.standard_normal(HD)).astype(np.float32)
     cos, sin = om.rope_tables(S, HD, theta)
     cosd, sind = dev(cos.astype(np.float32)), dev(sin.astype(np.float32))
-    qkvd = dev(qkv, torch.bfloat16)
-    qr, kr = zeros((T, Q), torch.bfloat16), zeros((T, KV), torch.bfloat16)
+    qkvd = dev(qkv, tdt)
+    qr, kr = zeros((T, Q), tdt), zeros((T, KV), tdt)
     rq, rk = zeros((T, NH)), zeros((T, NKV))
     gqd, gkd = (dev(gq), dev(gk)) if qk else (None, None)
-    call(L.ne_k_qk_prep_fwd, ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd), ptr(gkd), ptr(qr), ptr(kr), ptr(rq),
-         ptr(rk), T, S, NH, NKV, HD, 1e-5, None)
+    call(L.ne_k_qk_prep_fwd, dt, ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd), ptr(gkd), ptr(qr), ptr(kr),
+         ptr(rq), ptr(rk), T, S, NH, NKV, HD, 1e-5, None)
     q = qkv[:, :Q].reshape(B, S, NH, HD)
     k = qkv[:, Q:Q + KV].reshape(B, S, NKV, HD)
     if qk:
@@ -164,23 +177,23 @@ def test_qk_prep_fwd_bwd(HD, qk):
         np.testing.assert_allclose(host(rq), rqr.reshape(T, NH), rtol=1e-5)
     qe = om.rope_apply(q, cos, sin).reshape(T, Q)
     ke = om.rope_apply(k, cos, sin).reshape(T, KV)
-    assert rel_l2(host(qr), qe) < 4e-3 and rel_l2(host(kr), ke) < 4e-3
+    assert rel_l2(host(qr), qe) < u and rel_l2(host(kr), ke) < u
     # backward
     dq = rng.standard_normal((T, Q)).astype(np.float32)
     dk = rng.standard_normal((T, KV)).astype(np.float32)
-    dqkv = zeros((T, QKV), torch.bfloat16)
+    dqkv = zeros((T, QKV), tdt)
     dgq, dgk = (zeros((HD,)), zeros((HD,))) if qk else (None, None)
-    call(L.ne_k_qk_prep_bwd, ptr(dev(dq)), ptr(dev(dk)), ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd), ptr(gkd),
-         ptr(rq), ptr(rk), ptr(dqkv), ptr(dgq), ptr(dgk), T, S, NH, NKV, HD, None)
+    call(L.ne_k_qk_prep_bwd, dt, ptr(dev(dq)), ptr(dev(dk)), ptr(qkvd), QKV, ptr(cosd), ptr(sind), ptr(gqd),
+         ptr(gkd), ptr(rq), ptr(rk), ptr(dqkv), ptr(dgq), ptr(dgk), 2.0, T, S, NH, NKV, HD, None)
     dqn = om.rope_bwd(dq.reshape(B, S, NH, HD), cos, sin)
     dkn = om.rope_bwd(dk.reshape(B, S, NKV, HD), cos, sin)
     if qk:
         dqn, dgqr = om.rmsnorm_bwd(dqn, qkv[:, :Q].reshape(B, S, NH, HD), gq, rqr)
         dkn, dgkr = om.rmsnorm_bwd(dkn, qkv[:, Q:Q + KV].reshape(B, S, NKV, HD), gk, rkr)
-        assert rel_l2(host(dgq), dgqr) < 1e-4 and rel_l2(host(dgk), dgkr) < 1e-4
+        assert rel_l2(host(dgq), 2 * dgqr) < 1e-4 and rel_l2(host(dgk), 2 * dgkr) < 1e-4
     got = host(dqkv)
-    assert rel_l2(got[:, :Q], dqn.reshape(T, Q)) < 4e-3
-    assert rel_l2(got[:, Q:Q + KV], dkn.reshape(T, KV)) < 4e-3
+    assert rel_l2(got[:, :Q], dqn.reshape(T, Q)) < u
+    assert rel_l2(got[:, Q:Q + KV], dkn.reshape(T, KV)) < u
 
 
 # ------------------------------------------------------------------------ attention
@@ -214,55 +227,62 @@ def _attn_ref(q, k, v, do, NH, NKV, scale):
     return o, lse, dq, dk, dv
 
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("B,S,NH,NKV,HD", [(1, 64, 2, 2, 64), (2, 128, 4, 2, 64), (1, 256, 4, 2, 128),
                                            (2, 192, 2, 1, 128)])
-def test_flash_attention_fwd_bwd(B, S, NH, NKV, HD):
+def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
+    dt, tdt, rnd, u = FMT[fmt]
     T = B * S
     rng = np.random.default_rng(S + HD)
-    # q/k/v as slices of wider rows (strided like the model's qkv buffer)
-    q = bf16_round(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
-    k = bf16_round(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
-    v = bf16_round(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
-    do = bf16_round(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    q = rnd(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    k = rnd(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    v = rnd(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    do = rnd(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
     scale = 1.0 / math.sqrt(HD)
+    # q/k/v as column blocks of one wide row (strided like the model's qkv buffer)
     ld = NH * HD + 2 * NKV * HD
     qkv = np.concatenate([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], axis=1)
-    qkvd = dev(qkv, torch.bfloat16)
+    qkvd = dev(qkv, tdt)
     qd = qkvd[:, :NH * HD]
     kd = qkvd[:, NH * HD:NH * HD + NKV * HD]
     vd = qkvd[:, NH * HD + NKV * HD:]
-    o = zeros((T, NH * HD), torch.bfloat16)
+    o = zeros((T, NH * HD), tdt)
     lse = zeros((T, NH))
-    call(L.ne_k_attn_fwd, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse), B, S, NH, NKV, HD,
+    call(L.ne_k_attn_fwd, dt, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse), B, S, NH, NKV, HD,
          scale, None)
     o_r, lse_r, dq_r, dk_r, dv_r = _attn_ref(q, k, v, do, NH, NKV, scale)
-    assert rel_l2(host(o), o_r.reshape(T, -1)) < 8e-3
     np.testing.assert_allclose(host(lse), lse_r.reshape(T, NH), rtol=1e-4, atol=1e-4)
     delta = zeros((T, NH))
     dq, dk = zeros((T, NH * HD)), zeros((T, NKV * HD))
-    dqkv = zeros((T, ld), torch.bfloat16)
+    dqkv = zeros((T, ld), tdt)
     dv = dqkv[:, NH * HD + NKV * HD:]
-    call(L.ne_k_attn_bwd, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse), ptr(dev(do, torch.bfloat16)),
-         NH * HD, ptr(delta), ptr(dq), NH * HD, ptr(dk), NKV * HD, ptr(dv), ld, B, S, NH, NKV, HD, scale, None)
-    assert rel_l2(host(dq), dq_r.reshape(T, -1)) < 2e-2
-    assert rel_l2(host(dk), dk_r.reshape(T, -1)) < 2e-2
-    assert rel_l2(host(dqkv)[:, NH * HD + NKV * HD:], dv_r.reshape(T, -1)) < 2e-2
+    call(L.ne_k_attn_bwd, dt, ptr(qd), ld, ptr(kd), ld, ptr(vd), ld, ptr(o), NH * HD, ptr(lse),
+         ptr(dev(do, tdt)), NH * HD, ptr(delta), ptr(dq), NH * HD, ptr(dk), NKV * HD, ptr(dv), ld, B, S, NH, NKV, HD,
+         scale, None)
+    e = (rel_l2(host(o), o_r.reshape(T, -1)), rel_l2(host(dq), dq_r.reshape(T, -1)),
+         rel_l2(host(dk), dk_r.reshape(T, -1)), rel_l2(host(dqkv)[:, NH * HD + NKV * HD:], dv_r.reshape(T, -1)))
+    print(f"\n  {fmt} rel-L2 o={e[0]:.2e} dq={e[1]:.2e} dk={e[2]:.2e} dv={e[3]:.2e}")
+    # P and dS are rounded to the 16-bit format for the MFMAs: a few roundings deep
+    assert max(e) < 4 * u
     # q and k columns of dqkv untouched
     assert np.abs(host(dqkv)[:, :NH * HD + NKV * HD]).max() == 0
 
 
 # --------------------------------------------------------------- cross-entropy (LM head)
 
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000)])
-def test_fused_ce_fwd_bwd(T, D, V):
+def test_fused_ce_fwd_bwd(fmt, T, D, V):
+    dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(V)
-    x = bf16_round(rng.standard_normal((T, D)).astype(np.float32))
-    E = bf16_round(rng.standard_normal((V, D)).astype(np.float32) * 0.05)
+    x = rnd(rng.standard_normal((T, D)).astype(np.float32))
+    E = rnd(rng.standard_normal((V, D)).astype(np.float32) * 0.05)
     tgt = rng.integers(0, V, T).astype(np.int32)
-    xd, Ed, td = dev(x, torch.bfloat16), dev(E, torch.bfloat16), dev(tgt)
+    xd, Ed, td = dev(x, tdt), dev(E, tdt), dev(tgt)
     part = zeros((T * (V // 64) * 2,))
     tl, lse, rows, loss = zeros((T,)), zeros((T,)), zeros((T,)), zeros((4,))
-    call(L.ne_k_ce_fwd, ptr(xd), ptr(Ed), ptr(td), T, D, V, ptr(part), ptr(tl), ptr(lse), ptr(rows), ptr(loss), None)
+    call(L.ne_k_ce_fwd, dt, ptr(xd), ptr(Ed), ptr(td), T, D, V, ptr(part), ptr(tl), ptr(lse), ptr(rows), ptr(loss),
+         None)
     logits = x.astype(np.float64) @ E.T.astype(np.float64)
     m = logits.max(1, keepdims=True)
     lse_r = (m + np.log(np.exp(logits - m).sum(1, keepdims=True)))[:, 0]
@@ -270,17 +290,20 @@ def test_fused_ce_fwd_bwd(T, D, V):
     loss_r = np.mean(-np.log(p_t + 1e-10))
     np.testing.assert_allclose(host(lse), lse_r, rtol=1e-5)
     assert abs(host(loss)[0] - loss_r) < 1e-4 * abs(loss_r)
-    dl = zeros((T, V), torch.bfloat16)
-    call(L.ne_k_ce_bwd, ptr(xd), ptr(Ed), ptr(td), ptr(lse), T, D, V, 256.0 / T, ptr(dl), None)
+    dl = zeros((T, V), tdt)
+    scale = 1024.0
+    call(L.ne_k_ce_bwd, dt, ptr(xd), ptr(Ed), ptr(td), ptr(lse), T, D, V, scale, ptr(dl), None)
     ref = np.exp(logits - lse_r[:, None])
     ref[np.arange(T), tgt] -= 1
-    ref *= 256.0 / T
-    assert rel_l2(host(dl), ref) < 4e-3
+    ref *= scale
+    assert rel_l2(host(dl), ref) < u
 
 
 # ------------------------------------------------------------------------ optimizer
 
-def test_adam_matches_oracle_and_grad_norm():
+@pytest.mark.parametrize("fmt", FMTS)
+def test_adam_matches_oracle_and_grad_norm(fmt):
+    dt, tdt, rnd, _ = FMT[fmt]
     n, n_decay = 4096 * 3, 4096 * 2
     rng = np.random.default_rng(11)
     p = rng.standard_normal(n).astype(np.float32) * 0.02
@@ -288,7 +311,7 @@ def test_adam_matches_oracle_and_grad_norm():
     m = rng.standard_normal(n).astype(np.float32) * 1e-3
     v = np.abs(rng.standard_normal(n).astype(np.float32)) * 1e-5
     pd, gd, md, vd = dev(p), dev(g), dev(m), dev(v)
-    pb = zeros((n,), torch.bfloat16)
+    pb = zeros((n,), tdt)
     part = zeros((1024,), torch.float64)
     gs, gn = zeros((1,)), zeros((1,))
     call(L.ne_k_grad_norm, ptr(gd), n, 0.5, 1.0, ptr(part), ptr(gs), ptr(gn), None)
@@ -297,14 +320,16 @@ def test_adam_matches_oracle_and_grad_norm():
     scale = 0.5 * min(1.0, 1.0 / norm)
     assert abs(host(gs)[0] - scale) < 1e-6 * scale
     t = 7
-    call(L.ne_k_adam, ptr(pd), ptr(gd), ptr(md), ptr(vd), ptr(pb), n, n_decay, 3e-4, 0.9, 0.95, 1e-8, 0.1, t,
+    call(L.ne_k_adam, dt, ptr(pd), ptr(gd), ptr(md), ptr(vd), ptr(pb), n, n_decay, 3e-4, 0.9, 0.95, 1e-8, 0.1, t,
          ptr(gs), 1, None)
     pr, mr, vr = p.copy(), m.copy(), v.copy()
     ge = g * np.float32(host(gs)[0])
     om.adam_update(pr[:n_decay], ge[:n_decay], mr[:n_decay], vr[:n_decay], t, 3e-4, 0.9, 0.95, 1e-8, 0.1)
     om.adam_update(pr[n_decay:], ge[n_decay:], mr[n_decay:], vr[n_decay:], t, 3e-4, 0.9, 0.95, 1e-8, 0.0)
-    np.testing.assert_allclose(host(pd), pr, rtol=1e-5, atol=1e-9)
-    np.testing.assert_allclose(host(md), mr, rtol=1e-5, atol=1e-12)
-    np.testing.assert_allclose(host(vd), vr, rtol=1e-5, atol=1e-14)
+    # per element within 1e-5 relative, with an absolute floor of ~one fp32 ulp of the
+    # tensor's scale (terms that cancel in m = b1*m + (1-b1)*g leave ulp-level residue)
+    np.testing.assert_allclose(host(pd), pr, rtol=1e-5, atol=1e-7 * np.abs(pr).max())
+    np.testing.assert_allclose(host(md), mr, rtol=1e-5, atol=1e-7 * np.abs(mr).max())
+    np.testing.assert_allclose(host(vd), vr, rtol=1e-5, atol=1e-7 * np.abs(vr).max())
     assert np.abs(host(gd)).max() == 0
-    np.testing.assert_allclose(host(pb), bf16_round(host(pd)), rtol=0, atol=0)
+    np.testing.assert_array_equal(host(pb), rnd(host(pd)))

@@ -48,8 +48,9 @@ def test_train_step_matches_oracle(case):
     lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
     Go = om.backward(cfg, P, cache)
     assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
-    worst = max((rel_l2(G[n], Go[n]), n) for n in P)
-    print(f"  loss gpu={loss:.6f} oracle={lo:.6f}; worst grad rel-L2 {worst[0]:.2e} ({worst[1]})")
+    errs = sorted(((rel_l2(G[n], Go[n]), n) for n in P), reverse=True)
+    print(f"  loss gpu={loss:.6f} oracle={lo:.6f}; worst grad rel-L2: "
+          + ", ".join(f"{n}={e:.2e}" for e, n in errs[:6]))
     for n in P:
         assert rel_l2(G[n], Go[n]) <= GRAD_RL2, (n, rel_l2(G[n], Go[n]))
     m.close()
@@ -95,26 +96,33 @@ def test_optimizer_step_matches_oracle(clip):
     assert abs(gn - gno) < 1e-5 * gno
     sh = shapes(cfg)
     Pg = m.get_all(sh)
+    # per element within 1e-5 relative; absolute floor = one fp32 ulp at the tensor's scale
     for n in P:
-        np.testing.assert_allclose(Pg[n], Po[n], rtol=ADAM_RTOL, atol=1e-10, err_msg=n)
+        np.testing.assert_allclose(Pg[n], Po[n], rtol=ADAM_RTOL, atol=1e-7 * np.abs(Po[n]).max(), err_msg=n)
     Mg = m.get_all(sh, ne.NE_ADAM_M)
     for n in P:
-        np.testing.assert_allclose(Mg[n], M[n], rtol=ADAM_RTOL, atol=1e-12, err_msg=n)
+        np.testing.assert_allclose(Mg[n], M[n], rtol=ADAM_RTOL, atol=1e-7 * np.abs(M[n]).max(), err_msg=n)
     assert max(np.abs(m.get(n, ne.NE_GRAD)).max() for n in P) == 0
     assert m.state().adam_t == 5
     m.close()
 
 
-def _bf16_params(cfg, seed=0, std=0.02):
-    return {k: om.round_bf16(v) for k, v in om.init_params(cfg, seed=seed, std=std).items()}
+def _held_params(cfg, dtype, seed=0, std=0.02):
+    """Weights rounded to the context's 16-bit format, so the decode's weight shadow and the
+    fp32 oracle see identical values."""
+    P = om.init_params(cfg, seed=seed, std=std)
+    if dtype == ne.NE_BF16:
+        return {k: om.round_bf16(v) for k, v in P.items()}
+    return {k: v.astype(np.float16).astype(np.float32) for k, v in P.items()}
 
 
+@pytest.mark.parametrize("dtype", [ne.NE_BF16, ne.NE_FP16])
 @pytest.mark.parametrize("case", ["ref", "qwen3"])
-def test_decode_greedy_matches_oracle(case):
+def test_decode_greedy_matches_oracle(case, dtype):
     cfg = om.tiny(**CASES[case], vocab=1024)
-    P = _bf16_params(cfg, std=0.05)
+    P = _held_params(cfg, dtype, std=0.05)
     prompt = np.random.default_rng(2).integers(0, cfg.vocab, (3, 8)).astype(np.int32)
-    m = ne.Model.from_oracle(cfg, decode_batch=3, decode_ctx=64)
+    m = ne.Model.from_oracle(cfg, decode_batch=3, decode_ctx=64, dtype=dtype)
     m.set_params(P)
     got = m.decode(prompt, 24)
     want, margins, _ = om.decode(cfg, P, prompt, 24, return_logits=True)
@@ -125,10 +133,10 @@ def test_decode_greedy_matches_oracle(case):
 
 def test_decode_sampling_matches_oracle():
     cfg = om.tiny(**CASES["qwen3"], vocab=1024)
-    P = _bf16_params(cfg, std=0.3)
+    P = _held_params(cfg, ne.NE_BF16, std=0.3)
     prompt = np.random.default_rng(3).integers(0, cfg.vocab, (2, 5)).astype(np.int32)
     u = np.random.RandomState(3).random_sample((2, 16))
-    m = ne.Model.from_oracle(cfg, decode_batch=2, decode_ctx=32)
+    m = ne.Model.from_oracle(cfg, decode_batch=2, decode_ctx=32, dtype=ne.NE_BF16)
     m.set_params(P)
     for temp, top_p in ((0.6, 1.0), (0.8, 0.9)):
         got = m.decode(prompt, 16, temperature=temp, top_p=top_p, uniforms=u)

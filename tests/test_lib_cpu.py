@@ -32,21 +32,26 @@ def test_library_exports_every_header_symbol():
 def test_invalid_config_rejected_without_device():
     cfg = ne.Config(dim=100, hidden=256, n_heads=4, kv_heads=2, head_dim=64, n_layers=1, vocab=512,
                     seq=64, batch=1, qk_norm=0, rope_theta=1e4, res_alpha=1.0, norm_eps=1e-5,
-                    decode_batch=0, decode_ctx=0)
+                    decode_batch=0, decode_ctx=0, dtype=ne.NE_FP16)
     assert not ne.lib().ne_create(ctypes.byref(cfg))
     assert b"multiples of 64" in ne.lib().ne_last_error()
     cfg.dim, cfg.head_dim = 128, 96
     assert not ne.lib().ne_create(ctypes.byref(cfg))
     assert b"head_dim" in ne.lib().ne_last_error()
+    cfg.head_dim, cfg.dtype = 64, 7
+    assert not ne.lib().ne_create(ctypes.byref(cfg))
+    assert b"dtype" in ne.lib().ne_last_error()
 
 
 def test_kernel_entry_points_validate_shapes_before_launch():
     # a GEMM with M not a multiple of 64 must be refused on the host
-    rc = ne.lib().ne_k_gemm(0, 0, 65, 64, 64, None, 64, None, 64, None, 64, None, 0, 1.0, None)
+    rc = ne.lib().ne_k_gemm(1, 0, 0, 65, 64, 64, None, 64, None, 64, None, 64, None, 0, 1.0, None)
     assert rc == -1 and b"multiples of 64" in ne.lib().ne_last_error()
-    rc = ne.lib().ne_k_attn_fwd(None, 64, None, 64, None, 64, None, 64, None, 1, 100, 4, 2, 64, 0.125, None)
+    rc = ne.lib().ne_k_gemm(5, 0, 0, 64, 64, 64, None, 64, None, 64, None, 64, None, 0, 1.0, None)
+    assert rc == -1 and b"16-bit format" in ne.lib().ne_last_error()
+    rc = ne.lib().ne_k_attn_fwd(1, None, 64, None, 64, None, 64, None, 64, None, 1, 100, 4, 2, 64, 0.125, None)
     assert rc == -1 and b"multiple of 64" in ne.lib().ne_last_error()
-    rc = ne.lib().ne_k_adam(None, None, None, None, None, 8, 8, 1e-3, 0.9, 0.95, 1e-8, 0.1, 0, None, 1, None)
+    rc = ne.lib().ne_k_adam(1, None, None, None, None, None, 8, 8, 1e-3, 0.9, 0.95, 1e-8, 0.1, 0, None, 1, None)
     assert rc == -1
 
 
