@@ -114,10 +114,13 @@ int ne_optimizer_step(ne_ctx *ctx, float lr, float b1, float b2, float eps, floa
                       float grad_scale, float clip, float *gnorm_out);
 /* Zero all gradients.  Replaces layer_grads_zero (TD/config.h:164-170). */
 int ne_zero_grads(ne_ctx *ctx);
-/* Internal gradient scale of the 16-bit backward and the number of skipped (overflowed)
- * optimizer steps.  No reference counterpart (the ANE path had a fixed loss scale 256,
- * TD/train.m:180). */
-int ne_grad_scale_info(const ne_ctx *ctx, float *scale, int32_t *skipped_steps);
+/* Internal gradient scale of the 16-bit backward, the number of skipped (overflowed)
+ * optimizer steps and, for the last skipped step, a bit mask of the conversion sites that
+ * overflowed (bit i: 0 norm fwd, 1 qkv, 2 h1|h3, 3 swiglu gate, 4 dlogits, 5 norm bwd,
+ * 6 dh1|dh3, 7 d(attn out), 8 dv, 9 dq|dk).  Any pointer may be NULL.  No reference
+ * counterpart (the ANE path had a fixed loss scale 256, TD/train.m:180). */
+int ne_grad_scale_info(const ne_ctx *ctx, float *scale, int32_t *skipped_steps,
+                       int32_t *overflow_sites);
 int ne_get_state(const ne_ctx *ctx, ne_train_state *st);
 int ne_set_state(ne_ctx *ctx, const ne_train_state *st);
 
@@ -145,12 +148,14 @@ int ne_decode(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float
 
 /* ------------------------------------------------------------- profiling ---- */
 
-/* Per-kernel-family HIP-event timing on the context's stream (off by default). */
+/* Per-kernel-family HIP-event timing on the context's stream (off by default).
+ * ne_prof_enable takes a bit mask of families (1 << NE_PROF_*; 0 disables); only the
+ * selected families get an event pair around their launches. */
 enum {
   NE_PROF_GEMM_FWD = 0, NE_PROF_GEMM_BWD, NE_PROF_ATTN_FWD, NE_PROF_ATTN_BWD, NE_PROF_NORM,
   NE_PROF_CE, NE_PROF_ADAM, NE_PROF_GNORM, NE_PROF_EMBED, NE_PROF_DECODE, NE_PROF_COUNT
 };
-int ne_prof_enable(ne_ctx *ctx, int on);
+int ne_prof_enable(ne_ctx *ctx, int mask);
 int ne_prof_reset(ne_ctx *ctx);
 /* Total milliseconds and launch count of one family since the last reset (synchronises). */
 int ne_prof_get(ne_ctx *ctx, int family, double *ms, int64_t *count);

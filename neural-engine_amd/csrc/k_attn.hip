@@ -49,10 +49,10 @@ __device__ __forceinline__ typename HT::v8 pack_acc(const f32x4 &x, const f32x4 
 
 // Stage a 64-row x HD tile of rows t0.. (column offset col) into LDS row-major
 // (pitch RP) and/or transposed (pitch TP).
-template <int HD, int RP, int TP, bool ROW, bool TRN>
+template <int HD, int RP, int TP, bool ROW, bool TRN, int NT>
 __device__ __forceinline__ void stage_tile(const h16_t *__restrict__ src, long ld, long t0, int col,
                                            h16_t *rows, h16_t *trn) {
-  for (int c = threadIdx.x; c < BLK * HD / 8; c += 256) {
+  for (int c = threadIdx.x; c < BLK * HD / 8; c += NT) {
     const int r = c / (HD / 8), d8 = c % (HD / 8);
     const u16x8 v = *(const u16x8 *)(src + (t0 + r) * ld + col + d8 * 8);
     if (ROW) *(u16x8 *)(rows + r * RP + d8 * 8) = v;
@@ -63,19 +63,20 @@ __device__ __forceinline__ void stage_tile(const h16_t *__restrict__ src, long l
   }
 }
 
-template <typename HT, int HD>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+// NW waves per block, 16 queries per wave; key tiles of 64.
+template <typename HT, int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
   __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
   __shared__ __attribute__((aligned(16))) h16_t Vt[HD * TP];
-  const int nqb = a.S / BLK;
-  const int qb = nqb - 1 - blockIdx.x;  // longest rows first
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
+  const int kb_last = (q0 + NW * 16 - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (a.NH / a.NKV);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int qi = qb * BLK + w * 16 + c16;  // this lane's query (position in sequence)
+  const int qi = q0 + w * 16 + c16;  // this lane's query (position in sequence)
   const long tq = tb + qi;
   typename HT::v8 qf[NK];
 #pragma unroll
@@ -86,10 +87,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   float m_i = -INFINITY, l_i = 0.f;
   const float sl2 = a.scale * LOG2E;
 
-  for (int kb = 0; kb <= qb; kb++) {
+  for (int kb = 0; kb <= kb_last; kb++) {
     __syncthreads();
-    stage_tile<HD, RP, TP, true, false>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, nullptr);
-    stage_tile<HD, RP, TP, false, true>(a.v, a.ldv, tb + kb * BLK, kvh * HD, nullptr, Vt);
+    stage_tile<HD, RP, TP, true, false, NW * 64>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, nullptr);
+    stage_tile<HD, RP, TP, false, true, NW * 64>(a.v, a.ldv, tb + kb * BLK, kvh * HD, nullptr, Vt);
     __syncthreads();
     f32x4 s[4];
 #pragma unroll
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         float v = s[nb][i] * sl2;
-        if (kb == qb && kb * BLK + nb * 16 + g * 4 + i > qi) v = -INFINITY;
+        if (kb == kb_last && kb * BLK + nb * 16 + g * 4 + i > qi) v = -INFINITY;
         s[nb][i] = v;
         mx = fmaxf(mx, v);
       }
@@ -167,8 +168,9 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
   if (row < rows && j == 0) a.delta[row] = s;
 }
 
-template <typename HT, int HD>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+// NW waves per block, 16 keys per wave; query tiles of 64 from the diagonal on.
+template <typename HT, int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
   __shared__ __attribute__((aligned(16))) h16_t Qs[BLK * RP];
   __shared__ __attribute__((aligned(16))) h16_t dOs[BLK * RP];
@@ -176,13 +178,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) h16_t dOt[HD * TP];
   __shared__ float lse_s[BLK], dl_s[BLK];
   const int nqb = a.S / BLK;
-  const int kb = blockIdx.x;  // smallest kb has the most query tiles: launched first
+  const int k0 = blockIdx.x * NW * 16;  // smallest keys have the most query tiles: launched first
+  const int qb_first = k0 / BLK;
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int ratio = a.NH / a.NKV;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int ki = kb * BLK + w * 16 + c16;  // this lane's key (as MFMA column)
+  const int ki = k0 + w * 16 + c16;  // this lane's key (as MFMA column)
   const long tk = tb + ki;
   typename HT::v8 kf[NK], vf[NK];
 #pragma unroll
@@ -197,10 +200,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
 
   for (int hq = 0; hq < ratio; hq++) {
     const int h = kvh * ratio + hq;
-    for (int qb = kb; qb < nqb; qb++) {
+    for (int qb = qb_first; qb < nqb; qb++) {
       __syncthreads();
-      stage_tile<HD, RP, TP, true, true>(a.q, a.ldq, tb + qb * BLK, h * HD, Qs, Qt);
-      stage_tile<HD, RP, TP, true, true>(a.dout, a.lddo, tb + qb * BLK, h * HD, dOs, dOt);
+      stage_tile<HD, RP, TP, true, true, NW * 64>(a.q, a.ldq, tb + qb * BLK, h * HD, Qs, Qt);
+      stage_tile<HD, RP, TP, true, true, NW * 64>(a.dout, a.lddo, tb + qb * BLK, h * HD, dOs, dOt);
       if (threadIdx.x < BLK) {
         const long t = tb + qb * BLK + threadIdx.x;
         lse_s[threadIdx.x] = a.lse[t * a.NH + h] * LOG2E;
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         for (int i = 0; i < 4; i++) {
           const int ql = mb * 16 + g * 4 + i;
           float p = exp2f(sp[mb][i] * sl2 - lse_s[ql]);
-          if (qb == kb && ki > qb * BLK + ql) p = 0.f;
+          if (qb == qb_first && ki > qb * BLK + ql) p = 0.f;
           sp[mb][i] = p;
           dp[mb][i] = p * (dp[mb][i] - dl_s[ql]);
         }
@@ -258,20 +261,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   flag_overflow(a.ovf, bad);
 }
 
-template <typename HT, int HD>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
+// NW waves per block, 16 queries per wave; key tiles of 64 up to the diagonal.
+template <typename HT, int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
   __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
   __shared__ __attribute__((aligned(16))) h16_t Vs[BLK * RP];
   __shared__ __attribute__((aligned(16))) h16_t Kt[HD * TP];
-  const int nqb = a.S / BLK;
-  const int qb = nqb - 1 - blockIdx.x;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
+  const int kb_last = (q0 + NW * 16 - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (a.NH / a.NKV);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int qi = qb * BLK + w * 16 + c16;
+  const int qi = q0 + w * 16 + c16;
   const long tq = tb + qi;
   typename HT::v8 qf[NK], df[NK];
 #pragma unroll
@@ -286,10 +290,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   for (int d = 0; d < ND; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = a.scale * LOG2E;
 
-  for (int kb = 0; kb <= qb; kb++) {
+  for (int kb = 0; kb <= kb_last; kb++) {
     __syncthreads();
-    stage_tile<HD, RP, TP, true, true>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, Kt);
-    stage_tile<HD, RP, TP, true, false>(a.v, a.ldv, tb + kb * BLK, kvh * HD, Vs, nullptr);
+    stage_tile<HD, RP, TP, true, true, NW * 64>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, Kt);
+    stage_tile<HD, RP, TP, true, false, NW * 64>(a.v, a.ldv, tb + kb * BLK, kvh * HD, Vs, nullptr);
     __syncthreads();
     f32x4 sp[4], dp[4];
 #pragma unroll
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         float p = exp2f(sp[nb][i] * sl2 - lse2);
-        if (kb == qb && kb * BLK + nb * 16 + g * 4 + i > qi) p = 0.f;
+        if (kb == kb_last && kb * BLK + nb * 16 + g * 4 + i > qi) p = 0.f;
         dp[nb][i] = p * (dp[nb][i] - dl);
       }
 #pragma unroll
@@ -336,12 +340,29 @@ int check(const AttnArgs &a) {
 
 namespace {
 
+// One wave per block when 4-wave blocks would leave the chip mostly idle (short sequences).
+bool small_grid(const AttnArgs &a) { return (long)a.B * a.NH * (a.S / BLK) < 512; }
+
+template <typename HT, int HD, int NW>
+int fwd_hd(const AttnArgs &a, hipStream_t s) {
+  dim3 grid(a.S / (16 * NW), a.NH, a.B);
+  hipLaunchKernelGGL((attn_fwd_kernel<HT, HD, NW>), grid, dim3(NW * 64), 0, s, a);
+  return ne_hip_status(hipGetLastError(), "attn_fwd");
+}
+
 template <typename HT>
 int fwd_t(const AttnArgs &a, hipStream_t s) {
-  dim3 grid(a.S / BLK, a.NH, a.B);
-  if (a.HD == 128) hipLaunchKernelGGL((attn_fwd_kernel<HT, 128>), grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((attn_fwd_kernel<HT, 64>), grid, dim3(256), 0, s, a);
-  return ne_hip_status(hipGetLastError(), "attn_fwd");
+  const bool sm = small_grid(a);
+  if (a.HD == 128) return sm ? fwd_hd<HT, 128, 1>(a, s) : fwd_hd<HT, 128, 4>(a, s);
+  return sm ? fwd_hd<HT, 64, 1>(a, s) : fwd_hd<HT, 64, 4>(a, s);
+}
+
+template <typename HT, int HD, int NW>
+int bwd_hd(const AttnArgs &a, hipStream_t s) {
+  dim3 gkv(a.S / (16 * NW), a.NKV, a.B), gq(a.S / (16 * NW), a.NH, a.B);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW>), gkv, dim3(NW * 64), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, HD, NW>), gq, dim3(NW * 64), 0, s, a);
+  return ne_hip_status(hipGetLastError(), "attn_bwd");
 }
 
 template <typename HT>
@@ -351,15 +372,9 @@ int bwd_t(const AttnArgs &a, hipStream_t s) {
   if (a.HD == 128) hipLaunchKernelGGL((attn_delta_kernel<HT, 128>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   else hipLaunchKernelGGL((attn_delta_kernel<HT, 64>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   NE_HIP(hipGetLastError());
-  dim3 gkv(a.S / BLK, a.NKV, a.B), gq(a.S / BLK, a.NH, a.B);
-  if (a.HD == 128) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, 128>), gkv, dim3(256), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, 128>), gq, dim3(256), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, 64>), gkv, dim3(256), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, 64>), gq, dim3(256), 0, s, a);
-  }
-  return ne_hip_status(hipGetLastError(), "attn_bwd");
+  const bool sm = small_grid(a);
+  if (a.HD == 128) return sm ? bwd_hd<HT, 128, 1>(a, s) : bwd_hd<HT, 128, 4>(a, s);
+  return sm ? bwd_hd<HT, 64, 1>(a, s) : bwd_hd<HT, 64, 4>(a, s);
 }
 
 }  // namespace

@@ -1,10 +1,15 @@
-// bf16 MFMA GEMM for gfx950 with LDS-staged tiles and fused epilogues.
+// 16-bit MFMA GEMM for gfx950 with LDS-staged tiles, split-K and fused epilogues.
 //
 // C[M,N] = epi(alpha * sum_k A[m,k] B[k,n]).  Operands are 16-bit (fp16 or bf16) with fp32
-// accumulation on v_mfma_f32_32x32x16_{f16,bf16}.  Each operand may be K-contiguous (activation rows,
-// weight rows [N,K]) or M/N-contiguous (the dY^T and X of a weight-gradient GEMM);
-// both are staged into LDS K-contiguous so every MFMA operand is one 16-byte LDS read.
-// M/N-contiguous tiles are transposed in registers in 4x8 blocks on the way into LDS.
+// accumulation on v_mfma_f32_32x32x16_{f16,bf16}.  Each operand may be K-contiguous
+// (activation rows, weight rows [N,K]) or M/N-contiguous (the dY^T and X of a
+// weight-gradient GEMM); both are staged into LDS K-contiguous so every MFMA operand is
+// one 16-byte LDS read.  M/N-contiguous tiles are transposed in registers in 4x8 blocks on
+// the way into LDS.  Double-buffered LDS, one barrier per K step.
+//
+// Small-M shapes (a 256-token step) leave too few output tiles to fill 256 CUs, so the
+// launcher splits K over grid.z: each split writes its fp32 partial tile to a workspace
+// and an ordered reduction (deterministic) applies the epilogue.
 //
 // Replaces the ANE matmuls of TD/mil_dynamic.h (gen_sdpa_fwd_dynamic QKV/Wo,
 // gen_ffn_fused_dynamic W1/W3/W2, gen_ffn_bwd_full_dynamic, gen_wot_dynamic,
@@ -71,6 +76,39 @@ struct Stage {
 
 __device__ __forceinline__ float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+
+// Final store of one output element v (alpha already applied) for every non-CE epilogue.
+template <typename HT, int EPI>
+__device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, float v, bool &bad) {
+  if constexpr (EPI == EPI_H16) {
+    const h16_t o = HT::h(v);
+    bad |= HT::bad(o);
+    ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
+  } else if constexpr (EPI == EPI_F32) {
+    ((float *)g.C)[(long)row * g.ldc + col] = v;
+  } else if constexpr (EPI == EPI_F32_ACC) {
+    ((float *)g.C)[(long)row * g.ldc + col] += v;
+  } else if constexpr (EPI == EPI_RESID) {
+    ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    const h16_t *h = (const h16_t *)g.R + (long)row * g.ldr;
+    const float h1 = HT::f(h[col]), h3 = HT::f(h[g.N + col]);
+    const float sg = fast_sigmoid(h1);
+    h16_t *d = (h16_t *)g.C + (long)row * g.ldc;
+    const h16_t o1 = HT::h(v * h3 * sg * (1.f + h1 * (1.f - sg)));
+    const h16_t o3 = HT::h(v * h1 * sg);
+    bad |= HT::bad(o1) | HT::bad(o3);
+    d[col] = o1;
+    d[g.N + col] = o3;
+  } else if constexpr (EPI == EPI_CE_BWD) {
+    float p = __expf(v - g.lse[row]);
+    if (col == g.targets[row]) p -= 1.f;
+    const h16_t o = HT::h(p * g.scale);
+    bad |= HT::bad(o);
+    ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
+  }
+}
+
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
   constexpr int PITCH = BK + 8;
@@ -86,6 +124,10 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const h16_t *A = (const h16_t *)g.A;
   const h16_t *B = (const h16_t *)g.B;
+  // K steps of this split: [kt0, kt1)
+  const int nkt = g.K / BK;
+  const int kt0 = (int)((long)nkt * blockIdx.z / g.split);
+  const int kt1 = (int)((long)nkt * (blockIdx.z + 1) / g.split);
 
   Stage<BM, BK, AKC> sa;
   Stage<BN, BK, BKC> sb;
@@ -97,16 +139,15 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  const int nk = g.K / BK;
-  sa.load(A, g.lda, m0, 0, tid);
-  sb.load(B, g.ldb, n0, 0, tid);
+  sa.load(A, g.lda, m0, kt0 * BK, tid);
+  sb.load(B, g.ldb, n0, kt0 * BK, tid);
   sa.template store<PITCH>(lds[0], tid);
   sb.template store<PITCH>(lds[0] + BM * PITCH, tid);
   __syncthreads();
 
-  for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
+  for (int kt = kt0; kt < kt1; kt++) {
+    const int cur = (kt - kt0) & 1;
+    if (kt + 1 < kt1) {
       sa.load(A, g.lda, m0, (kt + 1) * BK, tid);
       sb.load(B, g.ldb, n0, (kt + 1) * BK, tid);
     }
@@ -126,7 +167,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = HT::mfma32(a[i], b[j], acc[i][j]);
     }
-    if (kt + 1 < nk) {
+    if (kt + 1 < kt1) {
       sa.template store<PITCH>(lds[cur ^ 1], tid);
       sb.template store<PITCH>(lds[cur ^ 1] + BM * PITCH, tid);
     }
@@ -183,6 +224,22 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
     return;
   }
 
+  if (g.split > 1) {  // fp32 partial tile -> workspace slice blockIdx.z
+    float *ws = g.ws + (long)blockIdx.z * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int col = n0 + wn * TN + j * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          ws[(long)row * g.N + col] = acc[i][j][e];
+        }
+      }
+    return;
+  }
+
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
@@ -192,36 +249,32 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const float v = acc[i][j][e] * alpha;
-        if constexpr (EPI == EPI_H16) {
-          const h16_t o = HT::h(v);
-          bad |= HT::bad(o);
-          ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
-        } else if constexpr (EPI == EPI_F32) {
-          ((float *)g.C)[(long)row * g.ldc + col] = v;
-        } else if constexpr (EPI == EPI_F32_ACC) {
-          ((float *)g.C)[(long)row * g.ldc + col] += v;
-        } else if constexpr (EPI == EPI_RESID) {
-          ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
-        } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-          const h16_t *h = (const h16_t *)g.R + (long)row * g.ldr;
-          const float h1 = HT::f(h[col]), h3 = HT::f(h[g.N + col]);
-          const float sg = fast_sigmoid(h1);
-          h16_t *d = (h16_t *)g.C + (long)row * g.ldc;
-          const h16_t o1 = HT::h(v * h3 * sg * (1.f + h1 * (1.f - sg)));
-          const h16_t o3 = HT::h(v * h1 * sg);
-          bad |= HT::bad(o1) | HT::bad(o3);
-          d[col] = o1;
-          d[g.N + col] = o3;
-        } else if constexpr (EPI == EPI_CE_BWD) {
-          float p = __expf(v - g.lse[row]);
-          if (col == g.targets[row]) p -= 1.f;
-          const h16_t o = HT::h(p * g.scale);
-          bad |= HT::bad(o);
-          ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
-        }
+        store_out<HT, EPI>(g, row, col, acc[i][j][e] * alpha, bad);
       }
     }
+  }
+  flag_overflow(g.ovf, bad);
+}
+
+// Ordered sum of the split-K partials (split 0 first) followed by the epilogue; four
+// consecutive columns per thread.
+template <typename HT, int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
+  const long n4 = (long)g.M * g.N / 4;
+  const long slice = (long)g.M * g.N;
+  bool bad = false;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const long e = i * 4;
+    float4 s = *(const float4 *)(g.ws + e);
+    for (int z = 1; z < g.split; z++) {
+      const float4 p = *(const float4 *)(g.ws + z * slice + e);
+      s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+    }
+    const int row = (int)(e / g.N), col = (int)(e % g.N);
+    store_out<HT, EPI>(g, row, col, s.x * g.alpha, bad);
+    store_out<HT, EPI>(g, row, col + 1, s.y * g.alpha, bad);
+    store_out<HT, EPI>(g, row, col + 2, s.z * g.alpha, bad);
+    store_out<HT, EPI>(g, row, col + 3, s.w * g.alpha, bad);
   }
   flag_overflow(g.ovf, bad);
 }
@@ -233,54 +286,62 @@ namespace {
 template <typename HT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int EPI>
 int launch_t(GemmArgs g, hipStream_t s) {
   g.n_tiles = g.N / BN;
-  dim3 grid(g.N / BN, g.M / BM);
+  dim3 grid(g.N / BN, g.M / BM, g.split);
   hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(NTHREADS), 0, s, g);
-  return ne_hip_status(hipGetLastError(), "gemm launch");
+  NE_HIP(hipGetLastError());
+  if (g.split > 1) {
+    if constexpr (EPI != EPI_CE_FWD) {
+      const long n4 = (long)g.M * g.N / 4;
+      const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
+      hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI>), dim3(blocks), dim3(256), 0, s, g);
+      NE_HIP(hipGetLastError());
+    }
+  }
+  return 0;
 }
 
 template <typename HT, bool AKC, bool BKC, int EPI>
-int launch_e(GemmArgs g, hipStream_t s) {
-  if (gemm_tile_n(g.M, g.N, g.K, EPI) == 128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
+int launch_e(GemmArgs g, int bm, hipStream_t s) {
+  if (bm == 128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
   return launch_t<HT, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
 }
 
 template <typename HT, bool AKC, bool BKC>
-int launch_l(int epi, GemmArgs g, hipStream_t s) {
+int launch_l(int epi, GemmArgs g, int bm, hipStream_t s) {
   switch (epi) {
-    case EPI_H16: return launch_e<HT, AKC, BKC, EPI_H16>(g, s);
-    case EPI_F32: return launch_e<HT, AKC, BKC, EPI_F32>(g, s);
-    case EPI_F32_ACC: return launch_e<HT, AKC, BKC, EPI_F32_ACC>(g, s);
-    case EPI_RESID: return launch_e<HT, AKC, BKC, EPI_RESID>(g, s);
-    case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, s);
-    case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, s);
-    case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, s);
+    case EPI_H16: return launch_e<HT, AKC, BKC, EPI_H16>(g, bm, s);
+    case EPI_F32: return launch_e<HT, AKC, BKC, EPI_F32>(g, bm, s);
+    case EPI_F32_ACC: return launch_e<HT, AKC, BKC, EPI_F32_ACC>(g, bm, s);
+    case EPI_RESID: return launch_e<HT, AKC, BKC, EPI_RESID>(g, bm, s);
+    case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, bm, s);
+    case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, bm, s);
+    case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, bm, s);
   }
   return ne_fail(NE_ERR_ARG, "gemm: unknown epilogue %d", epi);
 }
+
+template <typename HT>
+int launch_dt(int layout, int epi, GemmArgs g, int bm, hipStream_t s) {
+  switch (layout) {
+    case 0: return launch_l<HT, true, true>(epi, g, bm, s);
+    case 1: return launch_l<HT, false, true>(epi, g, bm, s);
+    case 2: return launch_l<HT, true, false>(epi, g, bm, s);
+    case 3: return launch_l<HT, false, false>(epi, g, bm, s);
+  }
+  return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
+}
+
+// Work-groups wanted per GEMM: two per CU on the 256-CU MI355X.
+constexpr long TARGET_WG = 512;
 
 }  // namespace
 
 int gemm_tile_n(int M, int N, int K, int epi) {
   (void)K;
   (void)epi;
-  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= 512) return 128;
+  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= TARGET_WG) return 128;
   return 64;
 }
-
-namespace {
-
-template <typename HT>
-int launch_dt(int layout, int epi, GemmArgs g, hipStream_t s) {
-  switch (layout) {
-    case 0: return launch_l<HT, true, true>(epi, g, s);
-    case 1: return launch_l<HT, false, true>(epi, g, s);
-    case 2: return launch_l<HT, true, false>(epi, g, s);
-    case 3: return launch_l<HT, false, false>(epi, g, s);
-  }
-  return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
-}
-
-}  // namespace
 
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
@@ -288,5 +349,15 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s) {
   if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
     return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
-  return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, s));
+  const int bn = gemm_tile_n(g.M, g.N, g.K, epi);
+  // split K while there are too few output tiles, keeping >= 4 K steps per split
+  g.split = 1;
+  if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD) {
+    const long tiles = (long)(g.M / bn) * (g.N / bn);
+    const int nkt = g.K / 64;
+    while (tiles * g.split < TARGET_WG && nkt / (g.split * 2) >= 4 && g.split < 64 &&
+           (long)g.M * g.N * g.split * 2 <= g.ws_elems)
+      g.split *= 2;
+  }
+  return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, bn, s));
 }

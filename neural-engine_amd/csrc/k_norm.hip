@@ -316,7 +316,8 @@ int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, 
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
                        int D, int *ovf, hipStream_t s) {
   if (D % 4 || D > 2048) return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
-  const int rows = 64;
+  // enough blocks to fill the chip at small T, few enough gain-gradient atomics at large T
+  const int rows = T <= 4096 ? 4 : 32;
   return DISPATCH_H16(dt, [&] {
     hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3((T + rows - 1) / rows), dim3(256), 0, s, dy, x, g, r, resid,
                        dx, dxb, bscale, dg, dg_scale, T, D, rows, ovf);
@@ -352,7 +353,8 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk, float dg_scale,
                        int T, int S, int NH, int NKV, int HD, int *ovf, hipStream_t s) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
-  const int tpb = 256;
+  // enough blocks for small T; few gain-gradient atomics for large T
+  const int tpb = T <= 4096 ? 16 : 128;
   dim3 grid((T + tpb - 1) / tpb, NH + NKV);
   return DISPATCH_H16(dt, [&] {
     if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf);

@@ -8,6 +8,7 @@
 
 struct Prof {
   bool on = false;
+  int mask = 0;  // families with event pairs
   std::vector<hipEvent_t> pool;
   struct Rec { int fam; hipEvent_t a, b; };
   std::vector<Rec> pending;
@@ -25,6 +26,12 @@ struct Prof {
   }
 };
 
+// 16-bit conversion sites with an overflow flag each
+enum {
+  OVF_NORM_FWD = 0, OVF_QKV, OVF_H13, OVF_SWIGLU, OVF_DLOGITS, OVF_NORM_BWD, OVF_DH13, OVF_DATTN,
+  OVF_DV, OVF_DQKV, OVF_COUNT
+};
+
 struct LayerAct {
   float *x_in, *r1, *x2, *r2, *rq, *rk, *lse;
   h16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
@@ -38,7 +45,7 @@ struct ne_ctx {
   ne_config c;
   int D, H, NH, NKV, HD, L, V, S, B, T, Q, KV, QKV;
   int dt;                 // 16-bit format (NE_BF16 / NE_FP16)
-  float gs = 1024.f;      // internal gradient scale: dlogits = (p - onehot) * gs
+  float gs = 256.f;       // internal gradient scale: dlogits = (p - onehot) * gs
   int32_t skipped = 0;    // optimizer steps skipped after a 16-bit overflow
   int good_steps = 0;     // consecutive non-overflowing optimizer steps
   hipStream_t st = nullptr;
@@ -59,9 +66,15 @@ struct ne_ctx {
   float *cosb, *sinb;
   double *gn_part;
   float *gscale, *gnorm;
-  int *ovf;               // device flag: a 16-bit value of this accumulation window overflowed
+  int *ovf;               // device flags [32], one per conversion site (OVF_*): a 16-bit value
+                          // of this accumulation window was not finite
+  int32_t last_ovf_sites = 0;  // bit mask of the sites that flagged the last skipped step
+  bool grads_fresh = true;     // G holds no accumulation yet: the next step overwrites it
+  float *ws = nullptr;         // split-K workspace
+  long ws_elems = 0;
   int32_t *h_tok = nullptr;  // pinned [2T]
   float *h_scalar = nullptr; // pinned [4]
+  int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};
   Prof prof;
   // token loop (k_decode.hip)

@@ -69,13 +69,12 @@ struct Plan {
 };
 
 void prof_begin(ne_ctx *c, int fam, hipEvent_t *e0) {
-  if (!c->prof.on) return;
+  if (!c->prof.on || !(c->prof.mask & (1 << fam))) return;
   *e0 = c->prof.get();
   hipEventRecord(*e0, c->st);
-  (void)fam;
 }
 void prof_end(ne_ctx *c, int fam, hipEvent_t e0) {
-  if (!c->prof.on) return;
+  if (!c->prof.on || !(c->prof.mask & (1 << fam))) return;
   hipEvent_t e1 = c->prof.get();
   hipEventRecord(e1, c->st);
   c->prof.pending.push_back({fam, e0, e1});
@@ -104,14 +103,16 @@ int prof_collect(ne_ctx *c) {
   return 0;
 }
 
-int gemm(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, const void *A, long lda, const void *B,
-         long ldb, void *C, long ldc, const void *R = nullptr, long ldr = 0, float alpha = 1.f) {
+int gemm(ne_ctx *c, int fam, int site, int layout, int epi, int M, int N, int K, const void *A, long lda,
+         const void *B, long ldb, void *C, long ldc, const void *R = nullptr, long ldr = 0, float alpha = 1.f) {
   ProfScope ps(c, fam);
   GemmArgs g = {};
   g.M = M; g.N = N; g.K = K;
   g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.R = R; g.ldr = ldr;
   g.alpha = alpha;
-  g.ovf = c->ovf;
+  g.ovf = site >= 0 ? c->ovf + site : nullptr;
+  g.ws = c->ws;
+  g.ws_elems = c->ws_elems;
   return gemm_launch(c->dt, layout, epi, g, c->st);
 }
 
@@ -231,7 +232,10 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
   pl.add(&c->tok_in, T); pl.add(&c->tok_tgt, T);
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
-  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 4);
+  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
+  // split-K partials: up to 64 MB, enough for a 256-token step's narrow GEMMs
+  c->ws_elems = std::min<long>(16L << 20, std::max<long>(4L << 20, (long)T * D * 16));
+  pl.add(&c->ws, (size_t)c->ws_elems);
 
   int rc = 0;
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
@@ -239,13 +243,14 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.assign((char *)c->arena);
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 2 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_scalar, 4 * sizeof(float), 0), "hipHostMalloc"))) goto fail;
+  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_ovf, 32 * sizeof(int), 0), "hipHostMalloc"))) goto fail;
   // zero weights, gains 1; zero grads and moments
   if ((rc = ne_hip_status(hipMemsetAsync(c->P, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = ne_hip_status(hipMemsetAsync(c->G, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = ne_hip_status(hipMemsetAsync(c->M, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = ne_hip_status(hipMemsetAsync(c->Vm, 0, c->n_params * 4, c->st), "memset"))) goto fail;
   if ((rc = launch_fill_f32(c->P + c->n_decay, 1.f, c->n_params - c->n_decay, c->st))) goto fail;
-  if ((rc = ne_hip_status(hipMemsetAsync(c->ovf, 0, 16, c->st), "memset"))) goto fail;
+  if ((rc = ne_hip_status(hipMemsetAsync(c->ovf, 0, 32 * sizeof(int), c->st), "memset"))) goto fail;
   if ((rc = launch_f32_to_h16(c->dt, c->P, c->Pb, c->n_params, c->st))) goto fail;
   {
     // RoPE tables [S, HD/2]: angle = pos * theta^(-2i/HD), evaluated in double
@@ -282,6 +287,7 @@ extern "C" void ne_destroy(ne_ctx *c) {
   if (c->arena) hipFree(c->arena);
   if (c->h_tok) hipHostFree(c->h_tok);
   if (c->h_scalar) hipHostFree(c->h_scalar);
+  if (c->h_ovf) hipHostFree(c->h_ovf);
   if (c->st) hipStreamDestroy(c->st);
   delete c;
 }
@@ -307,6 +313,10 @@ extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, siz
   if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
   float *base = kind_base(c, kind);
   if (!base) return ne_fail(NE_ERR_ARG, "bad tensor kind %d", kind);
+  if (kind == NE_GRAD && c->grads_fresh) {  // materialise the logical zeros before a partial write
+    NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
+    c->grads_fresh = false;
+  }
   NE_HIP(hipMemcpyAsync(base + c->t_off[id], host, n * 4, hipMemcpyHostToDevice, c->st));
   if (kind == NE_PARAM) NE_CHECK(launch_f32_to_h16(c->dt, c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
@@ -319,6 +329,10 @@ extern "C" int ne_get_tensor(ne_ctx *c, int kind, int id, float *host, size_t n)
   if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
   float *base = kind_base(c, kind);
   if (!base) return ne_fail(NE_ERR_ARG, "bad tensor kind %d", kind);
+  if (kind == NE_GRAD && c->grads_fresh) {  // logically zero since the last update
+    memset(host, 0, n * 4);
+    return 0;
+  }
   NE_HIP(hipMemcpyAsync(host, base + c->t_off[id], n * 4, hipMemcpyDeviceToHost, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   return 0;
@@ -363,7 +377,13 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // reference's loss_scale convention (TD/train.m:180, TD/cpu_ops.h:348-382).
   const int dt = c->dt;
   const float u = loss_scale / (float)T / c->gs;
-  int *ovf = c->ovf;
+  int *ovf = c->ovf;  // + OVF_* site index
+  // The first micro-step after an optimizer step (or zero_grads) writes the weight
+  // gradients instead of accumulating (no zeroing pass, no read of G); only the gains,
+  // which accumulate through atomics, are cleared.
+  const int EPI_DW = c->grads_fresh ? EPI_F32 : EPI_F32_ACC;
+  if (c->grads_fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
+  c->grads_fresh = false;
 
   // ---------------- forward ----------------
   {
@@ -376,9 +396,9 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
     float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf + OVF_NORM_FWD, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_QKV, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
     {
       ProfScope ps(c, NE_PROF_ATTN_FWD);
       NE_CHECK(launch_qk_prep_fwd(dt, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
@@ -388,76 +408,76 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       NE_CHECK(launch_attn_fwd(dt, at, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, D, a.x_in, D, alpha));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, -1, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, D, a.x_in, D, alpha));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf + OVF_NORM_FWD, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_H13, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf, c->st));
+      NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf + OVF_SWIGLU, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, D, a.x2, D, alpha));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, -1, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, D, a.x2, D, alpha));
   }
   {
     ProfScope ps(c, NE_PROF_NORM);
-    NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf, c->st));
+    NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf + OVF_NORM_FWD, c->st));
   }
   {
     ProfScope ps(c, NE_PROF_CE);
     NE_CHECK(ce_forward(dt, c->xf, Pb + c->off_E, c->tok_tgt, T, D, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
                         c->loss, c->st));
-    NE_CHECK(ce_backward(dt, c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, c->gs, c->dlogits, ovf, c->st));
+    NE_CHECK(ce_backward(dt, c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
   }
   if (loss_out) NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
-  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
-  NE_CHECK(gemm(c, NE_PROF_CE, GEMM_TN, EPI_F32_ACC, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
+  NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
+  NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, u, T, D, ovf, c->st));
+                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->st));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
     // FFN: dbf = alpha * dx
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DH13, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
                   a.h13, 2 * H));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H, nullptr, 0, u));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp, D));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D,
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H, nullptr, 0, u));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D,
                   nullptr, 0, u));
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
-                                  T, D, ovf, c->st));
+                                  T, D, ovf + OVF_NORM_BWD, c->st));
     }
     // attention: dbf = alpha * dx2
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q, nullptr, 0, u));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DATTN, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q, nullptr, 0, u));
     {
       ProfScope ps(c, NE_PROF_ATTN_BWD);
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
       at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = c->dqkv + Q + KV; at.lddv = QKV;
-      at.ovf = ovf;
+      at.ovf = ovf + OVF_DV;
       NE_CHECK(launch_attn_bwd(dt, at, c->st));
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
-                                  c->NH, c->NKV, c->HD, ovf, c->st));
+                                  c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, GEMM_TN, EPI_F32_ACC, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
                   0, u));
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att,
-                                  u, T, D, ovf, c->st));
+                                  u, T, D, ovf + OVF_NORM_BWD, c->st));
     }
   }
   {
@@ -473,9 +493,9 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
 
 extern "C" int ne_zero_grads(ne_ctx *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
-  NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
-  NE_HIP(hipMemsetAsync(c->ovf, 0, 4, c->st));
+  NE_HIP(hipMemsetAsync(c->ovf, 0, OVF_COUNT * sizeof(int), c->st));
   NE_HIP(hipStreamSynchronize(c->st));
+  c->grads_fresh = true;
   return 0;
 }
 
@@ -483,13 +503,15 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
                                  float clip, float *gnorm_out) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   // overflow check of the accumulation window (dynamic gradient scaling)
-  NE_HIP(hipMemcpyAsync(c->h_scalar + 2, c->ovf, 4, hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipMemcpyAsync(c->h_ovf, c->ovf, OVF_COUNT * sizeof(int), hipMemcpyDeviceToHost, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
-  int32_t flag;
-  memcpy(&flag, c->h_scalar + 2, 4);
-  if (flag) {
-    NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
-    NE_HIP(hipMemsetAsync(c->ovf, 0, 4, c->st));
+  int32_t sites = 0;
+  for (int i = 0; i < OVF_COUNT; i++)
+    if (c->h_ovf[i]) sites |= 1 << i;
+  if (sites) {
+    c->last_ovf_sites = sites;
+    c->grads_fresh = true;
+    NE_HIP(hipMemsetAsync(c->ovf, 0, OVF_COUNT * sizeof(int), c->st));
     NE_HIP(hipStreamSynchronize(c->st));
     c->gs = c->gs * 0.5f;
     c->skipped += 1;
@@ -510,11 +532,14 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   a.lr = lr; a.b1 = b1; a.b2 = b2; a.eps = eps; a.wd = wd;
   a.bc1 = 1.f - powf(b1, (float)t);
   a.bc2 = 1.f - powf(b2, (float)t);
-  a.gscale = c->gscale; a.zero_grad = 1;
+  a.gscale = c->gscale; a.zero_grad = 0;
+  const bool fresh = c->grads_fresh;  // no micro-step since the last update: all-zero grads
+  if (fresh) NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
   {
     ProfScope ps(c, NE_PROF_ADAM);
     NE_CHECK(launch_adam(c->dt, a, c->st));
   }
+  c->grads_fresh = true;
   c->state.lr = lr;
   // grow the internal scale after a long overflow-free run (bounded)
   if (++c->good_steps >= 1000 && c->gs < 65536.f) {
@@ -529,19 +554,22 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   return 0;
 }
 
-extern "C" int ne_grad_scale_info(const ne_ctx *c, float *scale, int32_t *skipped) {
+extern "C" int ne_grad_scale_info(const ne_ctx *c, float *scale, int32_t *skipped, int32_t *sites) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   if (scale) *scale = c->gs;
   if (skipped) *skipped = c->skipped;
+  if (sites) *sites = c->last_ovf_sites;
   return 0;
 }
 
 // ------------------------------------------------------------------------ profiling ----
 
-extern "C" int ne_prof_enable(ne_ctx *c, int on) {
+extern "C" int ne_prof_enable(ne_ctx *c, int mask) {
+  const int on = mask;
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   NE_CHECK(prof_collect(c));
   c->prof.on = on != 0;
+  c->prof.mask = on;
   return 0;
 }
 

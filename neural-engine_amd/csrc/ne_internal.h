@@ -56,7 +56,10 @@ struct GemmArgs {
   float *part;               // [M, n_tiles, 2] (EPI_CE_FWD): tile max, tile sum exp
   float *tgt_logit;          // [M] (EPI_CE_FWD)
   int *ovf;                  // 16-bit outputs: overflow flag (nullable)
+  float *ws;                 // split-K workspace (nullable: no split)
+  long ws_elems;             // its capacity in floats
   int n_tiles;               // set by the launcher: N / BN
+  int split;                 // set by the launcher: K splits (grid.z)
 };
 
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s);

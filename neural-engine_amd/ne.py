@@ -20,6 +20,7 @@ NE_BF16, NE_FP16 = 0, 1
 PROF_FAMILIES = ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "norm", "ce", "adam", "gnorm",
                  "embed", "decode")
 LAYER_TENSORS = ("Wq", "Wk", "Wv", "Wo", "W1", "W2", "W3", "rms_att", "rms_ffn")
+OVF_SITES = ("norm_fwd", "qkv", "h13", "swiglu", "dlogits", "norm_bwd", "dh13", "dattn", "dv", "dqkv")
 
 # every symbol include/ne.h declares
 EXPORTS = (
@@ -76,7 +77,7 @@ def lib():
         "ne_train_step": (I, [P, P, F, P]),
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
-        "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
+        "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
         "ne_get_state": (I, [P, C.POINTER(TrainState)]),
         "ne_set_state": (I, [P, C.POINTER(TrainState)]),
         "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
@@ -202,9 +203,11 @@ class Model:
         return float(gn.value) if want_norm else None
 
     def grad_scale_info(self):
-        sc, sk = C.c_float(0), C.c_int32(0)
-        check(lib().ne_grad_scale_info(self._h, C.byref(sc), C.byref(sk)), "grad_scale_info")
-        return float(sc.value), int(sk.value)
+        """(internal gradient scale, skipped steps, overflow-site names of the last skip)"""
+        sc, sk, st = C.c_float(0), C.c_int32(0), C.c_int32(0)
+        check(lib().ne_grad_scale_info(self._h, C.byref(sc), C.byref(sk), C.byref(st)), "grad_scale_info")
+        names = [n for i, n in enumerate(OVF_SITES) if st.value >> i & 1]
+        return float(sc.value), int(sk.value), names
 
     def zero_grads(self):
         check(lib().ne_zero_grads(self._h), "zero_grads")
@@ -239,8 +242,12 @@ class Model:
                               _ptr(u) if u is not None else None, _ptr(out)), "decode")
         return out
 
-    def prof_enable(self, on=True):
-        check(lib().ne_prof_enable(self._h, int(on)), "prof_enable")
+    def prof_enable(self, families=PROF_FAMILIES):
+        """Time the given families (names from PROF_FAMILIES) with HIP events; () disables."""
+        mask = 0
+        for f in families:
+            mask |= 1 << PROF_FAMILIES.index(f)
+        check(lib().ne_prof_enable(self._h, mask), "prof_enable")
 
     def prof_reset(self):
         check(lib().ne_prof_reset(self._h), "prof_reset")
