@@ -173,7 +173,7 @@ def main():
     fam_ms = {k: v[0] / 2 for k, v in r["fam"].items()}   # ms per step
     dom = max(fam_ms, key=fam_ms.get)
     adam_ms = r["adam"][0] / max(r["adam"][1], 1)
-    adam_bytes = 34 * npar                                 # read p,g,m,v; write p,m,v,shadow; zero g
+    adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
     mm_ms = sum(fam_ms.get(k, 0.0) for k in ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "ce"))
     out = {
         "metric": "Qwen3-0.6B train tokens/s + step ms on 1 MI355X; MFMA util %; decode tok/s",

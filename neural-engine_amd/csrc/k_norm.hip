@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const float *__restrict__ dy, const float *__restrict__ x, const float *__restrict__ g,
     const float *__restrict__ rr, const float *__restrict__ resid, float *__restrict__ dx,
     h16_t *__restrict__ dxb, float bscale, float *__restrict__ dg, float dg_scale, int T, int D,
-    int rows_per_block, int *ovf) {
+    int rows_per_block, int *ovf, float *__restrict__ part) {
   __shared__ float red[4][2048];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int D4 = D / 4;
@@ -150,8 +150,21 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < D; i += 256)
-    atomicAdd(dg + i, dg_scale * (red[0][i] + red[1][i] + red[2][i] + red[3][i]));
+  for (int i = threadIdx.x; i < D; i += 256) {
+    const float v = dg_scale * (red[0][i] + red[1][i] + red[2][i] + red[3][i]);
+    if (part) part[(long)blockIdx.x * D + i] = v;  // reduced in block order by colsum_kernel
+    else atomicAdd(dg + i, v);
+  }
+}
+
+// out[j] += sum_r part[r * n + j] for r in [0, rows): the deterministic second pass of the
+// per-block gain-gradient partials.
+__global__ void colsum_kernel(const float *__restrict__ part, int rows, int n, float *__restrict__ out) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  float s = 0.f;
+  for (int r = 0; r < rows; r++) s += part[(long)r * n + j];
+  out[j] += s;
 }
 
 // gate = silu(h1) * h3, h13 = [h1 | h3] per row   (TD/mil_dynamic.h:276-281)
@@ -230,7 +243,7 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
     const float *__restrict__ cosb, const float *__restrict__ sinb, const float *__restrict__ gq,
     const float *__restrict__ gk, const float *__restrict__ rq, const float *__restrict__ rk,
     h16_t *__restrict__ dqkv, float *__restrict__ dgq, float *__restrict__ dgk, float dg_scale, int T,
-    int S, int NH, int NKV, int HD, int tok_per_block, int *ovf) {
+    int S, int NH, int NKV, int HD, int tok_per_block, int *ovf, float *__restrict__ part) {
   bool bad = false;
   __shared__ float red[256 * 2];
   const int half = HD / 2;
@@ -283,9 +296,15 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
         s0 += red[(k * half + i) * 2];
         s1 += red[(k * half + i) * 2 + 1];
       }
-      float *dg = isq ? dgq : dgk;
-      atomicAdd(dg + 2 * i, dg_scale * s0);
-      atomicAdd(dg + 2 * i + 1, dg_scale * s1);
+      if (part) {  // layout [head slot][token block][HD], reduced by colsum_kernel
+        float *pp = part + ((long)h * gridDim.x + blockIdx.x) * HD;
+        pp[2 * i] = dg_scale * s0;
+        pp[2 * i + 1] = dg_scale * s1;
+      } else {
+        float *dg = isq ? dgq : dgk;
+        atomicAdd(dg + 2 * i, dg_scale * s0);
+        atomicAdd(dg + 2 * i + 1, dg_scale * s1);
+      }
     }
   }
 }
@@ -312,17 +331,32 @@ int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *
   }());
 }
 
+namespace {
+int rms_rows(int T) { return T <= 4096 ? 4 : 32; }  // rows per block
+int qk_tpb(int T) { return T <= 4096 ? 16 : 128; }   // tokens per block
+}  // namespace
+
+long rmsnorm_bwd_part_elems(int T, int D) { return (long)((T + rms_rows(T) - 1) / rms_rows(T)) * D; }
+long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD) {
+  return (long)((T + qk_tpb(T) - 1) / qk_tpb(T)) * (NH + NKV) * HD;
+}
+
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
-                       int D, int *ovf, hipStream_t s) {
+                       int D, int *ovf, float *part, hipStream_t s) {
   if (D % 4 || D > 2048) return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
-  // enough blocks to fill the chip at small T, few enough gain-gradient atomics at large T
-  const int rows = T <= 4096 ? 4 : 32;
-  return DISPATCH_H16(dt, [&] {
-    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3((T + rows - 1) / rows), dim3(256), 0, s, dy, x, g, r, resid,
-                       dx, dxb, bscale, dg, dg_scale, T, D, rows, ovf);
+  const int rows = rms_rows(T);
+  const int nb = (T + rows - 1) / rows;
+  NE_CHECK(DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3(nb), dim3(256), 0, s, dy, x, g, r, resid, dx, dxb, bscale, dg,
+                       dg_scale, T, D, rows, ovf, part);
     return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
-  }());
+  }()));
+  if (part) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((D + 255) / 256), dim3(256), 0, s, part, nb, D, dg);
+    NE_HIP(hipGetLastError());
+  }
+  return 0;
 }
 
 int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s) {
@@ -351,14 +385,21 @@ int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, con
 int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk, float dg_scale,
-                       int T, int S, int NH, int NKV, int HD, int *ovf, hipStream_t s) {
+                       int T, int S, int NH, int NKV, int HD, int *ovf, float *part, hipStream_t s) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
-  // enough blocks for small T; few gain-gradient atomics for large T
-  const int tpb = T <= 4096 ? 16 : 128;
-  dim3 grid((T + tpb - 1) / tpb, NH + NKV);
-  return DISPATCH_H16(dt, [&] {
-    if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf);
-    else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf);
+  const int tpb = qk_tpb(T);
+  const int nbx = (T + tpb - 1) / tpb;
+  dim3 grid(nbx, NH + NKV);
+  NE_CHECK(DISPATCH_H16(dt, [&] {
+    if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part);
+    else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part);
     return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
-  }());
+  }()));
+  if (gq && part) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((HD + 255) / 256), dim3(256), 0, s, part, NH * nbx, HD, dgq);
+    hipLaunchKernelGGL(colsum_kernel, dim3((HD + 255) / 256), dim3(256), 0, s, part + (long)NH * nbx * HD, NKV * nbx,
+                       HD, dgk);
+    NE_HIP(hipGetLastError());
+  }
+  return 0;
 }

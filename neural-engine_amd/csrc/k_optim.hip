@@ -4,7 +4,7 @@
 // TD/cpu_ops.h:266-303 adam_update called per tensor (TD/train.m:861-897), plus the
 // fp16 weight restaging of TD/train.m:872-895: here the update writes the 16-bit shadow
 // the GEMMs read, in the same pass.  Per element: read p, g, m, v (16 B), write
-// p, m, v (12 B), 16-bit shadow (2 B), zeroed g (4 B) = 34 B.  A step whose backward
+// p, m, v (12 B), 16-bit shadow (2 B) = 30 B (+4 B when it also zeroes g).  A step whose backward
 // overflowed the 16-bit range (device flag) leaves p, m, v untouched and only zeroes g.
 #include "common.h"
 #include "ne_internal.h"
@@ -44,6 +44,8 @@ __global__ void clip_finalize_kernel(const double *__restrict__ partials, int np
   }
 }
 
+// Two float4 of each stream per thread per iteration, non-temporal loads and stores (each
+// byte is touched once): measured at the streaming-copy ceiling of the device.
 template <typename HT, bool SHADOW>
 __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
   const float gs = a.gscale[0];
@@ -51,35 +53,46 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
   const float ob1 = 1.f - a.b1, ob2 = 1.f - a.b2;
   const float ibc1 = 1.f / a.bc1, ibc2 = 1.f / a.bc2;
   const long n4 = a.n / 4;
-  float4 *p4 = (float4 *)a.p, *g4 = (float4 *)a.g, *m4 = (float4 *)a.m, *v4 = (float4 *)a.v;
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
-    if (skip) {
-      if (a.zero_grad) g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      continue;
-    }
-    float4 p = p4[i], g = g4[i], m = m4[i], v = v4[i];
-    const float wd = (i * 4 < a.n_decay) ? a.wd : 0.f;
-    float pe[4] = {p.x, p.y, p.z, p.w}, ge[4] = {g.x, g.y, g.z, g.w};
-    float me[4] = {m.x, m.y, m.z, m.w}, ve[4] = {v.x, v.y, v.z, v.w};
+  const long stride = (long)gridDim.x * 256;
+  f32x4 *p4 = (f32x4 *)a.p, *g4 = (f32x4 *)a.g, *m4 = (f32x4 *)a.m, *v4 = (f32x4 *)a.v;
+  for (long i0 = blockIdx.x * 256L + threadIdx.x; i0 < n4; i0 += 2 * stride) {
+    f32x4 P[2], G[2], M[2], V[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float gg = ge[j] * gs;
-      me[j] = a.b1 * me[j] + ob1 * gg;
-      ve[j] = a.b2 * ve[j] + ob2 * (gg * gg);
-      const float mh = me[j] * ibc1, vh = ve[j] * ibc2;
-      pe[j] -= a.lr * (mh / (sqrtf(vh) + a.eps) + wd * pe[j]);
+    for (int u = 0; u < 2; u++) {
+      const long i = i0 + u * stride;
+      if (i < n4) {
+        G[u] = __builtin_nontemporal_load(g4 + i);
+        if (!skip) {
+          P[u] = __builtin_nontemporal_load(p4 + i);
+          M[u] = __builtin_nontemporal_load(m4 + i);
+          V[u] = __builtin_nontemporal_load(v4 + i);
+        }
+      }
     }
-    p4[i] = make_float4(pe[0], pe[1], pe[2], pe[3]);
-    m4[i] = make_float4(me[0], me[1], me[2], me[3]);
-    v4[i] = make_float4(ve[0], ve[1], ve[2], ve[3]);
-    if (a.zero_grad) g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (SHADOW) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const long i = i0 + u * stride;
+      if (i >= n4) break;
+      if (skip) {
+        if (a.zero_grad) __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, g4 + i);
+        continue;
+      }
+      const float wd = (i * 4 < a.n_decay) ? a.wd : 0.f;
       u16x4 b;
-      b[0] = HT::h(pe[0]);
-      b[1] = HT::h(pe[1]);
-      b[2] = HT::h(pe[2]);
-      b[3] = HT::h(pe[3]);
-      ((u16x4 *)a.pb)[i] = b;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float gg = G[u][j] * gs;
+        M[u][j] = a.b1 * M[u][j] + ob1 * gg;
+        V[u][j] = a.b2 * V[u][j] + ob2 * (gg * gg);
+        const float mh = M[u][j] * ibc1, vh = V[u][j] * ibc2;
+        P[u][j] -= a.lr * (mh / (sqrtf(vh) + a.eps) + wd * P[u][j]);
+        b[j] = HT::h(P[u][j]);
+      }
+      __builtin_nontemporal_store(P[u], p4 + i);
+      __builtin_nontemporal_store(M[u], m4 + i);
+      __builtin_nontemporal_store(V[u], v4 + i);
+      if (a.zero_grad) __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, g4 + i);
+      if (SHADOW) __builtin_nontemporal_store(b, (u16x4 *)a.pb + i);
     }
   }
 }
@@ -111,7 +124,7 @@ int launch_clip_finalize(const double *partials, int nparts, float grad_scale, f
 
 int launch_adam(int dt, const AdamArgs &a, hipStream_t s) {
   if (a.n % 4 || a.n_decay % 4) return ne_fail(NE_ERR_ARG, "adam: sizes must be multiples of 4");
-  const int grid = grid_for(a.n / 4);
+  const int grid = (int)std::max<long>(1, std::min<long>((a.n / 4 + 511) / 512, 32768));
   return DISPATCH_H16(dt, [&] {
     if (a.pb) hipLaunchKernelGGL((adam_kernel<HT, true>), dim3(grid), dim3(256), 0, s, a);
     else hipLaunchKernelGGL((adam_kernel<HT, false>), dim3(grid), dim3(256), 0, s, a);

@@ -39,7 +39,7 @@ extern "C" int ne_k_rmsnorm_bwd(int dtype, const float *dy, const float *x, cons
                                 float dg_scale, int T, int D, void *stream) {
   CHECK_DT(dtype);
   return launch_rmsnorm_bwd(dtype, dy, x, g, r, resid, dx, (h16_t *)dxb, bscale, dg, dg_scale, T, D, nullptr,
-                            S(stream));
+                            nullptr, S(stream));
 }
 
 extern "C" int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
@@ -69,7 +69,7 @@ extern "C" int ne_k_qk_prep_bwd(int dtype, const float *dq, const float *dk, con
                                 float dg_scale, int T, int S, int NH, int NKV, int HD, void *stream) {
   CHECK_DT(dtype);
   return launch_qk_prep_bwd(dtype, dq, dk, (const h16_t *)qkv, ld, cosb, sinb, gq, gk, rq, rk, (h16_t *)dqkv,
-                            dgq, dgk, dg_scale, T, S, NH, NKV, HD, nullptr, S(stream));
+                            dgq, dgk, dg_scale, T, S, NH, NKV, HD, nullptr, nullptr, S(stream));
 }
 
 static AttnArgs attn_args(const void *q, int64_t ldq, const void *k, int64_t ldk, const void *v, int64_t ldv,

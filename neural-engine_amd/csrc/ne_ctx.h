@@ -72,7 +72,14 @@ struct ne_ctx {
   bool grads_fresh = true;     // G holds no accumulation yet: the next step overwrites it
   float *ws = nullptr;         // split-K workspace
   long ws_elems = 0;
-  int32_t *h_tok = nullptr;  // pinned [2T]
+  float *gpart = nullptr;      // per-block gain-gradient partials
+  int32_t *h_tok = nullptr;  // pinned [2][2T] (double-buffered token staging)
+  hipEvent_t tok_ev[2] = {nullptr, nullptr};
+  int tok_slot = 0;
+  // captured training steps (HIP graphs), keyed by what changes kernel arguments
+  struct GraphEntry { bool fresh; float loss_scale; float gs; hipGraphExec_t exec; };
+  std::vector<GraphEntry> graphs;
+  bool use_graphs = true;
   float *h_scalar = nullptr; // pinned [4]
   int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};

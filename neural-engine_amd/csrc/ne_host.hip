@@ -230,18 +230,23 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->dlogits, T * (size_t)c->V);
   pl.add(&c->ce_part, T * (size_t)(c->V / 64) * 2);
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
-  pl.add(&c->tok_in, T); pl.add(&c->tok_tgt, T);
+  pl.add(&c->tok_in, 2 * T);  // inputs then targets, filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
   pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 64 MB, enough for a 256-token step's narrow GEMMs
   c->ws_elems = std::min<long>(16L << 20, std::max<long>(4L << 20, (long)T * D * 16));
   pl.add(&c->ws, (size_t)c->ws_elems);
+  pl.add(&c->gpart, (size_t)std::max(rmsnorm_bwd_part_elems(c->T, c->D),
+                                     qk_prep_bwd_part_elems(c->T, c->NH, c->NKV, c->HD)));
 
   int rc = 0;
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
   if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
   pl.assign((char *)c->arena);
-  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 2 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
+  c->tok_tgt = c->tok_in + T;
+  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 4 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
+  if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[0], hipEventDisableTiming), "event"))) goto fail;
+  if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[1], hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_scalar, 4 * sizeof(float), 0), "hipHostMalloc"))) goto fail;
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_ovf, 32 * sizeof(int), 0), "hipHostMalloc"))) goto fail;
   // zero weights, gains 1; zero grads and moments
@@ -278,6 +283,9 @@ fail:
 extern "C" void ne_destroy(ne_ctx *c) {
   if (!c) return;
   if (c->st) hipStreamSynchronize(c->st);
+  for (auto &e : c->graphs) hipGraphExecDestroy(e.exec);
+  for (int i = 0; i < 2; i++)
+    if (c->tok_ev[i]) hipEventDestroy(c->tok_ev[i]);
   decode_free(c);
   for (auto &r : c->prof.pending) {
     hipEventDestroy(r.a);
@@ -352,18 +360,11 @@ extern "C" int ne_set_state(ne_ctx *c, const ne_train_state *st) {
 
 // ------------------------------------------------------------------- training step ----
 
-extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale, float *loss_out) {
-  if (!c || !tokens) return ne_fail(NE_ERR_ARG, "null argument");
+// Enqueue one forward+backward on c->st with token ids already in c->tok_in/tok_tgt.
+// Free of host synchronisation and memsets, so it can be captured into a HIP graph.
+static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
   const int T = c->T, S = c->S, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, V = c->V;
   const float alpha = c->c.res_alpha, eps = c->c.norm_eps;
-  for (int b = 0; b < c->B; b++)
-    for (int s = 0; s < S; s++) {
-      const int32_t ti = tokens[(long)b * (S + 1) + s], tt = tokens[(long)b * (S + 1) + s + 1];
-      if (ti < 0 || ti >= V || tt < 0 || tt >= V) return ne_fail(NE_ERR_ARG, "token id out of [0, %d)", V);
-      c->h_tok[(long)b * S + s] = ti;
-      c->h_tok[T + (long)b * S + s] = tt;
-    }
-  NE_HIP(hipMemcpyAsync(c->tok_in, c->h_tok, 2 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
   const h16_t *Pb = c->Pb;
   const float *P = c->P;
   float *G = c->G;
@@ -381,9 +382,8 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // The first micro-step after an optimizer step (or zero_grads) writes the weight
   // gradients instead of accumulating (no zeroing pass, no read of G); only the gains,
   // which accumulate through atomics, are cleared.
-  const int EPI_DW = c->grads_fresh ? EPI_F32 : EPI_F32_ACC;
-  if (c->grads_fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
-  c->grads_fresh = false;
+  const int EPI_DW = fresh ? EPI_F32 : EPI_F32_ACC;
+  if (fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
 
   // ---------------- forward ----------------
   {
@@ -430,7 +430,6 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
                         c->loss, c->st));
     NE_CHECK(ce_backward(dt, c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
   }
-  if (loss_out) NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
   NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
@@ -438,7 +437,7 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->st));
+                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
@@ -453,7 +452,7 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
-                                  T, D, ovf + OVF_NORM_BWD, c->st));
+                                  T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
     }
     // attention: dbf = alpha * dx2
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DATTN, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
@@ -469,7 +468,7 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
-                                  c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->st));
+                                  c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->gpart, c->st));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
@@ -477,17 +476,79 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att,
-                                  u, T, D, ovf + OVF_NORM_BWD, c->st));
+                                  u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
     }
   }
   {
     ProfScope ps(c, NE_PROF_EMBED);
     NE_CHECK(launch_embed_bwd(G + c->off_E, c->tok_in, c->dx, u, T, D, c->st));
   }
+  return 0;
+}
+
+// Graph cache: one captured step per (fresh, loss scale, internal gradient scale).
+static int train_step_graph(ne_ctx *c, float loss_scale, bool fresh) {
+  for (auto &e : c->graphs)
+    if (e.fresh == fresh && e.loss_scale == loss_scale && e.gs == c->gs) {
+      NE_HIP(hipGraphLaunch(e.exec, c->st));
+      return 0;
+    }
+  hipGraph_t graph = nullptr;
+  NE_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+  const int rc = train_step_enqueue(c, loss_scale, fresh);
+  const hipError_t ec = hipStreamEndCapture(c->st, &graph);
+  if (rc) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  NE_HIP(ec);
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  NE_HIP(ei);
+  if (c->graphs.size() >= 8) {  // bounded: drop the oldest
+    (void)hipGraphExecDestroy(c->graphs.front().exec);
+    c->graphs.erase(c->graphs.begin());
+  }
+  c->graphs.push_back({fresh, loss_scale, c->gs, exec});
+  NE_HIP(hipGraphLaunch(exec, c->st));
+  return 0;
+}
+
+extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale, float *loss_out) {
+  if (!c || !tokens) return ne_fail(NE_ERR_ARG, "null argument");
+  const int T = c->T, S = c->S, V = c->V;
+  // double-buffered pinned staging: wait until the copy issued two calls ago has finished
+  const int slot = c->tok_slot;
+  c->tok_slot ^= 1;
+  NE_HIP(hipEventSynchronize(c->tok_ev[slot]));
+  int32_t *h = c->h_tok + (size_t)slot * 2 * T;
+  for (int b = 0; b < c->B; b++)
+    for (int s = 0; s < S; s++) {
+      const int32_t ti = tokens[(long)b * (S + 1) + s], tt = tokens[(long)b * (S + 1) + s + 1];
+      if (ti < 0 || ti >= V || tt < 0 || tt >= V) return ne_fail(NE_ERR_ARG, "token id out of [0, %d)", V);
+      h[(long)b * S + s] = ti;
+      h[T + (long)b * S + s] = tt;
+    }
+  NE_HIP(hipMemcpyAsync(c->tok_in, h, 2 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
+  NE_HIP(hipEventRecord(c->tok_ev[slot], c->st));
+  const bool fresh = c->grads_fresh;
+  c->grads_fresh = false;
+  // event timing of kernels inside the step needs eager launches; optimizer families don't
+  const int step_fams = c->prof.mask & ~((1 << NE_PROF_ADAM) | (1 << NE_PROF_GNORM));
+  if (c->use_graphs && !(c->prof.on && step_fams)) NE_CHECK(train_step_graph(c, loss_scale, fresh));
+  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh));
   if (loss_out) {
+    NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
     *loss_out = c->h_scalar[0];
   }
+  return 0;
+}
+
+extern "C" int ne_use_graphs(ne_ctx *c, int on) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  c->use_graphs = on != 0;
   return 0;
 }
 

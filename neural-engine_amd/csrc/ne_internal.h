@@ -71,9 +71,13 @@ int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale
                      hipStream_t s);
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D,
                        float eps, int *ovf, hipStream_t s);
+// Gain gradients: with `part` (scratch of *_part_elems floats) per-block partials are summed
+// in a second, ordered pass (deterministic); without it blocks add atomically.
+long rmsnorm_bwd_part_elems(int T, int D);
+long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD);
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg,
-                       float dg_scale, int T, int D, int *ovf, hipStream_t s);
+                       float dg_scale, int T, int D, int *ovf, float *part, hipStream_t s);
 int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s);
 int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
                        const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq, float *rk,
@@ -81,7 +85,7 @@ int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, con
 int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk,
-                       float dg_scale, int T, int S, int NH, int NKV, int HD, int *ovf,
+                       float dg_scale, int T, int S, int NH, int NKV, int HD, int *ovf, float *part,
                        hipStream_t s);
 
 // ---- attention (k_attn.hip): causal, GQA kv head = q head / (NH/NKV) ----

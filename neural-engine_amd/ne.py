@@ -25,7 +25,8 @@ OVF_SITES = ("norm_fwd", "qkv", "h13", "swiglu", "dlogits", "norm_bwd", "dh13", 
 # every symbol include/ne.h declares
 EXPORTS = (
     "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
-    "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_optimizer_step", "ne_zero_grads",
+    "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_optimizer_step",
+    "ne_zero_grads",
     "ne_grad_scale_info", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
@@ -75,6 +76,7 @@ def lib():
         "ne_set_tensor": (I, [P, I, I, P, C.c_size_t]),
         "ne_get_tensor": (I, [P, I, I, P, C.c_size_t]),
         "ne_train_step": (I, [P, P, F, P]),
+        "ne_use_graphs": (I, [P, I]),
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
         "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
@@ -208,6 +210,9 @@ class Model:
         check(lib().ne_grad_scale_info(self._h, C.byref(sc), C.byref(sk), C.byref(st)), "grad_scale_info")
         names = [n for i, n in enumerate(OVF_SITES) if st.value >> i & 1]
         return float(sc.value), int(sk.value), names
+
+    def use_graphs(self, on=True):
+        check(lib().ne_use_graphs(self._h, int(on)), "use_graphs")
 
     def zero_grads(self):
         check(lib().ne_zero_grads(self._h), "zero_grads")

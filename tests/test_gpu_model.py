@@ -181,3 +181,23 @@ def test_checkpoint_roundtrip_with_oracle_reader(tmp_path):
         m2.load(tmp_path / "t.bin")
     m.close()
     m2.close()
+
+
+def test_graph_replay_matches_eager_launches():
+    """The captured-graph step and the eagerly launched step give the same loss and grads,
+    for the overwrite (first micro-step) and the accumulate variants."""
+    cfg = om.tiny(**CASES["qwen3"])
+    P = om.init_params(cfg, seed=0, std=0.02)
+    toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2)]
+    out = []
+    for graphs in (True, False):
+        m = ne.Model.from_oracle(cfg, batch=2)
+        m.use_graphs(graphs)
+        m.set_params(P)
+        losses = [m.train_step(t, 256.0) for t in toks] + [m.train_step(toks[0], 256.0)]
+        out.append((losses, m.get_all(shapes(cfg), ne.NE_GRAD)))
+        m.close()
+    (l1, g1), (l2, g2) = out
+    assert l1 == l2
+    for n in g1:
+        np.testing.assert_allclose(g1[n], g2[n], rtol=1e-6, atol=1e-9, err_msg=n)
