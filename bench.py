@@ -126,6 +126,17 @@ def run_decode(w, B, n_new=200, prompt_len=32):
     return B * n_new / dt, dt
 
 
+def calib_copy(nbytes=1 << 30):
+    """Three device-to-device copies of nbytes (reads nbytes, writes nbytes each)."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def cpu_baseline(wname, w, n_steps=2):
     """The numpy oracle (fwd + bwd + AdamW) on this host's cores for n_steps full steps."""
     from oracle import model as om
@@ -159,6 +170,9 @@ def main():
     ap.add_argument("--workload", default="qwen3-0.6b-s256-b1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run three plain 1 GiB device copies (a known-size kernel that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -166,6 +180,8 @@ def main():
         sys.exit(2)
     w = WORKLOADS[a.workload]
     T = w["batch"] * w["seq"]
+    if a.calib_copy:
+        calib_copy()
     r = run_train(w, a.steps, a.warmup)
     fl = flops(w)
     npar = n_params(w)

@@ -28,6 +28,46 @@ __global__ void embed_bwd_kernel(float *__restrict__ gE, const int32_t *__restri
   for (int i = lane; i < D; i += 64) atomicAdd(dst + i, scale * src[i]);
 }
 
+// Deterministic form of embed_bwd_kernel: the rows of one token id are chained in token
+// order (nxt[t]: next row with the same id, -1 at the end; first[t]: t is the id's first
+// row), and the wave of the first row sums the chain in that order and adds it to gE once.
+// No atomics, so the result does not depend on scheduling.
+constexpr int EMB_MAXV = 8;  // float4 per lane: D <= 2048
+__global__ __launch_bounds__(256) void embed_bwd_chain_kernel(float *__restrict__ gE, const int32_t *__restrict__ tok,
+                                                              const int32_t *__restrict__ nxt,
+                                                              const int32_t *__restrict__ first,
+                                                              const float *__restrict__ dx, float scale, int T,
+                                                              int D) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T || !first[row]) return;
+  const int D4 = D / 4;
+  float4 acc[EMB_MAXV];
+#pragma unroll
+  for (int j = 0; j < EMB_MAXV; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int t = row; t >= 0; t = nxt[t]) {
+    const float4 *src = (const float4 *)(dx + (long)t * D);
+#pragma unroll
+    for (int j = 0; j < EMB_MAXV; j++) {
+      const int i = lane + 64 * j;
+      if (i < D4) {
+        const float4 v = src[i];
+        acc[j].x += v.x; acc[j].y += v.y; acc[j].z += v.z; acc[j].w += v.w;
+      }
+    }
+  }
+  float4 *dst = (float4 *)(gE + (long)tok[row] * D);
+#pragma unroll
+  for (int j = 0; j < EMB_MAXV; j++) {
+    const int i = lane + 64 * j;
+    if (i < D4) {
+      float4 g = dst[i];
+      g.x += scale * acc[j].x; g.y += scale * acc[j].y; g.z += scale * acc[j].z; g.w += scale * acc[j].w;
+      dst[i] = g;
+    }
+  }
+}
+
 // y = x * r * g, r = (mean(x^2) + eps)^-1/2   (TD/cpu_ops.h:20-60 rmsnorm)
 template <typename HT>
 __global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
@@ -320,6 +360,13 @@ int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D,
 int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D, hipStream_t s) {
   hipLaunchKernelGGL(embed_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, dx, scale, T, D);
   return ne_hip_status(hipGetLastError(), "embed_bwd");
+}
+
+int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, const int32_t *first,
+                           const float *dx, float scale, int T, int D, hipStream_t s) {
+  if (D % 4 || D > 4 * 64 * EMB_MAXV) return ne_fail(NE_ERR_ARG, "embed_bwd: D must be a multiple of 4, <= 2048");
+  hipLaunchKernelGGL(embed_bwd_chain_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, nxt, first, dx, scale, T, D);
+  return ne_hip_status(hipGetLastError(), "embed_bwd_chain");
 }
 
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D, float eps,

@@ -62,7 +62,8 @@ struct ne_ctx {
   float *dx, *dx2, *dtmp, *dq, *dk, *delta;
   h16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
   float *ce_part, *ce_tgt, *ce_lse, *ce_rows, *loss;
-  int32_t *tok_in, *tok_tgt;
+  int32_t *tok_in, *tok_tgt, *tok_nxt, *tok_first;  // [T] each, one staging copy
+  std::vector<int32_t> tok_last;                     // host scratch [V] for the id chains
   float *cosb, *sinb;
   double *gn_part;
   float *gscale, *gnorm;
@@ -73,7 +74,7 @@ struct ne_ctx {
   float *ws = nullptr;         // split-K workspace
   long ws_elems = 0;
   float *gpart = nullptr;      // per-block gain-gradient partials
-  int32_t *h_tok = nullptr;  // pinned [2][2T] (double-buffered token staging)
+  int32_t *h_tok = nullptr;  // pinned [2][4T] (double-buffered token staging)
   hipEvent_t tok_ev[2] = {nullptr, nullptr};
   int tok_slot = 0;
   // captured training steps (HIP graphs), keyed by what changes kernel arguments

@@ -20,10 +20,6 @@
 
 #include "ne_ctx.h"
 
-int ce_forward(const void *x, const void *E, const int32_t *targets, int T, int D, int V, float *part,
-               float *tgt_logit, float *lse, float *loss_rows, float *loss, hipStream_t s);
-int ce_backward(const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D, int V,
-                float scale, void *dlogits, hipStream_t s);
 int decode_run(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temp, float top_p,
                const double *uniforms, int32_t *out);
 int decode_alloc(ne_ctx *ctx);
@@ -230,7 +226,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->dlogits, T * (size_t)c->V);
   pl.add(&c->ce_part, T * (size_t)(c->V / 64) * 2);
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
-  pl.add(&c->tok_in, 2 * T);  // inputs then targets, filled by one copy
+  pl.add(&c->tok_in, 4 * T);  // inputs, targets, id chains: filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
   pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 64 MB, enough for a 256-token step's narrow GEMMs
@@ -244,7 +240,10 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
   pl.assign((char *)c->arena);
   c->tok_tgt = c->tok_in + T;
-  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 4 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
+  c->tok_nxt = c->tok_in + 2 * T;
+  c->tok_first = c->tok_in + 3 * T;
+  c->tok_last.assign(c->V, -1);
+  if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 8 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[0], hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[1], hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_scalar, 4 * sizeof(float), 0), "hipHostMalloc"))) goto fail;
@@ -481,7 +480,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
   }
   {
     ProfScope ps(c, NE_PROF_EMBED);
-    NE_CHECK(launch_embed_bwd(G + c->off_E, c->tok_in, c->dx, u, T, D, c->st));
+    NE_CHECK(launch_embed_bwd_chain(G + c->off_E, c->tok_in, c->tok_nxt, c->tok_first, c->dx, u, T, D, c->st));
   }
   return 0;
 }
@@ -522,7 +521,7 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   const int slot = c->tok_slot;
   c->tok_slot ^= 1;
   NE_HIP(hipEventSynchronize(c->tok_ev[slot]));
-  int32_t *h = c->h_tok + (size_t)slot * 2 * T;
+  int32_t *h = c->h_tok + (size_t)slot * 4 * T;
   for (int b = 0; b < c->B; b++)
     for (int s = 0; s < S; s++) {
       const int32_t ti = tokens[(long)b * (S + 1) + s], tt = tokens[(long)b * (S + 1) + s + 1];
@@ -530,7 +529,17 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
       h[(long)b * S + s] = ti;
       h[T + (long)b * S + s] = tt;
     }
-  NE_HIP(hipMemcpyAsync(c->tok_in, h, 2 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
+  // per-id chains of input rows in token order, for the deterministic embedding scatter
+  int32_t *nxt = h + 2 * T, *first = h + 3 * T;
+  for (int t = 0; t < T; t++) {
+    int32_t &last = c->tok_last[h[t]];
+    first[t] = last < 0;
+    if (last >= 0) nxt[last] = t;
+    nxt[t] = -1;
+    last = t;
+  }
+  for (int t = 0; t < T; t++) c->tok_last[h[t]] = -1;
+  NE_HIP(hipMemcpyAsync(c->tok_in, h, 4 * (size_t)T * 4, hipMemcpyHostToDevice, c->st));
   NE_HIP(hipEventRecord(c->tok_ev[slot], c->st));
   const bool fresh = c->grads_fresh;
   c->grads_fresh = false;

@@ -69,6 +69,9 @@ int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this
 int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, hipStream_t s);
 int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D,
                      hipStream_t s);
+// Deterministic scatter over per-id row chains (nxt / first arrays built on the host).
+int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, const int32_t *first,
+                           const float *dx, float scale, int T, int D, hipStream_t s);
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D,
                        float eps, int *ovf, hipStream_t s);
 // Gain gradients: with `part` (scratch of *_part_elems floats) per-block partials are summed
