@@ -75,9 +75,10 @@ def batches(w, n, seed0=1000):
             for i in range(n)]
 
 
-def run_train(w, steps, warmup):
+def run_train(w, steps, warmup, graphs=True):
     alpha = 1.0 / math.sqrt(2.0 * w["n_layers"])
     m = ne.Model(**w, res_alpha=alpha, dtype=ne.NE_FP16)
+    m.use_graphs(graphs)
     init_weights(m, w)
     toks = batches(w, steps + warmup)
     lr = 3e-4
@@ -170,6 +171,9 @@ def main():
     ap.add_argument("--workload", default="qwen3-0.6b-s256-b1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="launch the step's kernels one by one instead of replaying a captured HIP graph "
+                         "(for tracers that do not follow graph launches)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run three plain 1 GiB device copies (a known-size kernel that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
@@ -182,7 +186,7 @@ def main():
     T = w["batch"] * w["seq"]
     if a.calib_copy:
         calib_copy()
-    r = run_train(w, a.steps, a.warmup)
+    r = run_train(w, a.steps, a.warmup, graphs=not a.no_graphs)
     fl = flops(w)
     npar = n_params(w)
     # dominant family by time share

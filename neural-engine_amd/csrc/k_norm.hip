@@ -198,13 +198,41 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
 }
 
 // out[j] += sum_r part[r * n + j] for r in [0, rows): the deterministic second pass of the
-// per-block gain-gradient partials.
-__global__ void colsum_kernel(const float *__restrict__ part, int rows, int n, float *__restrict__ out) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= n) return;
+// per-block gain-gradient partials.  Block = 64 columns x 16 row groups; row group g sums
+// rows g, g+16, ... in order, then the 16 group sums are added in group order, so the
+// result does not depend on scheduling.  grid.y selects one of two (part, rows, out) sets.
+constexpr int CS_COLS = 64, CS_GROUPS = 16;
+__global__ __launch_bounds__(CS_COLS * CS_GROUPS) void colsum_kernel(const float *__restrict__ part0, int rows0,
+                                                                     float *__restrict__ out0,
+                                                                     const float *__restrict__ part1, int rows1,
+                                                                     float *__restrict__ out1, int n) {
+  __shared__ float red[CS_GROUPS][CS_COLS];
+  const float *part = blockIdx.y ? part1 : part0;
+  const int rows = blockIdx.y ? rows1 : rows0;
+  float *out = blockIdx.y ? out1 : out0;
+  const int c = threadIdx.x % CS_COLS, grp = threadIdx.x / CS_COLS;
+  const int j = blockIdx.x * CS_COLS + c;
   float s = 0.f;
-  for (int r = 0; r < rows; r++) s += part[(long)r * n + j];
-  out[j] += s;
+  if (j < n) {
+    int r = grp;
+    for (; r + 3 * CS_GROUPS < rows; r += 4 * CS_GROUPS) {
+      const float a = part[(long)r * n + j], b = part[(long)(r + CS_GROUPS) * n + j];
+      const float d = part[(long)(r + 2 * CS_GROUPS) * n + j], e = part[(long)(r + 3 * CS_GROUPS) * n + j];
+      s += a;
+      s += b;
+      s += d;
+      s += e;
+    }
+    for (; r < rows; r += CS_GROUPS) s += part[(long)r * n + j];
+  }
+  red[grp][c] = s;
+  __syncthreads();
+  if (grp == 0 && j < n) {
+    float t = red[0][c];
+#pragma unroll
+    for (int g = 1; g < CS_GROUPS; g++) t += red[g][c];
+    out[j] += t;
+  }
 }
 
 // gate = silu(h1) * h3, h13 = [h1 | h3] per row   (TD/mil_dynamic.h:276-281)
@@ -400,7 +428,8 @@ int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, 
     return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
   }()));
   if (part) {
-    hipLaunchKernelGGL(colsum_kernel, dim3((D + 255) / 256), dim3(256), 0, s, part, nb, D, dg);
+    hipLaunchKernelGGL(colsum_kernel, dim3((D + CS_COLS - 1) / CS_COLS, 1), dim3(CS_COLS * CS_GROUPS), 0, s, part, nb,
+                       dg, part, nb, dg, D);
     NE_HIP(hipGetLastError());
   }
   return 0;
@@ -443,9 +472,8 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
     return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
   }()));
   if (gq && part) {
-    hipLaunchKernelGGL(colsum_kernel, dim3((HD + 255) / 256), dim3(256), 0, s, part, NH * nbx, HD, dgq);
-    hipLaunchKernelGGL(colsum_kernel, dim3((HD + 255) / 256), dim3(256), 0, s, part + (long)NH * nbx * HD, NKV * nbx,
-                       HD, dgk);
+    hipLaunchKernelGGL(colsum_kernel, dim3((HD + CS_COLS - 1) / CS_COLS, 2), dim3(CS_COLS * CS_GROUPS), 0, s, part,
+                       NH * nbx, dgq, part + (long)NH * nbx * HD, NKV * nbx, dgk, HD);
     NE_HIP(hipGetLastError());
   }
   return 0;
