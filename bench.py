@@ -114,9 +114,10 @@ def run_train(w, steps, warmup, graphs=True):
     return dict(ms=ms, adam=(adam_ms, adam_n), fam=fam, skipped=skipped, scale=scale, loss=loss, sites=sites)
 
 
-def run_decode(w, B, n_new=200, prompt_len=32):
+def run_decode(w, B, n_new=200, prompt_len=32, graphs=True):
     m = ne.Model(**{**w, "batch": 1, "seq": 64}, res_alpha=1.0, decode_batch=B, decode_ctx=prompt_len + n_new,
                  dtype=ne.NE_BF16)
+    m.use_graphs(graphs)
     init_weights(m, w)
     prompt = np.random.default_rng(2).integers(0, w["vocab"], (B, prompt_len)).astype(np.int32)
     m.decode(prompt[:, :4], 4)                       # warm-up
@@ -225,8 +226,8 @@ def main():
         "loss_last": r["loss"],
     }
     if not a.no_decode and a.workload.startswith("qwen3"):
-        d1, _ = run_decode(w, 1)
-        d32, _ = run_decode(w, 32)
+        d1, _ = run_decode(w, 1, graphs=not a.no_graphs)
+        d32, _ = run_decode(w, 32, graphs=not a.no_graphs)
         out["decode"] = {"tokens_per_s_b1": d1, "tokens_per_s_b32": d32, "prompt": 32, "new_tokens": 200,
                          "weights": "bf16"}
     if not a.no_cpu:

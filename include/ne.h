@@ -102,9 +102,11 @@ int ne_get_tensor(ne_ctx *ctx, int kind, int tensor_id, float *host, size_t n);
  * residual / RoPE / GQA ops, cross_entropy_loss (TD/cpu_ops.h:348-382), the dW sgemms and
  * embed_backward. */
 int ne_train_step(ne_ctx *ctx, const int32_t *tokens, float loss_scale, float *loss_out);
-/* Replay the step from a captured HIP graph (default on; off while profiling is enabled).
- * The graph is captured on first use per (fresh accumulation, loss_scale, internal gradient
- * scale) and replaces the reference's per-kernel ANE dispatch (TD/io.h:190-229). */
+/* Replay the step, and each position of ne_decode, from captured HIP graphs (default on;
+ * the step's graph is off while per-kernel profiling is enabled).  The step's graph is
+ * captured on first use per (fresh accumulation, loss_scale, internal gradient scale), the
+ * decode graphs per (batch size, greedy or sampling); they replace the reference's
+ * per-kernel ANE dispatch (TD/io.h:190-229).  Off: every kernel is launched eagerly. */
 int ne_use_graphs(ne_ctx *ctx, int on);
 
 /* Scale grads by grad_scale, global L2 norm, clip to `clip` (if > 0), AdamW with

@@ -1,15 +1,22 @@
 // KV-cached token loop: the MI355X form of generate() in TD/tools/generate.py:113-228.
 //
-// Per generated position every layer runs: RMSNorm -> fused QKV GEMV -> (QK-norm) RoPE +
-// KV-cache append -> GQA attention over the cache -> Wo GEMV + residual -> RMSNorm ->
-// W1|W3 GEMV -> SwiGLU -> W2 GEMV + residual; then the final norm, the tied LM-head GEMV
-// and greedy / temperature / top-p sampling on device.  Weights are the 16-bit shadow;
-// activations, the KV cache and all accumulation are fp32.
+// Per position every layer runs: RMSNorm -> fused QKV GEMV -> (QK-norm) RoPE + KV-cache
+// append -> GQA attention over the cache -> Wo GEMV + residual -> RMSNorm -> W1|W3 GEMV ->
+// SwiGLU -> W2 GEMV + residual; then the final norm, the tied LM-head GEMV and greedy /
+// temperature / top-p sampling on the device.  Weights are the 16-bit shadow; activations,
+// the KV cache and all accumulation are fp32.
 //
-// The GEMVs run on v_mfma_f32_16x16x4_f32: a wave multiplies 16 weight rows by up to 16
-// (or 32) sequences, each lane loading 8 consecutive 16-bit weights per 32-wide K chunk, so
-// every weight byte is read once per step whatever the batch.  The four waves of a block
-// split K and reduce through LDS (deterministic).
+// Every kernel reads the position from device memory (DecState), so the launch sequence of
+// one position does not depend on it: it is captured once as a HIP graph (one for prompt
+// positions, one for generated positions) and replayed per position.
+//
+// GEMVs are HBM-bound (each weight byte is read once per position whatever the batch):
+//  * batch <= 4: VALU kernel.  The block stages its input rows in LDS (fusing the RMSNorm or
+//    the SwiGLU gate into that prologue), each wave streams 1-4 weight rows with 16-byte
+//    loads (8 weights per lane, two chunks of 512 in flight), wave reductions.  The LM-head
+//    launch also writes per-block (max, first index) partials for greedy argmax.
+//  * batch 5..32: v_mfma_f32_16x16x4_f32, 16 weight rows x 16 sequences per MFMA tile,
+//    K split over the 4 waves of a block and over grid.y (fp32 partials, ordered reduction).
 #include <math.h>
 
 #include "common.h"
@@ -17,74 +24,264 @@
 
 namespace {
 
+struct DecState {
+  int pos;      // position being processed
+  int P;        // prompt length
+  float temp;   // < 1e-6: greedy
+  float top_p;
+};
+
+constexpr int VB = 4;            // largest batch of the VALU GEMV path
+constexpr int BIG_ARGMAX = 256;  // argmax partials per sequence on the MFMA path
+
 struct Dec {
-  int Bp;                 // padded batch (16 or 32)
+  int Bmax;               // decode_batch
+  int Bp;                 // MFMA path: batch padded to 16 or 32
   int ctx;                // max positions
-  float *kc, *vc;         // [L][Bp][NKV][ctx][HD]
-  float *x, *xn, *qkv, *q, *att, *h13, *gate, *logits;  // [Bp, *]
+  float *kc, *vc;         // [L][Bmax][NKV][ctx][HD]
+  float *x, *xn, *qkv, *att, *h13, *logits;  // [Bp, *]
+  float *ws;              // MFMA split-K partials
+  long ws_elems;
+  float *amv;             // argmax partials [Bmax][nblk]
+  int32_t *ami;
+  int lm_nblk;
   int32_t *tok;           // [Bp] current token
   int32_t *out;           // [Bp, ctx] generated tokens
+  int32_t *prompt;        // [Bp, ctx]
   double *unif;           // [Bp, ctx]
   float *cosb, *sinb;     // [ctx, HD/2]
+  DecState *st;
   void *arena;
+  struct Graph { int B; bool greedy; hipGraphExec_t pre, gen; };
+  std::vector<Graph> graphs;
 };
+
+// ------------------------------------------------------------------ GEMV, batch <= 4 ----
+
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2 };
+
+// out[b, n] = alpha * sum_k W[n, k] * in'(b, k) + (resid ? resid[b, n] : 0), rows n of this
+// block = (blockIdx.x * 4 + wave) * RPW + r.  in' = in (PRO_NONE), in / rms(in) * g
+// (PRO_RMSNORM, generate.py:81-84) or silu(h1) * h3 with in = [h1 | h3] rows of 2K
+// (PRO_SWIGLU).  resid may alias out (each element is read, then written, by one lane).
+// AMX: also write the block's (max, first row) of each sequence to amv/ami [b][blockIdx.x].
+// The wave's weights (KC chunks of 512 per row, K <= 512*KC) are loaded before the input
+// prologue, so HBM latency overlaps the prologue.
+template <typename HT, int NB, int RPW, int KC, int PRO, bool AMX>
+__global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict__ W, int K,
+                                                        const float *__restrict__ in, long ldi,
+                                                        const float *__restrict__ g, float eps, float *out, long ldo,
+                                                        const float *resid, float alpha, int B, float *amv,
+                                                        int32_t *ami, int nblk) {
+  extern __shared__ float xs[];  // [NB][K]
+  __shared__ float red[4][NB];
+  __shared__ float bmv[NB][4 * RPW];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const long row0 = ((long)blockIdx.x * 4 + w) * RPW;
+  u16x8 wv[RPW][KC];
+#pragma unroll
+  for (int c = 0; c < KC; c++) {
+    const int k = c * 512 + lane * 8;
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+      if (k < K) wv[r][c] = __builtin_nontemporal_load((const u16x8 *)(W + (row0 + r) * K + k));
+  }
+  for (int b = 0; b < NB; b++) {
+    const float *src = in + (long)b * ldi;
+    for (int k = tid; k < K; k += 256) {
+      float v = 0.f;
+      if (b < B) {
+        if (PRO == PRO_SWIGLU) {
+          const float h1 = src[k], h3 = src[K + k];
+          v = h1 * (1.f / (1.f + expf(-h1))) * h3;
+        } else {
+          v = src[k];
+        }
+      }
+      xs[b * K + k] = v;
+    }
+  }
+  if (PRO == PRO_RMSNORM) {
+    __syncthreads();
+    float ss[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      ss[b] = 0.f;
+      for (int k = tid; k < K; k += 256) ss[b] += xs[b * K + k] * xs[b * K + k];
+      ss[b] = wave_sum(ss[b]);
+    }
+    if (lane == 0)
+#pragma unroll
+      for (int b = 0; b < NB; b++) red[w][b] = ss[b];
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const float rms = sqrtf((red[0][b] + red[1][b] + red[2][b] + red[3][b]) / (float)K + eps);
+      for (int k = tid; k < K; k += 256) xs[b * K + k] = xs[b * K + k] / rms * g[k];
+    }
+  }
+  __syncthreads();
+
+  float acc[RPW][NB];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[r][b] = 0.f;
+#pragma unroll
+  for (int c = 0; c < KC; c++) {
+    const int k = c * 512 + lane * 8;
+    if (k < K) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const float4 x0 = *(const float4 *)(xs + b * K + k), x1 = *(const float4 *)(xs + b * K + k + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc[r][b] = fmaf(HT::f(wv[r][c][j]), xv[j], acc[r][b]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
+  if (lane < RPW * NB) {
+    const int r = lane / NB, b = lane % NB;
+    float v = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++)
+#pragma unroll
+      for (int bb = 0; bb < NB; bb++)
+        if (rr == r && bb == b) v = acc[rr][bb];
+    if (b < B) {
+      const long n = row0 + r;
+      float o = alpha * v;
+      if (resid) o += resid[(long)b * ldo + n];
+      out[(long)b * ldo + n] = o;
+      if (AMX) bmv[b][w * RPW + r] = o;
+    }
+  }
+  if (AMX) {
+    __syncthreads();
+    if (tid < NB && tid < B) {
+      float best = bmv[tid][0];
+      int bi = 0;
+      for (int i = 1; i < 4 * RPW; i++)
+        if (bmv[tid][i] > best) { best = bmv[tid][i]; bi = i; }  // first maximum
+      amv[(long)tid * nblk + blockIdx.x] = best;
+      ami[(long)tid * nblk + blockIdx.x] = (int32_t)(blockIdx.x * 4 * RPW + bi);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ GEMV, batch 5..32 ----
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// out[b, n] = (resid ? resid[b,n] : 0) + alpha * sum_k W[n,k] x[b,k]
-template <typename HT, int NB>
-__global__ __launch_bounds__(256) void gemv_kernel(const h16_t *__restrict__ W, long ldw,
-                                                   const float *__restrict__ x, int K,
-                                                   float *out, long ldo, const float *resid, float alpha) {
-  __shared__ f32x4 red[4][NB][64];
+// Partial (or, with one split, final) products of 16 weight rows (blockIdx.x) over the K
+// range of split blockIdx.y, for NT tiles of 16 sequences.  x rows [Bp, K] fp32, or with
+// SWIGLU rows [Bp, 2K] of [h1 | h3] and x = silu(h1) * h3 formed on the fly.  Each wave
+// loads up to 8 weight chunks ahead of their use.
+template <typename HT, int NT, bool SWIGLU>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(const h16_t *__restrict__ W, long ldw,
+                                                        const float *__restrict__ x, int K, int ksplit,
+                                                        float *out, long ldo, const float *resid, float alpha,
+                                                        float *ws, int N, int B) {
+  __shared__ f32x4 red[4][NT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const long row = (long)blockIdx.x * 16 + r;
-  const int ks = K / 4;
-  const int kbeg = w * ks;
-  f32x4 acc[NB];
+  const int kc = K / ksplit, ks = kc / 4;
+  const int kbeg = blockIdx.y * kc + w * ks, kend = kbeg + ks;
+  const long ldx = SWIGLU ? 2L * K : K;
+  f32x4 acc[NT];
 #pragma unroll
-  for (int nb = 0; nb < NB; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const h16_t *wr = W + row * ldw;
-  for (int k0 = kbeg; k0 < kbeg + ks; k0 += 32) {
-    const u16x8 wv = *(const u16x8 *)(wr + k0 + g * 8);
+  for (int base = kbeg; base < kend; base += 8 * 32) {
+    u16x8 wv[8];
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      const float4 *xr = (const float4 *)(x + (long)(nb * 16 + r) * K + k0 + g * 8);
-      const float4 xa = xr[0], xb = xr[1];
-      const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    for (int i = 0; i < 8; i++)
+      if (base + i * 32 < kend) wv[i] = __builtin_nontemporal_load((const u16x8 *)(wr + base + i * 32 + g * 8));
 #pragma unroll
-      for (int j = 0; j < 8; j++) acc[nb] = mfma_f32(HT::f(wv[j]), xs[j], acc[nb]);
+    for (int i = 0; i < 8; i++) {
+      const int k0 = base + i * 32;
+      if (k0 < kend) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const float *xr = x + (long)(t * 16 + r) * ldx + k0 + g * 8;
+          float xv[8];
+          if (SWIGLU) {
+            const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 4);
+            const float4 b0 = *(const float4 *)(xr + K), b1 = *(const float4 *)(xr + K + 4);
+            const float h1[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float h3[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = h1[j] * (1.f / (1.f + expf(-h1[j]))) * h3[j];
+          } else {
+            const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 4);
+            xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+            xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+          }
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc[t] = mfma_f32(HT::f(wv[i][j]), xv[j], acc[t]);
+        }
+      }
     }
   }
 #pragma unroll
-  for (int nb = 0; nb < NB; nb++) red[w][nb][lane] = acc[nb];
+  for (int t = 0; t < NT; t++) red[w][t][lane] = acc[t];
   __syncthreads();
   if (w == 0) {
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-      f32x4 s = red[0][nb][lane] + red[1][nb][lane] + red[2][nb][lane] + red[3][nb][lane];
-      // s[i] = out[batch nb*16 + r][row block*16 + 4g + i]
-      const long b = nb * 16 + r;
+    for (int t = 0; t < NT; t++) {
+      const f32x4 s = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
+      // s[i] = sum for sequence t*16 + r, weight row blockIdx.x*16 + 4g + i
+      const int b = t * 16 + r;
       const long n = (long)blockIdx.x * 16 + g * 4;
-      float4 o = make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
-      if (resid) {
-        const float4 q = *(const float4 *)(resid + b * ldo + n);
-        o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+      if (ksplit > 1) {
+        *(f32x4 *)(ws + ((long)blockIdx.y * NT * 16 + b) * N + n) = s;
+      } else if (b < B) {
+        float4 o = make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
+        if (resid) {
+          const float4 q = *(const float4 *)(resid + b * ldo + n);
+          o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+        }
+        *(float4 *)(out + b * ldo + n) = o;
       }
-      *(float4 *)(out + b * ldo + n) = o;
     }
   }
 }
 
+// Ordered sum of the split-K partials (split 0 first), alpha, residual.
+__global__ void gemv_reduce_kernel(const float *__restrict__ ws, int ksplit, int Bp, int N, float *out, long ldo,
+                                   const float *resid, float alpha, int B) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= (long)B * N) return;
+  const int b = (int)(i / N), n = (int)(i % N);
+  float s = 0.f;
+  for (int z = 0; z < ksplit; z++) s += ws[((long)z * Bp + b) * N + n];
+  float o = alpha * s;
+  if (resid) o += resid[(long)b * ldo + n];
+  out[(long)b * ldo + n] = o;
+}
+
+// ------------------------------------------------------------- elementwise / attention ----
+
+// Token of this position (prompt id while pos < P, else the last sampled id) and its
+// embedding row.  One block per sequence.
 template <typename HT>
-__global__ void dec_embed_kernel(const h16_t *__restrict__ E, const int32_t *__restrict__ tok, float *x, int D,
-                                 int B) {
+__global__ void dec_token_kernel(const int32_t *__restrict__ prompt, int ctx, const DecState *__restrict__ st,
+                                 int32_t *tok, const h16_t *__restrict__ E, float *x, int D, int B) {
   const int b = blockIdx.x;
-  for (int i = threadIdx.x; i < D; i += blockDim.x)
-    x[(long)b * D + i] = (b < B) ? HT::f(E[(long)tok[b] * D + i]) : 0.f;
+  const int pos = st->pos;
+  const int t = pos < st->P ? prompt[(long)b * ctx + pos] : tok[b];
+  for (int i = threadIdx.x; i < D; i += blockDim.x) x[(long)b * D + i] = b < B ? HT::f(E[(long)t * D + i]) : 0.f;
+  __syncthreads();
+  if (threadIdx.x == 0) tok[b] = t;
 }
 
 // generate.py:81-84: (x / rms) * w, rms = sqrt(mean(x^2) + eps); one block per sequence
@@ -103,97 +300,131 @@ __global__ void dec_rmsnorm_kernel(const float *__restrict__ x, const float *__r
   for (int i = threadIdx.x; i < D; i += 256) y[(long)b * D + i] = xr[i] / rms * g[i];
 }
 
-// One block per (sequence, head slot): optional per-head RMSNorm, RoPE at position pos,
-// q -> qbuf, k/v -> cache[l][b][kvh][pos].  HD/2 threads, one pair each.
-__global__ void dec_qk_kernel(const float *__restrict__ qkv, int QKV, const float *__restrict__ gq,
-                              const float *__restrict__ gk, const float *__restrict__ cosb,
-                              const float *__restrict__ sinb, float *q, float *kc, float *vc, int NH, int NKV,
-                              int HD, int ctx, int pos, float eps, int B) {
-  const int b = blockIdx.x, h = blockIdx.y;
-  const int i = threadIdx.x, half = HD / 2;
-  if (b >= B) return;
-  const bool isq = h < NH;
-  const int hh = isq ? h : h - NH;
-  const float *src = qkv + (long)b * QKV + (isq ? 0 : NH * HD) + hh * HD;
-  float x0 = src[2 * i], x1 = src[2 * i + 1];
-  const float *gg = isq ? gq : gk;
-  if (gg) {
-    float ss = x0 * x0 + x1 * x1;
-    for (int o = 1; o < half; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    const float rms = sqrtf(ss / (float)HD + eps);
-    x0 = x0 / rms * gg[2 * i];
-    x1 = x1 / rms * gg[2 * i + 1];
-  }
-  const float c = cosb[pos * half + i], s = sinb[pos * half + i];
-  const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-  if (isq) {
-    q[(long)b * NH * HD + hh * HD + 2 * i] = y0;
-    q[(long)b * NH * HD + hh * HD + 2 * i + 1] = y1;
-  } else {
-    const long base = (((long)b * NKV + hh) * ctx + pos) * HD;
-    kc[base + 2 * i] = y0;
-    kc[base + 2 * i + 1] = y1;
-    const float *vs = qkv + (long)b * QKV + (NH + NKV) * HD + hh * HD;
-    vc[base + 2 * i] = vs[2 * i];
-    vc[base + 2 * i + 1] = vs[2 * i + 1];
-  }
-}
-
-// One block per (sequence, q head): softmax(q.K^T * scale) V over positions 0..pos
-// (generate.py:164-181).  256 threads; npos <= ctx.
-__global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ q, const float *__restrict__ kc,
-                                                       const float *__restrict__ vc, float *att, int NH, int NKV,
-                                                       int HD, int ctx, int npos, double scale, int B) {
-  extern __shared__ float sm[];
-  float *qs = sm;          // [HD]
-  float *sc = sm + HD;     // [npos]
-  __shared__ float red[8];
-  const int b = blockIdx.x, h = blockIdx.y;
-  if (b >= B) return;
-  const int kvh = h / (NH / NKV);
-  for (int d = threadIdx.x; d < HD; d += 256) qs[d] = q[(long)b * NH * HD + h * HD + d];
-  __syncthreads();
-  const float *K = kc + ((long)b * NKV + kvh) * ctx * HD;
-  const float *V = vc + ((long)b * NKV + kvh) * ctx * HD;
-  float mx = -INFINITY;
-  for (int t = threadIdx.x; t < npos; t += 256) {
-    const float4 *kr = (const float4 *)(K + (long)t * HD);
-    float s = 0.f;
-    for (int d4 = 0; d4 < HD / 4; d4++) {
-      const float4 kv = kr[d4];
-      s += qs[4 * d4] * kv.x + qs[4 * d4 + 1] * kv.y + qs[4 * d4 + 2] * kv.z + qs[4 * d4 + 3] * kv.w;
+template <int HD, int RATIO>
+__global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv, int QKV,
+                                                       const float *__restrict__ gq, const float *__restrict__ gk,
+                                                       const float *__restrict__ cosb, const float *__restrict__ sinb,
+                                                       float *kc, float *vc, float *att, int NH, int NKV, int ctx,
+                                                       const DecState *__restrict__ st, float eps, double scale) {
+  extern __shared__ float sc[];  // [RATIO][ctx]
+  constexpr int C4 = HD / 4, NG = 256 / C4, HALF = HD / 2;
+  __shared__ float4 qs[RATIO][C4];
+  __shared__ float4 kn[C4], vn[C4];
+  __shared__ float4 part[NG][RATIO][C4];
+  __shared__ float red[RATIO][8];
+  const int b = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+  const int pos = st->pos, npos = pos + 1;
+  float *K = kc + ((long)b * NKV + kvh) * ctx * HD;
+  float *V = vc + ((long)b * NKV + kvh) * ctx * HD;
+  const float *row = qkv + (long)b * QKV;
+  // slots 0..RATIO-1: q heads kvh*RATIO + slot; RATIO: k head kvh; RATIO+1: v head kvh
+  for (int i = tid; i < (RATIO + 2) * HALF; i += 256) {
+    const int slot = i / HALF, p = i % HALF;
+    float *q2 = (float *)qs, *k2 = (float *)kn, *v2 = (float *)vn;
+    if (slot == RATIO + 1) {
+      const float *src = row + (NH + NKV) * HD + kvh * HD;
+      const float y0 = src[2 * p], y1 = src[2 * p + 1];
+      v2[2 * p] = y0; v2[2 * p + 1] = y1;
+      V[(long)pos * HD + 2 * p] = y0;
+      V[(long)pos * HD + 2 * p + 1] = y1;
+      continue;
     }
-    s = (float)((double)s * scale);
-    sc[t] = s;
-    mx = fmaxf(mx, s);
+    const bool isq = slot < RATIO;
+    const float *src = isq ? row + (kvh * RATIO + slot) * HD : row + NH * HD + kvh * HD;
+    float x0 = src[2 * p], x1 = src[2 * p + 1];
+    const float *gg = isq ? gq : gk;
+    if (gg) {  // uniform per block: every lane of the slot's (half-)wave takes part
+      float ss = x0 * x0 + x1 * x1;
+      for (int o = 1; o < HALF; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      const float rms = sqrtf(ss / (float)HD + eps);
+      x0 = x0 / rms * gg[2 * p];
+      x1 = x1 / rms * gg[2 * p + 1];
+    }
+    const float c = cosb[pos * HALF + p], s = sinb[pos * HALF + p];
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    if (isq) {
+      q2[slot * HD + 2 * p] = y0;
+      q2[slot * HD + 2 * p + 1] = y1;
+    } else {
+      k2[2 * p] = y0; k2[2 * p + 1] = y1;
+      K[(long)pos * HD + 2 * p] = y0;
+      K[(long)pos * HD + 2 * p + 1] = y1;
+    }
   }
-  mx = wave_max(mx);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float sum = 0.f;
-  for (int t = threadIdx.x; t < npos; t += 256) {
-    const float e = __expf(sc[t] - mx);
-    sc[t] = e;
-    sum += e;
+  float mx[RATIO];
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) mx[r] = -INFINITY;
+  for (int t = tid; t < npos; t += 256) {
+    const float4 *kr = t == pos ? kn : (const float4 *)(K + (long)t * HD);
+    float s[RATIO];
+#pragma unroll
+    for (int r = 0; r < RATIO; r++) s[r] = 0.f;
+#pragma unroll 8
+    for (int d4 = 0; d4 < C4; d4++) {
+      const float4 kv = kr[d4];
+#pragma unroll
+      for (int r = 0; r < RATIO; r++) {
+        const float4 qv = qs[r][d4];
+        s[r] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RATIO; r++) {
+      const float v = (float)((double)s[r] * scale);
+      sc[r * ctx + t] = v;
+      mx[r] = fmaxf(mx[r], v);
+    }
   }
-  sum = wave_sum(sum);
-  if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = sum;
-  __syncthreads();
-  const float inv = 1.f / (red[4] + red[5] + red[6] + red[7]);
-  for (int d = threadIdx.x; d < HD; d += 256) {
-    float o = 0.f;
-    for (int t = 0; t < npos; t++) o += sc[t] * inv * V[(long)t * HD + d];
-    att[(long)b * NH * HD + h * HD + d] = o;
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) {
+    mx[r] = wave_max(mx[r]);
+    if ((tid & 63) == 0) red[r][tid >> 6] = mx[r];
   }
-}
-
-__global__ void dec_swiglu_kernel(const float *__restrict__ h13, float *gate, int H, int B) {
-  const int b = blockIdx.y;
-  for (int j = blockIdx.x * 256 + threadIdx.x; j < H; j += gridDim.x * 256) {
-    const float h1 = h13[(long)b * 2 * H + j], h3 = h13[(long)b * 2 * H + H + j];
-    gate[(long)b * H + j] = h1 * (1.f / (1.f + expf(-h1))) * h3;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) mx[r] = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3]));
+  float sum[RATIO];
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) sum[r] = 0.f;
+  for (int t = tid; t < npos; t += 256)
+#pragma unroll
+    for (int r = 0; r < RATIO; r++) {
+      const float e = __expf(sc[r * ctx + t] - mx[r]);
+      sc[r * ctx + t] = e;
+      sum[r] += e;
+    }
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) {
+    sum[r] = wave_sum(sum[r]);
+    if ((tid & 63) == 0) red[r][4 + (tid >> 6)] = sum[r];
+  }
+  __syncthreads();
+  const int c = tid % C4, grp = tid / C4;
+  float4 acc[RATIO];
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int t = grp; t < npos; t += NG) {
+    const float4 v = t == pos ? vn[c] : *(const float4 *)(V + (long)t * HD + c * 4);
+#pragma unroll
+    for (int r = 0; r < RATIO; r++) {
+      const float p = sc[r * ctx + t];
+      acc[r].x += p * v.x; acc[r].y += p * v.y; acc[r].z += p * v.z; acc[r].w += p * v.w;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RATIO; r++) part[grp][r][c] = acc[r];
+  __syncthreads();
+  if (grp < RATIO) {
+    const int r = grp;
+    const float inv = 1.f / (red[r][4] + red[r][5] + red[r][6] + red[r][7]);
+    float4 o = part[0][r][c];
+    for (int gi = 1; gi < NG; gi++) {
+      const float4 p = part[gi][r][c];
+      o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
+    }
+    o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
+    *(float4 *)(att + (long)b * NH * HD + (long)(kvh * RATIO + r) * HD + c * 4) = o;
   }
 }
 
@@ -217,43 +448,83 @@ __device__ double block_sum_d(double v, double *red) {
   return s;
 }
 
-// Greedy: first index of the maximum logit (np.argmax).  Sampling: p = softmax(logits/T)
-// in fp32, optional top-p mask, then the first index whose fp64 cumulative mass exceeds
-// u * total (np.random.choice: cdf.searchsorted(u, side='right')).  One block / sequence.
-__global__ __launch_bounds__(1024) void dec_sample_kernel(float *logits, int V, float temp, float top_p,
-                                                          const double *__restrict__ unif, int ctx, int step,
-                                                          int32_t *tok, int32_t *out) {
+__device__ __forceinline__ int gen_step(const DecState *st) { return st->pos - (st->P - 1); }
+
+// Greedy from per-block partials: first index of the maximum logit (np.argmax).  One block
+// (256 threads) per sequence.
+__global__ __launch_bounds__(256) void dec_argmax_kernel(const float *__restrict__ amv, const int32_t *__restrict__ ami,
+                                                         int nblk, const DecState *__restrict__ st, int ctx,
+                                                         int32_t *tok, int32_t *out) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < nblk; i += 256) {
+    const float v = amv[(long)b * nblk + i];
+    const int j = ami[(long)b * nblk + i];
+    if (v > best || (v == best && j < bi)) { best = v; bi = j; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { rv[tid >> 6] = best; ri[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    best = rv[0]; bi = ri[0];
+    for (int w = 1; w < 4; w++)
+      if (rv[w] > best || (rv[w] == best && ri[w] < bi)) { best = rv[w]; bi = ri[w]; }
+    tok[b] = bi;
+    out[(long)b * ctx + gen_step(st)] = bi;
+  }
+}
+
+// Greedy over full logits rows (batch > 4): per-block partials of 4096-wide chunks.
+__global__ __launch_bounds__(256) void dec_argmax_part_kernel(const float *__restrict__ logits, int V, int nblk,
+                                                              float *amv, int32_t *ami) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int chunk = (V + nblk - 1) / nblk;
+  const int i0 = blockIdx.x * chunk, i1 = min(V, i0 + chunk);
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = i0 + tid; i < i1; i += 256) {
+    const float v = logits[(long)b * V + i];
+    if (v > best) { best = v; bi = i; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+  }
+  if ((tid & 63) == 0) { rv[tid >> 6] = best; ri[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    best = rv[0]; bi = ri[0];
+    for (int w = 1; w < 4; w++)
+      if (rv[w] > best || (rv[w] == best && ri[w] < bi)) { best = rv[w]; bi = ri[w]; }
+    amv[(long)b * nblk + blockIdx.x] = best;
+    ami[(long)b * nblk + blockIdx.x] = bi;
+  }
+}
+
+// Sampling: p = softmax(logits/T) in fp32, optional top-p mask, then the first index whose
+// fp64 cumulative mass exceeds u * total (np.random.choice: cdf.searchsorted(u,
+// side='right')).  One block (1024 threads) per sequence.
+__global__ __launch_bounds__(1024) void dec_sample_kernel(float *logits, int V, const DecState *__restrict__ st,
+                                                          const double *__restrict__ unif, int ctx, int32_t *tok,
+                                                          int32_t *out) {
   __shared__ float redf[16];
   __shared__ double redd[16];
-  __shared__ int redi[16];
   __shared__ double wsum[16];
   const int b = blockIdx.x;
+  const float temp = st->temp, top_p = st->top_p;
+  const int step = gen_step(st);
   float *lg = logits + (long)b * V;
   const int tid = threadIdx.x, nt = blockDim.x;
-  if (temp < 1e-6f) {
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = tid; i < V; i += nt) {
-      const float v = lg[i];
-      if (v > best) { best = v; bi = i; }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
-    }
-    if ((tid & 63) == 0) { redf[tid >> 6] = best; redi[tid >> 6] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-      float bv = redf[0];
-      int bj = redi[0];
-      for (int w = 1; w < nt / 64; w++)
-        if (redf[w] > bv || (redf[w] == bv && redi[w] < bj)) { bv = redf[w]; bj = redi[w]; }
-      tok[b] = bj;
-      out[(long)b * ctx + step] = bj;
-    }
-    return;
-  }
   // p_i = exp(x_i - max) / sum, x_i = logit_i / temp  (generate.py:201-202, softmax 87-90)
   float mx = -INFINITY;
   for (int i = tid; i < V; i += nt) mx = fmaxf(mx, lg[i] / temp);
@@ -323,19 +594,204 @@ __global__ __launch_bounds__(1024) void dec_sample_kernel(float *logits, int V, 
   }
 }
 
-__global__ void set_tokens_kernel(const int32_t *__restrict__ prompt, int P, int pos, int32_t *tok, int B) {
-  const int b = threadIdx.x;
-  if (b < B) tok[b] = prompt[(long)b * P + pos];
+__global__ void dec_advance_kernel(DecState *st) {
+  if (threadIdx.x == 0) st->pos += 1;
 }
 
-int gemv(ne_ctx *c, const h16_t *W, int N, int K, const float *x, float *out, const float *resid, float alpha) {
+// ----------------------------------------------------------------------- launchers ----
+
+int pick_rpw(int N) {
+  for (int rpw : {4, 2}) if (N % (4 * rpw) == 0 && N / (4 * rpw) >= 512) return rpw;
+  return 1;
+}
+
+template <typename HT, int NB, int RPW, int PRO, bool AMX>
+int gemv_valu_kc(const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps, float *out,
+                 long ldo, const float *resid, float alpha, int B, float *amv, int32_t *ami, hipStream_t s) {
+  const int nblk = N / (4 * RPW);
+  const size_t sh = (size_t)NB * K * sizeof(float);
+  if (K <= 1024)
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 2, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
+                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+  else if (K <= 2048)
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 4, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
+                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+  else
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 6, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
+                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+  return ne_hip_status(hipGetLastError(), "decode gemv");
+}
+
+template <typename HT, int NB, int PRO, bool AMX>
+int gemv_valu_nb(const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps, float *out,
+                 long ldo, const float *resid, float alpha, int B, float *amv, int32_t *ami, hipStream_t s) {
+  const int rpw = pick_rpw(N);
+  if (rpw == 4) return gemv_valu_kc<HT, NB, 4, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (rpw == 2) return gemv_valu_kc<HT, NB, 2, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  return gemv_valu_kc<HT, NB, 1, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+}
+
+template <typename HT, int PRO, bool AMX>
+int gemv_valu_pro(int B, const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps,
+                  float *out, long ldo, const float *resid, float alpha, float *amv, int32_t *ami, hipStream_t s) {
+  if (B == 1) return gemv_valu_nb<HT, 1, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (B == 2) return gemv_valu_nb<HT, 2, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  return gemv_valu_nb<HT, 4, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+}
+
+// Batch <= 4: out = alpha * W . pro(in) + resid.  Requires N % 4 == 0, K % 8 == 0.
+int gemv_small(ne_ctx *c, int B, int pro, bool amx, const h16_t *W, int N, int K, const float *in, long ldi,
+               const float *g, float *out, long ldo, const float *resid, float alpha) {
+  Dec *d = (Dec *)c->dec;
+  if (N % 4 || K % 8 || K > 3072)
+    return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%4, K%%8, K <= 3072)", N, K);
+  const float eps = c->c.norm_eps;
+  return DISPATCH_H16(c->dt, [&] {
+    if (pro == PRO_RMSNORM) {
+      if (amx) return gemv_valu_pro<HT, PRO_RMSNORM, true>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, d->amv, d->ami, c->st);
+      return gemv_valu_pro<HT, PRO_RMSNORM, false>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, nullptr, nullptr, c->st);
+    }
+    if (pro == PRO_SWIGLU)
+      return gemv_valu_pro<HT, PRO_SWIGLU, false>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, nullptr, nullptr, c->st);
+    return gemv_valu_pro<HT, PRO_NONE, false>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, nullptr, nullptr, c->st);
+  }());
+}
+
+template <typename HT, int NT, bool SW>
+void launch_mfma(dim3 grid, hipStream_t st, const h16_t *W, int K, const float *x, int ks, float *out, long ldo,
+                 const float *resid, float alpha, float *ws, int N, int B) {
+  hipLaunchKernelGGL((gemv_mfma_kernel<HT, NT, SW>), grid, dim3(256), 0, st, W, (long)K, x, K, ks, out, ldo, resid,
+                     alpha, ws, N, B);
+}
+
+// Batch 5..32: out = alpha * W . x + resid with x [Bp, K] fp32 (swiglu: x = gate of h13 rows
+// [Bp, 2K]).  Requires N % 16, K % 128.
+int gemv_big(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, float *out, long ldo,
+             const float *resid, float alpha, bool swiglu = false) {
   Dec *d = (Dec *)c->dec;
   if (N % 16 || K % 128) return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%16, K%%128)", N, K);
-  return DISPATCH_H16(c->dt, [&] {
-    if (d->Bp == 16) hipLaunchKernelGGL((gemv_kernel<HT, 1>), dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
-    else hipLaunchKernelGGL((gemv_kernel<HT, 2>), dim3(N / 16), dim3(256), 0, c->st, W, (long)K, x, K, out, (long)N, resid, alpha);
+  int ks = 1;
+  while ((N / 16) * ks < 512 && K % (128 * ks * 2) == 0 && (long)ks * 2 * d->Bp * N <= d->ws_elems) ks *= 2;
+  const dim3 grid(N / 16, ks);
+  NE_CHECK(DISPATCH_H16(c->dt, [&] {
+    if (d->Bp == 16) {
+      if (swiglu) launch_mfma<HT, 1, true>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+      else launch_mfma<HT, 1, false>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+    } else {
+      if (swiglu) launch_mfma<HT, 2, true>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+      else launch_mfma<HT, 2, false>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+    }
     return ne_hip_status(hipGetLastError(), "decode gemv");
-  }());
+  }()));
+  if (ks > 1) {
+    const long n = (long)B * N;
+    hipLaunchKernelGGL(gemv_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, c->st, d->ws, ks, d->Bp, N, out, ldo,
+                       resid, alpha, B);
+    NE_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc) {
+  Dec *d = (Dec *)c->dec;
+  const int ratio = c->NH / c->NKV;
+  const size_t sh = (size_t)ratio * d->ctx * sizeof(float);
+  const double scale = 1.0 / sqrt((double)c->HD);
+  const float *gq = c->c.qk_norm ? c->P + o.gq : nullptr, *gk = c->c.qk_norm ? c->P + o.gk : nullptr;
+  const dim3 grid(B, c->NKV);
+#define NE_DEC_ATTN(HDV, R)                                                                                     \
+  hipLaunchKernelGGL((dec_attn_kernel<HDV, R>), grid, dim3(256), sh, c->st, d->qkv, c->QKV, gq, gk, d->cosb,   \
+                     d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale)
+  if (c->HD == 128) {
+    if (ratio == 1) NE_DEC_ATTN(128, 1);
+    else if (ratio == 2) NE_DEC_ATTN(128, 2);
+    else NE_DEC_ATTN(128, 4);
+  } else {
+    if (ratio == 1) NE_DEC_ATTN(64, 1);
+    else if (ratio == 2) NE_DEC_ATTN(64, 2);
+    else NE_DEC_ATTN(64, 4);
+  }
+#undef NE_DEC_ATTN
+  return ne_hip_status(hipGetLastError(), "decode attention");
+}
+
+// Enqueue the kernels of one position for B sequences.  gen: also the final norm, LM head
+// and token choice.  Position-independent (everything position-dependent is read from
+// d->st), so it can be captured once and replayed.
+int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
+  Dec *d = (Dec *)c->dec;
+  const int D = c->D, H = c->H, Q = c->Q, NKV = c->NKV, HD = c->HD, QKV = c->QKV, V = c->V;
+  const float eps = c->c.norm_eps, alpha = c->c.res_alpha;
+  const h16_t *Pb = c->Pb;
+  const float *Pf = c->P;
+  const bool small = B <= VB;
+  if (c->dt == NE_FP16)
+    hipLaunchKernelGGL(dec_token_kernel<H16F>, dim3(B), dim3(256), 0, c->st, d->prompt, d->ctx, d->st, d->tok,
+                       Pb + c->off_E, d->x, D, B);
+  else
+    hipLaunchKernelGGL(dec_token_kernel<H16B>, dim3(B), dim3(256), 0, c->st, d->prompt, d->ctx, d->st, d->tok,
+                       Pb + c->off_E, d->x, D, B);
+  NE_HIP(hipGetLastError());
+  for (int l = 0; l < c->L; l++) {
+    const LayerOff &o = c->lo[l];
+    const size_t kvl = (size_t)l * d->Bmax * NKV * d->ctx * HD;
+    if (small) {
+      NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.wqkv, QKV, D, d->x, D, Pf + o.g_att, d->qkv, QKV, nullptr, 1.f));
+    } else {
+      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_att, d->xn, D, eps);
+      NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, d->qkv, QKV, nullptr, 1.f));
+    }
+    NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl));
+    if (small) {
+      NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.wo, D, Q, d->att, Q, nullptr, d->x, D, d->x, alpha));
+      NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.w13, 2 * H, D, d->x, D, Pf + o.g_ffn, d->h13, 2 * H, nullptr, 1.f));
+      NE_CHECK(gemv_small(c, B, PRO_SWIGLU, false, Pb + o.w2, D, H, d->h13, 2 * H, nullptr, d->x, D, d->x, alpha));
+    } else {
+      NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, d->x, D, d->x, alpha));
+      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_ffn, d->xn, D, eps);
+      NE_CHECK(gemv_big(c, B, Pb + o.w13, 2 * H, D, d->xn, d->h13, 2 * H, nullptr, 1.f));
+      NE_CHECK(gemv_big(c, B, Pb + o.w2, D, H, d->h13, d->x, D, d->x, alpha, true));
+    }
+  }
+  if (gen) {
+    if (small) {
+      NE_CHECK(gemv_small(c, B, PRO_RMSNORM, greedy, Pb + c->off_E, V, D, d->x, D, Pf + c->off_gfinal, d->logits, V,
+                          nullptr, 1.f));
+      if (greedy)
+        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(256), 0, c->st, d->amv, d->ami, V / (4 * pick_rpw(V)),
+                           d->st, d->ctx, d->tok, d->out);
+    } else {
+      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + c->off_gfinal, d->xn, D, eps);
+      NE_CHECK(gemv_big(c, B, Pb + c->off_E, V, D, d->xn, d->logits, V, nullptr, 1.f));
+      if (greedy) {
+        hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(BIG_ARGMAX, B), dim3(256), 0, c->st, d->logits, V, BIG_ARGMAX,
+                           d->amv, d->ami);
+        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(256), 0, c->st, d->amv, d->ami, BIG_ARGMAX, d->st, d->ctx,
+                           d->tok, d->out);
+      }
+    }
+    if (!greedy)
+      hipLaunchKernelGGL(dec_sample_kernel, dim3(B), dim3(1024), 0, c->st, d->logits, V, d->st, d->unif, d->ctx,
+                         d->tok, d->out);
+  }
+  hipLaunchKernelGGL(dec_advance_kernel, dim3(1), dim3(64), 0, c->st, d->st);
+  return ne_hip_status(hipGetLastError(), "decode position");
+}
+
+int capture(ne_ctx *c, int B, bool gen, bool greedy, hipGraphExec_t *exec) {
+  hipGraph_t graph = nullptr;
+  NE_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_position(c, B, gen, greedy);
+  const hipError_t ec = hipStreamEndCapture(c->st, &graph);
+  if (rc) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  NE_HIP(ec);
+  const hipError_t ei = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  NE_HIP(ei);
+  return 0;
 }
 
 }  // namespace
@@ -344,25 +800,39 @@ int decode_alloc(ne_ctx *c) {
   Dec *d = new Dec();
   c->dec = d;
   if (c->c.decode_batch > 32) return ne_fail(NE_ERR_ARG, "decode_batch %d > 32", c->c.decode_batch);
-  d->Bp = c->c.decode_batch <= 16 ? 16 : 32;
+  if (c->NH / c->NKV > 4) return ne_fail(NE_ERR_ARG, "decode: more than 4 query heads per KV head");
+  if (c->D % 128 || c->H % 128 || c->Q % 128)
+    return ne_fail(NE_ERR_ARG, "decode: dim, hidden and q_dim must be multiples of 128");
+  d->Bmax = c->c.decode_batch;
+  d->Bp = d->Bmax <= 16 ? 16 : 32;
   d->ctx = c->c.decode_ctx;
-  const size_t Bp = d->Bp, ctx = d->ctx, L = c->L, D = c->D, H = c->H, Q = c->Q, NKV = c->NKV, HD = c->HD;
-  const size_t kv = L * Bp * NKV * ctx * HD;
+  const size_t Bp = d->Bp, Bm = d->Bmax, ctx = d->ctx, L = c->L, D = c->D, H = c->H, Q = c->Q, NKV = c->NKV,
+               HD = c->HD, V = c->V;
+  const size_t kv = L * Bm * NKV * ctx * HD;
+  d->lm_nblk = std::max<int>(c->V / (4 * pick_rpw(c->V)), BIG_ARGMAX);
+  d->ws_elems = (long)8 * Bp * std::max<size_t>(2 * H, Q + 2 * NKV * HD);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += (bytes + 255) & ~(size_t)255; return o; };
-  const size_t o_kc = take(kv * 4), o_vc = take(kv * 4), o_x = take(Bp * D * 4), o_xn = take(Bp * D * 4);
-  const size_t o_qkv = take(Bp * (Q + 2 * NKV * HD) * 4), o_q = take(Bp * Q * 4), o_att = take(Bp * Q * 4);
-  const size_t o_h13 = take(Bp * 2 * H * 4), o_gate = take(Bp * H * 4), o_lg = take(Bp * (size_t)c->V * 4);
-  const size_t o_tok = take(Bp * 4), o_out = take(Bp * ctx * 4), o_u = take(Bp * ctx * 8);
-  const size_t o_cos = take(ctx * HD / 2 * 4), o_sin = take(ctx * HD / 2 * 4);
+  const size_t o_kc = take(kv * 4), o_vc = take(kv * 4), o_x = take(Bp * D * 4);
+  const size_t o_xn = take(Bp * std::max(D, H) * 4);
+  const size_t o_qkv = take(Bp * (Q + 2 * NKV * HD) * 4), o_att = take(Bp * Q * 4);
+  const size_t o_h13 = take(Bp * 2 * H * 4), o_lg = take(Bp * V * 4);
+  const size_t o_ws = take((size_t)d->ws_elems * 4);
+  const size_t o_amv = take(Bp * (size_t)d->lm_nblk * 4), o_ami = take(Bp * (size_t)d->lm_nblk * 4);
+  const size_t o_tok = take(Bp * 4), o_out = take(Bp * ctx * 4), o_pr = take(Bp * ctx * 4), o_u = take(Bp * ctx * 8);
+  const size_t o_cos = take(ctx * HD / 2 * 4), o_sin = take(ctx * HD / 2 * 4), o_st = take(sizeof(DecState));
   NE_HIP(hipMalloc(&d->arena, off));
   char *base = (char *)d->arena;
   d->kc = (float *)(base + o_kc); d->vc = (float *)(base + o_vc);
   d->x = (float *)(base + o_x); d->xn = (float *)(base + o_xn);
-  d->qkv = (float *)(base + o_qkv); d->q = (float *)(base + o_q); d->att = (float *)(base + o_att);
-  d->h13 = (float *)(base + o_h13); d->gate = (float *)(base + o_gate); d->logits = (float *)(base + o_lg);
-  d->tok = (int32_t *)(base + o_tok); d->out = (int32_t *)(base + o_out); d->unif = (double *)(base + o_u);
+  d->qkv = (float *)(base + o_qkv); d->att = (float *)(base + o_att);
+  d->h13 = (float *)(base + o_h13); d->logits = (float *)(base + o_lg);
+  d->ws = (float *)(base + o_ws);
+  d->amv = (float *)(base + o_amv); d->ami = (int32_t *)(base + o_ami);
+  d->tok = (int32_t *)(base + o_tok); d->out = (int32_t *)(base + o_out); d->prompt = (int32_t *)(base + o_pr);
+  d->unif = (double *)(base + o_u);
   d->cosb = (float *)(base + o_cos); d->sinb = (float *)(base + o_sin);
+  d->st = (DecState *)(base + o_st);
   NE_HIP(hipMemset(d->arena, 0, off));
   // RoPE tables for decode positions: float64 angles rounded to fp32 (generate.py:101-105)
   const int half = c->HD / 2;
@@ -381,9 +851,17 @@ int decode_alloc(ne_ctx *c) {
 void decode_free(ne_ctx *c) {
   Dec *d = (Dec *)c->dec;
   if (!d) return;
+  for (auto &g : d->graphs) {
+    if (g.pre) hipGraphExecDestroy(g.pre);
+    if (g.gen) hipGraphExecDestroy(g.gen);
+  }
   if (d->arena) hipFree(d->arena);
   delete d;
   c->dec = nullptr;
+}
+
+namespace {
+int replay(ne_ctx *c, int B, int P, int n_new, bool greedy);
 }
 
 int decode_run(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float temp, float top_p,
@@ -393,65 +871,61 @@ int decode_run(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float 
   if (B <= 0 || B > c->c.decode_batch || P <= 0 || n_new <= 0 || P + n_new > d->ctx)
     return ne_fail(NE_ERR_ARG, "decode: B=%d P=%d n_new=%d exceed decode_batch=%d / decode_ctx=%d", B, P, n_new,
                    c->c.decode_batch, d->ctx);
-  if (temp >= 1e-6f && !uniforms) return ne_fail(NE_ERR_ARG, "decode: sampling needs uniforms");
+  const bool greedy = temp < 1e-6f;
+  if (!greedy && !uniforms) return ne_fail(NE_ERR_ARG, "decode: sampling needs uniforms");
   for (long i = 0; i < (long)B * P; i++)
     if (prompt[i] < 0 || prompt[i] >= c->V) return ne_fail(NE_ERR_ARG, "decode: prompt id out of range");
-  const int D = c->D, H = c->H, Q = c->Q, NH = c->NH, NKV = c->NKV, HD = c->HD, QKV = c->QKV, V = c->V;
-  const float eps = c->c.norm_eps, alpha = c->c.res_alpha;
-  const double scale = 1.0 / sqrt((double)HD);
-  int32_t *dprompt = nullptr;
-  NE_HIP(hipMalloc((void **)&dprompt, (size_t)B * P * 4));
-  NE_HIP(hipMemcpyAsync(dprompt, prompt, (size_t)B * P * 4, hipMemcpyHostToDevice, c->st));
-  if (uniforms) {
-    std::vector<double> u((size_t)d->Bp * d->ctx, 0.0);
+  // per-call inputs: prompt rows, uniforms, state (outside the captured graphs)
+  std::vector<int32_t> pr((size_t)d->Bp * d->ctx, 0);
+  for (int b = 0; b < B; b++)
+    for (int j = 0; j < P; j++) pr[(size_t)b * d->ctx + j] = prompt[(size_t)b * P + j];
+  NE_HIP(hipMemcpyAsync(d->prompt, pr.data(), pr.size() * 4, hipMemcpyHostToDevice, c->st));
+  std::vector<double> u;
+  if (!greedy) {
+    u.assign((size_t)d->Bp * d->ctx, 0.0);
     for (int b = 0; b < B; b++)
       for (int j = 0; j < n_new; j++) u[(size_t)b * d->ctx + j] = uniforms[(size_t)b * n_new + j];
     NE_HIP(hipMemcpyAsync(d->unif, u.data(), u.size() * 8, hipMemcpyHostToDevice, c->st));
-    NE_HIP(hipStreamSynchronize(c->st));
   }
-  const h16_t *Pb = c->Pb;
-  const float *Pf = c->P;
-  int rc = 0;
-  int step = 0;
-  for (int pos = 0; pos < P + n_new - 1 && !rc; pos++) {
-    if (pos < P) hipLaunchKernelGGL(set_tokens_kernel, dim3(1), dim3(64), 0, c->st, dprompt, P, pos, d->tok, B);
-    if (c->dt == NE_FP16) hipLaunchKernelGGL(dec_embed_kernel<H16F>, dim3(d->Bp), dim3(256), 0, c->st, Pb + c->off_E, d->tok, d->x, D, B);
-    else hipLaunchKernelGGL(dec_embed_kernel<H16B>, dim3(d->Bp), dim3(256), 0, c->st, Pb + c->off_E, d->tok, d->x, D, B);
-    for (int l = 0; l < c->L && !rc; l++) {
-      const LayerOff &o = c->lo[l];
-      const size_t kvl = (size_t)l * d->Bp * NKV * d->ctx * HD;
-      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_att, d->xn, D, eps);
-      if ((rc = gemv(c, Pb + o.wqkv, QKV, D, d->xn, d->qkv, nullptr, 1.f))) break;
-      hipLaunchKernelGGL(dec_qk_kernel, dim3(B, NH + NKV), dim3(HD / 2), 0, c->st, d->qkv, QKV,
-                         c->c.qk_norm ? Pf + o.gq : nullptr, c->c.qk_norm ? Pf + o.gk : nullptr, d->cosb, d->sinb,
-                         d->q, d->kc + kvl, d->vc + kvl, NH, NKV, HD, d->ctx, pos, eps, B);
-      hipLaunchKernelGGL(dec_attn_kernel, dim3(B, NH), dim3(256), (HD + d->ctx) * sizeof(float), c->st, d->q,
-                         d->kc + kvl, d->vc + kvl, d->att, NH, NKV, HD, d->ctx, pos + 1, scale, B);
-      if ((rc = gemv(c, Pb + o.wo, D, Q, d->att, d->x, d->x, alpha))) break;
-      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_ffn, d->xn, D, eps);
-      if ((rc = gemv(c, Pb + o.w13, 2 * H, D, d->xn, d->h13, nullptr, 1.f))) break;
-      hipLaunchKernelGGL(dec_swiglu_kernel, dim3((H + 255) / 256, B), dim3(256), 0, c->st, d->h13, d->gate, H, B);
-      if ((rc = gemv(c, Pb + o.w2, D, H, d->gate, d->x, d->x, alpha))) break;
-    }
-    if (rc) break;
-    hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + c->off_gfinal, d->xn, D, eps);
-    if (pos >= P - 1) {
-      if ((rc = gemv(c, Pb + c->off_E, V, D, d->xn, d->logits, nullptr, 1.f))) break;
-      hipLaunchKernelGGL(dec_sample_kernel, dim3(B), dim3(1024), 0, c->st, d->logits, V, temp, top_p, d->unif,
-                         d->ctx, step, d->tok, d->out);
-      step++;
-    }
-    if ((rc = ne_hip_status(hipGetLastError(), "decode step"))) break;
+  const DecState s0 = {0, P, temp, top_p};
+  NE_HIP(hipMemcpyAsync(d->st, &s0, sizeof s0, hipMemcpyHostToDevice, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));  // host staging vectors are released at return
+
+  if (!c->use_graphs) {  // eager launches (tracers that do not follow graph launches)
+    for (int pos = 0; pos < P + n_new - 1; pos++) NE_CHECK(enqueue_position(c, B, pos >= P - 1, greedy));
+  } else {
+    NE_CHECK(replay(c, B, P, n_new, greedy));
   }
-  if (!rc) {
-    std::vector<int32_t> o((size_t)d->Bp * d->ctx);
-    rc = ne_hip_status(hipMemcpyAsync(o.data(), d->out, o.size() * 4, hipMemcpyDeviceToHost, c->st), "decode out");
-    if (!rc) rc = ne_hip_status(hipStreamSynchronize(c->st), "decode sync");
-    if (!rc)
-      for (int b = 0; b < B; b++)
-        for (int j = 0; j < n_new; j++) out[(size_t)b * n_new + j] = o[(size_t)b * d->ctx + j];
-  }
-  hipStreamSynchronize(c->st);
-  hipFree(dprompt);
-  return rc;
+  std::vector<int32_t> o((size_t)d->Bp * d->ctx);
+  NE_HIP(hipMemcpyAsync(o.data(), d->out, o.size() * 4, hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  for (int b = 0; b < B; b++)
+    for (int j = 0; j < n_new; j++) out[(size_t)b * n_new + j] = o[(size_t)b * d->ctx + j];
+  return 0;
 }
+
+namespace {
+
+// Replay the captured position graphs (captured on first use per batch size and mode).
+int replay(ne_ctx *c, int B, int P, int n_new, bool greedy) {
+  Dec *d = (Dec *)c->dec;
+  Dec::Graph *gr = nullptr;
+  for (auto &g : d->graphs)
+    if (g.B == B && g.greedy == greedy) gr = &g;
+  if (!gr) {
+    Dec::Graph g = {B, greedy, nullptr, nullptr};
+    int rc = capture(c, B, false, greedy, &g.pre);
+    if (!rc) rc = capture(c, B, true, greedy, &g.gen);
+    if (rc) {
+      if (g.pre) hipGraphExecDestroy(g.pre);
+      return rc;
+    }
+    d->graphs.push_back(g);
+    gr = &d->graphs.back();
+  }
+  for (int pos = 0; pos < P - 1; pos++) NE_HIP(hipGraphLaunch(gr->pre, c->st));
+  for (int j = 0; j < n_new; j++) NE_HIP(hipGraphLaunch(gr->gen, c->st));
+  return 0;
+}
+
+}  // namespace

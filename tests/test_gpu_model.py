@@ -201,3 +201,35 @@ def test_graph_replay_matches_eager_launches():
     assert l1 == l2
     for n in g1:
         np.testing.assert_allclose(g1[n], g2[n], rtol=1e-6, atol=1e-9, err_msg=n)
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 5, 16, 32])
+def test_decode_batch_sizes_match_oracle(B):
+    """Greedy decode through both GEMV paths (VALU for batch <= 4, split-K MFMA above), with
+    the per-position HIP graphs reused across calls of the same batch size and rebuilt for a
+    new one."""
+    cfg = om.tiny(**CASES["qwen3"], vocab=1024)
+    P = _held_params(cfg, ne.NE_BF16, std=0.05)
+    prompt = np.random.default_rng(10 + B).integers(0, cfg.vocab, (B, 6)).astype(np.int32)
+    m = ne.Model.from_oracle(cfg, decode_batch=32, decode_ctx=64, dtype=ne.NE_BF16)
+    m.set_params(P)
+    want = om.decode(cfg, P, prompt, 20)
+    for _ in range(2):  # second call replays the cached graphs
+        np.testing.assert_array_equal(m.decode(prompt, 20), want)
+    # a different batch size and prompt length on the same context
+    p2 = prompt[:1, :3]
+    np.testing.assert_array_equal(m.decode(p2, 12), om.decode(cfg, P, p2, 12))
+    m.close()
+
+
+def test_decode_sampling_mfma_path():
+    cfg = om.tiny(**CASES["qwen3"], vocab=1024)
+    P = _held_params(cfg, ne.NE_BF16, std=0.3)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, (8, 5)).astype(np.int32)
+    u = np.random.RandomState(5).random_sample((8, 12))
+    m = ne.Model.from_oracle(cfg, decode_batch=8, decode_ctx=32, dtype=ne.NE_BF16)
+    m.set_params(P)
+    got = m.decode(prompt, 12, temperature=0.6, top_p=0.95, uniforms=u)
+    want = om.decode(cfg, P, prompt, 12, temperature=0.6, top_p=0.95, uniforms=u)
+    np.testing.assert_array_equal(got, want)
+    m.close()

@@ -55,3 +55,23 @@ def test_qwen3_step_parity():
     P = om.init_params(cfg, seed=0, std=0.02)
     tok = om.tokens_for_step(cfg, 1, 256, seed=1)
     _compare_grads(cfg, P, tok, "qwen3-0.6b B=1 S=256 qk-norm theta=1e6").close()
+
+
+@pytest.mark.parametrize("B", [1, 32])
+def test_qwen3_decode_greedy_64_tokens(B):
+    """The Qwen3-0.6B token loop: bf16-held N(0, 0.02) weights from seed 0, a 32-token
+    prompt of uniform ids, 64 greedy tokens, token-identical to the oracle's generate
+    path on the same bf16 weights (fp32 activations and KV cache on both sides)."""
+    cfg = om.qwen3_06b(res_alpha=1.0)
+    P = {k: om.round_bf16(v) for k, v in om.init_params(cfg, seed=0, std=0.02).items()}
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, (B, 32)).astype(np.int32)
+    m = ne.Model.from_oracle(cfg, batch=1, decode_batch=B, decode_ctx=96, dtype=ne.NE_BF16)
+    m.set_params(P)
+    t0 = time.time()
+    got = m.decode(prompt, 64)
+    t1 = time.time()
+    want, margins, _ = om.decode(cfg, P, prompt, 64, return_logits=True)
+    print(f"\n[decode B={B}] gpu {t1 - t0:.2f}s oracle {time.time() - t1:.1f}s; "
+          f"min top-2 margin {margins.min():.3e}", flush=True)
+    np.testing.assert_array_equal(got, want)
+    m.close()
