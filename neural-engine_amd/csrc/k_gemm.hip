@@ -5,7 +5,9 @@
 // (activation rows, weight rows [N,K]) or M/N-contiguous (the dY^T and X of a
 // weight-gradient GEMM); both are staged into LDS K-contiguous so every MFMA operand is
 // one 16-byte LDS read.  M/N-contiguous tiles are transposed in registers in 4x8 blocks on
-// the way into LDS.  Double-buffered LDS, one barrier per K step.
+// the way into LDS, with a thread mapping that keeps those 8-byte LDS writes free of bank
+// conflicts.  Double-buffered LDS, one barrier per K step.  Block tiles: 256x256 with 8 waves
+// (64x128 each) for large shapes, 128x128 or 64x64 with 4 waves (64x64 / 32x32) otherwise.
 //
 // Small-M shapes (a 256-token step) leave too few output tiles to fill 256 CUs, so the
 // launcher splits K over grid.z: each split writes its fp32 partial tile to a workspace
@@ -20,26 +22,35 @@
 
 namespace {
 
-constexpr int NTHREADS = 256;
-
-template <int R, int BK, bool KC>
+template <int NT, int R, int BK, bool KC>
 struct Stage {
   // KC: element (r, k) at p[r*ld + k]; otherwise at p[k*ld + r].
   static constexpr int NCH = KC ? R * BK / 8 : (R / 8) * (BK / 4);
-  static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+  static constexpr int PER = (NCH + NT - 1) / NT;
   static constexpr int NV = KC ? PER : PER * 4;
+  static_assert(KC || (R / 8) % 4 == 0, "MN-contiguous tiles need R % 32 == 0");
   u16x8 v[NV];
+
+  // MN-contiguous chunk c -> (k block of 4, 8-wide r chunk): 4 consecutive threads take
+  // consecutive r chunks (64-byte row segments in HBM), the next bits walk the k blocks, so
+  // the 8-byte LDS writes of a wave land on distinct banks.
+  __device__ __forceinline__ static void mn_idx(int c, int &kb, int &rc) {
+    const int lo = c % 4, kk = (c / 4) % (BK / 4), hi = c / (4 * (BK / 4));
+    kb = kk;
+    rc = hi * 4 + lo;
+  }
 
   __device__ __forceinline__ void load(const h16_t *p, long ld, int r0, int k0, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      int c = tid + i * NTHREADS;
-      if (NCH % NTHREADS == 0 || c < NCH) {
+      int c = tid + i * NT;
+      if (NCH % NT == 0 || c < NCH) {
         if (KC) {
           int r = c / (BK / 8), k8 = c % (BK / 8);
           v[i] = *(const u16x8 *)(p + (long)(r0 + r) * ld + k0 + k8 * 8);
         } else {
-          int kb = c / (R / 8), rc = c % (R / 8);
+          int kb, rc;
+          mn_idx(c, kb, rc);
 #pragma unroll
           for (int j = 0; j < 4; j++)
             v[i * 4 + j] = *(const u16x8 *)(p + (long)(k0 + kb * 4 + j) * ld + r0 + rc * 8);
@@ -52,13 +63,14 @@ struct Stage {
   __device__ __forceinline__ void store(h16_t *lds, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      int c = tid + i * NTHREADS;
-      if (NCH % NTHREADS == 0 || c < NCH) {
+      int c = tid + i * NT;
+      if (NCH % NT == 0 || c < NCH) {
         if (KC) {
           int r = c / (BK / 8), k8 = c % (BK / 8);
           *(u16x8 *)(lds + r * PITCH + k8 * 8) = v[i];
         } else {
-          int kb = c / (R / 8), rc = c % (R / 8);
+          int kb, rc;
+          mn_idx(c, kb, rc);
 #pragma unroll
           for (int e = 0; e < 8; e++) {
             u16x4 t;
@@ -110,12 +122,13 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
 }
 
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
-__global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+  constexpr int NTHREADS = WM * WN * 64;
   constexpr int PITCH = BK + 8;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
-  static_assert(WM * WN == 4, "4 waves");
   static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
+  // 256x256 tiles: 144 KB of the 160 KB LDS of a gfx950 CU (one work-group per CU)
   __shared__ __attribute__((aligned(16))) h16_t lds[2][(BM + BN) * PITCH];
 
   const int tid = threadIdx.x;
@@ -129,8 +142,8 @@ __global__ __launch_bounds__(NTHREADS) void gemm_kernel(GemmArgs g) {
   const int kt0 = (int)((long)nkt * blockIdx.z / g.split);
   const int kt1 = (int)((long)nkt * (blockIdx.z + 1) / g.split);
 
-  Stage<BM, BK, AKC> sa;
-  Stage<BN, BK, BKC> sb;
+  Stage<NTHREADS, BM, BK, AKC> sa;
+  Stage<NTHREADS, BN, BK, BKC> sb;
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; i++)
@@ -287,7 +300,7 @@ template <typename HT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int E
 int launch_t(GemmArgs g, hipStream_t s) {
   g.n_tiles = g.N / BN;
   dim3 grid(g.N / BN, g.M / BM, g.split);
-  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(NTHREADS), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
   NE_HIP(hipGetLastError());
   if (g.split > 1) {
     if constexpr (EPI != EPI_CE_FWD) {
@@ -302,6 +315,7 @@ int launch_t(GemmArgs g, hipStream_t s) {
 
 template <typename HT, bool AKC, bool BKC, int EPI>
 int launch_e(GemmArgs g, int bm, hipStream_t s) {
+  if (bm == 256) return launch_t<HT, 256, 256, 4, 2, AKC, BKC, EPI>(g, s);
   if (bm == 128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
   return launch_t<HT, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
 }
@@ -336,10 +350,14 @@ constexpr long TARGET_WG = 512;
 
 }  // namespace
 
+// Square block tile for a shape: 256 (8 waves of 64x128) when that still gives a full wave
+// of work-groups over the 256 CUs, else 128 (4 waves of 64x64) when that gives at least
+// half a wave (split-K fills the rest), else 64.
 int gemm_tile_n(int M, int N, int K, int epi) {
   (void)K;
   (void)epi;
-  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= TARGET_WG) return 128;
+  if (M % 256 == 0 && N % 256 == 0 && (long)(M / 256) * (N / 256) >= 256) return 256;
+  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= 128) return 128;
   return 64;
 }
 

@@ -36,7 +36,8 @@ def _operands(rng, M, N, K, layout, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("layout", [0, 2, 3, 1])
-@pytest.mark.parametrize("shape", [(64, 64, 64), (128, 192, 320), (256, 4096, 1024), (1024, 1024, 256)])
+@pytest.mark.parametrize("shape", [(64, 64, 64), (128, 192, 320), (256, 4096, 1024), (1024, 1024, 256),
+                                   (2048, 1024, 4096), (4096, 4096, 128)])
 def test_gemm_f32_layouts(fmt, layout, shape):
     M, N, K = shape
     rng = np.random.default_rng(M + N + K + layout)
@@ -271,7 +272,7 @@ def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
 # --------------------------------------------------------------- cross-entropy (LM head)
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000)])
+@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768)])
 def test_fused_ce_fwd_bwd(fmt, T, D, V):
     dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(V)
