@@ -5,14 +5,17 @@
 // backward programs gen_sdpa_bwd1_noweight / gen_sdpa_bwd2 (TD/mil_dynamic.h:583-707)
 // together with the GQA tile/reduce of TD/io.h:423-430 and TD/cpu_ops.h:585-605.
 // Nothing O(S^2) is stored: the forward keeps the row log-sum-exp, the backward
-// recomputes P per tile.  GQA: kv head = q head / (NH/NKV); the dK/dV kernel loops over
-// the query heads of its kv head, so the reduction happens in registers.
+// recomputes P per tile.  GQA: kv head = q head / (NH/NKV).
 //
-// Score tiles are computed transposed where that lets the fp32 accumulator registers be
-// reused directly as the next MFMA's operand: a 16x16 accumulator gives lane l the rows
-// 4*(l/16)+i of column l%16, i.e. 4 values along the row index, which is what an
-// operand needs along K.  Two 16-row blocks give the 8 K-values of a 32-deep MFMA; the
-// other operand is read from LDS with the same K permutation.
+// Tiles of 64 keys (or queries) are staged row-major in LDS (16-byte copies, double
+// buffered through registers, one barrier per tile).  Operands that are needed transposed
+// (V^T for P.V, Q^T and dO^T for dK/dV, K^T for dQ) are read from the same row-major tiles
+// with gfx950's LDS transpose read (ds_read_b64_tr_b16): the 16 lanes of a group each give
+// the address of 4 consecutive elements, and lane i receives column i of the 4 rows.
+//
+// Score tiles are computed transposed so the fp32 accumulator of a 16x16 MFMA (lane l holds
+// rows 4*(l/16)+i of column l%16, 4 values along the row index) is re-packed in registers
+// as the next MFMA's K operand; the transposed reads use the same K permutation.
 #include "common.h"
 #include "ne_internal.h"
 
@@ -20,19 +23,33 @@ namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
-constexpr int BLK = 64;  // queries per q tile and keys per kv tile
+constexpr int BLK = 64;  // keys per kv tile, queries per q tile
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename HT>
 __device__ __forceinline__ typename HT::v8 ld8(const h16_t *p) { return HT::op(*(const u16x8 *)p); }
 
-// 8 K-values from a transposed LDS tile: columns c0..c0+3 and c1..c1+3 of one row.
-template <typename HT>
-__device__ __forceinline__ typename HT::v8 ld_pair4(const h16_t *row, int c0, int c1) {
-  const u16x4 x = *(const u16x4 *)(row + c0);
-  const u16x4 y = *(const u16x4 *)(row + c1);
+// Lane i of each 16-lane group receives tile[row0 + k][col0 + i], k = 0..3 (row pitch RP);
+// row0 / col0 may differ between the 4 groups of the wave.
+template <int RP>
+__device__ __forceinline__ u16x4 tr4(const h16_t *tile, int row0, int col0) {
+  const int m = threadIdx.x & 15;
+  const h16_t *p = tile + (row0 + (m >> 2)) * RP + col0 + 4 * (m & 3);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p);
+  return __builtin_bit_cast(u16x4, r);
+}
+
+// MFMA K operand of a transposed tile: rows (keys/queries) {32c + 4g + 0..3} then
+// {32c + 16 + 4g + 0..3} (the order pack_acc gives), column col0 + lane%16.
+template <typename HT, int RP>
+__device__ __forceinline__ typename HT::v8 tr8(const h16_t *tile, int c, int col0) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const u16x4 lo = tr4<RP>(tile, 32 * c + 4 * g, col0);
+  const u16x4 hi = tr4<RP>(tile, 32 * c + 16 + 4 * g, col0);
   u16x8 r;
-  r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3];
-  r[4] = y[0]; r[5] = y[1]; r[6] = y[2]; r[7] = y[3];
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
   return HT::op(r);
 }
 
@@ -47,28 +64,42 @@ __device__ __forceinline__ typename HT::v8 pack_acc(const f32x4 &x, const f32x4 
   return HT::op(r);
 }
 
-// Stage a 64-row x HD tile of rows t0.. (column offset col) into LDS row-major
-// (pitch RP) and/or transposed (pitch TP).
-template <int HD, int RP, int TP, bool ROW, bool TRN, int NT>
-__device__ __forceinline__ void stage_tile(const h16_t *__restrict__ src, long ld, long t0, int col,
-                                           h16_t *rows, h16_t *trn) {
-  for (int c = threadIdx.x; c < BLK * HD / 8; c += NT) {
-    const int r = c / (HD / 8), d8 = c % (HD / 8);
-    const u16x8 v = *(const u16x8 *)(src + (t0 + r) * ld + col + d8 * 8);
-    if (ROW) *(u16x8 *)(rows + r * RP + d8 * 8) = v;
-    if (TRN) {
+// Register-staged copy of 64-row x HD tiles (row-major, pitch RP) of up to two sources.
+template <int HD, int NT, int NSRC>
+struct TileCopy {
+  static constexpr int CH = BLK * HD / 8;       // 16-byte chunks per tile
+  static constexpr int PER = (CH + NT - 1) / NT;
+  u16x8 v[NSRC][PER];
+  __device__ __forceinline__ void load(int s, const h16_t *__restrict__ src, long ld, long t0, int col) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) trn[(d8 * 8 + j) * TP + r] = v[j];
+    for (int i = 0; i < PER; i++) {
+      const int c = threadIdx.x + i * NT;
+      if (CH % NT == 0 || c < CH) {
+        const int r = c / (HD / 8), d8 = c % (HD / 8);
+        v[s][i] = *(const u16x8 *)(src + (t0 + r) * ld + col + d8 * 8);
+      }
     }
   }
-}
+  template <int RP>
+  __device__ __forceinline__ void store(int s, h16_t *dst) {
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int c = threadIdx.x + i * NT;
+      if (CH % NT == 0 || c < CH) {
+        const int r = c / (HD / 8), d8 = c % (HD / 8);
+        *(u16x8 *)(dst + r * RP + d8 * 8) = v[s][i];
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------- forward ----
 
 // NW waves per block, 16 queries per wave; key tiles of 64.
 template <typename HT, int HD, int NW>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
-  __shared__ __attribute__((aligned(16))) h16_t Vt[HD * TP];
+  constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
   const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
   const int kb_last = (q0 + NW * 16 - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -87,11 +118,19 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   float m_i = -INFINITY, l_i = 0.f;
   const float sl2 = a.scale * LOG2E;
 
+  TileCopy<HD, NT, 2> cp;
+  cp.load(0, a.k, a.ldk, tb, kvh * HD);
+  cp.load(1, a.v, a.ldv, tb, kvh * HD);
+  cp.template store<RP>(0, lds[0]);
+  cp.template store<RP>(1, lds[0] + TILE);
+  __syncthreads();
   for (int kb = 0; kb <= kb_last; kb++) {
-    __syncthreads();
-    stage_tile<HD, RP, TP, true, false, NW * 64>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, nullptr);
-    stage_tile<HD, RP, TP, false, true, NW * 64>(a.v, a.ldv, tb + kb * BLK, kvh * HD, nullptr, Vt);
-    __syncthreads();
+    const int cur = kb & 1;
+    if (kb < kb_last) {
+      cp.load(0, a.k, a.ldk, tb + (kb + 1) * BLK, kvh * HD);
+      cp.load(1, a.v, a.ldv, tb + (kb + 1) * BLK, kvh * HD);
+    }
+    const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
     f32x4 s[4];
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {
@@ -131,9 +170,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
     for (int c = 0; c < 2; c++) {
       const typename HT::v8 pb = pack_acc<HT>(s[2 * c], s[2 * c + 1]);
 #pragma unroll
-      for (int d = 0; d < ND; d++)
-        acc[d] = HT::mfma16(ld_pair4<HT>(Vt + (d * 16 + c16) * TP, 2 * c * 16 + g * 4, (2 * c + 1) * 16 + g * 4), pb, acc[d]);
+      for (int d = 0; d < ND; d++) acc[d] = HT::mfma16(tr8<HT, RP>(Vs, c, d * 16), pb, acc[d]);
     }
+    if (kb < kb_last) {
+      cp.template store<RP>(0, lds[cur ^ 1]);
+      cp.template store<RP>(1, lds[cur ^ 1] + TILE);
+    }
+    __syncthreads();
   }
   const float l_tot = quad16_sum(l_i);
   const float inv = 1.f / l_tot;
@@ -146,6 +189,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   }
   if (g == 0) a.lse[tq * a.NH + h] = (m_i + log2f(l_tot)) * LN2;
 }
+
+// --------------------------------------------------------------------------- backward ----
 
 // delta[t, h] = sum_d dO[t,h,d] * O[t,h,d]
 template <typename HT, int HD>
@@ -168,20 +213,21 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
   if (row < rows && j == 0) a.delta[row] = s;
 }
 
-// NW waves per block, 16 keys per wave; query tiles of 64 from the diagonal on.
-template <typename HT, int HD, int NW>
+// dK / dV of NW*16 keys (16 per wave) of one kv head.  SPLIT: the block handles one query
+// head (blockIdx.y) and writes fp32 per-query-head partials to a.part (reduced by
+// gqa_reduce_kernel); otherwise it loops over the query heads of its kv head (blockIdx.y)
+// and writes dK (fp32) and dV (16-bit) directly.  Query tiles of 64 from the diagonal on.
+template <typename HT, int HD, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
-  constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) h16_t Qs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) h16_t dOs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) h16_t Qt[HD * TP];
-  __shared__ __attribute__((aligned(16))) h16_t dOt[HD * TP];
-  __shared__ float lse_s[BLK], dl_s[BLK];
+  constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][Q tile, dO tile]
+  __shared__ float lse_s[2][BLK], dl_s[2][BLK];
   const int nqb = a.S / BLK;
   const int k0 = blockIdx.x * NW * 16;  // smallest keys have the most query tiles: launched first
   const int qb_first = k0 / BLK;
-  const int kvh = blockIdx.y, b = blockIdx.z;
   const int ratio = a.NH / a.NKV;
+  const int kvh = SPLIT ? blockIdx.y / ratio : blockIdx.y, b = blockIdx.z;
+  const int h_begin = SPLIT ? blockIdx.y : kvh * ratio, h_end = SPLIT ? blockIdx.y + 1 : (kvh + 1) * ratio;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
@@ -198,65 +244,124 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
   for (int d = 0; d < ND; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = a.scale * LOG2E;
 
-  for (int hq = 0; hq < ratio; hq++) {
-    const int h = kvh * ratio + hq;
-    for (int qb = qb_first; qb < nqb; qb++) {
-      __syncthreads();
-      stage_tile<HD, RP, TP, true, true, NW * 64>(a.q, a.ldq, tb + qb * BLK, h * HD, Qs, Qt);
-      stage_tile<HD, RP, TP, true, true, NW * 64>(a.dout, a.lddo, tb + qb * BLK, h * HD, dOs, dOt);
-      if (threadIdx.x < BLK) {
-        const long t = tb + qb * BLK + threadIdx.x;
-        lse_s[threadIdx.x] = a.lse[t * a.NH + h] * LOG2E;
-        dl_s[threadIdx.x] = a.delta[t * a.NH + h];
-      }
-      __syncthreads();
-      f32x4 sp[4], dp[4];
+  // flattened (head, query tile) iteration with a one-tile register prefetch
+  const int per_head = nqb - qb_first;
+  const int n_it = (h_end - h_begin) * per_head;
+  TileCopy<HD, NT, 2> cp;
+  float lse_r = 0.f, dl_r = 0.f;
+  auto fetch = [&](int it) {
+    const int h = h_begin + it / per_head, qb = qb_first + it % per_head;
+    cp.load(0, a.q, a.ldq, tb + qb * BLK, h * HD);
+    cp.load(1, a.dout, a.lddo, tb + qb * BLK, h * HD);
+    if (threadIdx.x < BLK) {
+      const long t = tb + qb * BLK + threadIdx.x;
+      lse_r = a.lse[t * a.NH + h] * LOG2E;
+      dl_r = a.delta[t * a.NH + h];
+    }
+  };
+  auto put = [&](int buf) {
+    cp.template store<RP>(0, lds[buf]);
+    cp.template store<RP>(1, lds[buf] + TILE);
+    if (threadIdx.x < BLK) {
+      lse_s[buf][threadIdx.x] = lse_r;
+      dl_s[buf][threadIdx.x] = dl_r;
+    }
+  };
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int it = 0; it < n_it; it++) {
+    const int cur = it & 1;
+    const int qb = qb_first + it % per_head;
+    if (it + 1 < n_it) fetch(it + 1);
+    const h16_t *Qs = lds[cur], *dOs = lds[cur] + TILE;
+    f32x4 sp[4], dp[4];
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++) {
-        sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < 4; mb++) {
+      sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; kk++) {
-          sp[mb] = HT::mfma16(ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8), kf[kk], sp[mb]);
-          dp[mb] = HT::mfma16(ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8), vf[kk], dp[mb]);
-        }
-      }
-      // sp[mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki)
-#pragma unroll
-      for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int ql = mb * 16 + g * 4 + i;
-          float p = exp2f(sp[mb][i] * sl2 - lse_s[ql]);
-          if (qb == qb_first && ki > qb * BLK + ql) p = 0.f;
-          sp[mb][i] = p;
-          dp[mb][i] = p * (dp[mb][i] - dl_s[ql]);
-        }
-#pragma unroll
-      for (int c = 0; c < 2; c++) {
-        const typename HT::v8 pb = pack_acc<HT>(sp[2 * c], sp[2 * c + 1]);
-        const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
-        const int c0 = 2 * c * 16 + g * 4, c1 = (2 * c + 1) * 16 + g * 4;
-#pragma unroll
-        for (int d = 0; d < ND; d++) {
-          dv[d] = HT::mfma16(ld_pair4<HT>(dOt + (d * 16 + c16) * TP, c0, c1), pb, dv[d]);
-          dk[d] = HT::mfma16(ld_pair4<HT>(Qt + (d * 16 + c16) * TP, c0, c1), sb, dk[d]);
-        }
+      for (int kk = 0; kk < NK; kk++) {
+        sp[mb] = HT::mfma16(ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8), kf[kk], sp[mb]);
+        dp[mb] = HT::mfma16(ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8), vf[kk], dp[mb]);
       }
     }
+    // sp[mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki)
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int ql = mb * 16 + g * 4 + i;
+        float p = exp2f(sp[mb][i] * sl2 - lse_s[cur][ql]);
+        if (qb == qb_first && ki > qb * BLK + ql) p = 0.f;
+        sp[mb][i] = p;
+        dp[mb][i] = p * (dp[mb][i] - dl_s[cur][ql]);
+      }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const typename HT::v8 pb = pack_acc<HT>(sp[2 * c], sp[2 * c + 1]);
+      const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
+#pragma unroll
+      for (int d = 0; d < ND; d++) {
+        dv[d] = HT::mfma16(tr8<HT, RP>(dOs, c, d * 16), pb, dv[d]);
+        dk[d] = HT::mfma16(tr8<HT, RP>(Qs, c, d * 16), sb, dk[d]);
+      }
+    }
+    if (it + 1 < n_it) put(cur ^ 1);
+    __syncthreads();
   }
   // dv[d][i] = dV[key ki][dim d*16 + 4g + i]
-  bool bad = false;
+  if (SPLIT) {
+    const int h = blockIdx.y;
+    float *pk = a.part, *pv = a.part + (long)a.B * a.S * a.NH * HD;
 #pragma unroll
-  for (int d = 0; d < ND; d++) {
-    *(float4 *)(a.dk + tk * a.lddk + kvh * HD + d * 16 + g * 4) =
-        make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
-    u16x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      o[i] = HT::h(dv[d][i]);
-      bad |= HT::bad(o[i]);
+    for (int d = 0; d < ND; d++) {
+      const long o = tk * a.NH * HD + h * HD + d * 16 + g * 4;
+      *(float4 *)(pk + o) = make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
+      *(float4 *)(pv + o) = make_float4(dv[d][0], dv[d][1], dv[d][2], dv[d][3]);
     }
-    *(u16x4 *)(a.dv + tk * a.lddv + kvh * HD + d * 16 + g * 4) = o;
+  } else {
+    bool bad = false;
+#pragma unroll
+    for (int d = 0; d < ND; d++) {
+      *(float4 *)(a.dk + tk * a.lddk + kvh * HD + d * 16 + g * 4) =
+          make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
+      u16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o[i] = HT::h(dv[d][i]);
+        bad |= HT::bad(o[i]);
+      }
+      *(u16x4 *)(a.dv + tk * a.lddv + kvh * HD + d * 16 + g * 4) = o;
+    }
+    flag_overflow(a.ovf, bad);
+  }
+}
+
+// Sum of the per-query-head dK / dV partials of each kv head, in head order: dK fp32,
+// dV 16-bit.  One thread per 4 elements of [T, NKV*HD].
+template <typename HT>
+__global__ void gqa_reduce_kernel(AttnArgs a) {
+  const long n4 = (long)a.B * a.S * a.NKV * a.HD / 4;
+  const int ratio = a.NH / a.NKV;
+  const float *pk = a.part, *pv = a.part + (long)a.B * a.S * a.NH * a.HD;
+  bool bad = false;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+    const long e = i * 4;
+    const long t = e / ((long)a.NKV * a.HD);
+    const int col = (int)(e % ((long)a.NKV * a.HD));  // kvh * HD + d
+    const int kvh = col / a.HD, d = col % a.HD;
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int r = 0; r < ratio; r++) {
+      const long o = t * a.NH * a.HD + (long)(kvh * ratio + r) * a.HD + d;
+      const float4 x = *(const float4 *)(pk + o), y = *(const float4 *)(pv + o);
+      sk.x += x.x; sk.y += x.y; sk.z += x.z; sk.w += x.w;
+      sv.x += y.x; sv.y += y.y; sv.z += y.z; sv.w += y.w;
+    }
+    *(float4 *)(a.dk + t * a.lddk + col) = sk;
+    u16x4 o;
+    o[0] = HT::h(sv.x); o[1] = HT::h(sv.y); o[2] = HT::h(sv.z); o[3] = HT::h(sv.w);
+    bad |= HT::bad(o[0]) | HT::bad(o[1]) | HT::bad(o[2]) | HT::bad(o[3]);
+    *(u16x4 *)(a.dv + t * a.lddv + col) = o;
   }
   flag_overflow(a.ovf, bad);
 }
@@ -264,10 +369,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
 // NW waves per block, 16 queries per wave; key tiles of 64 up to the diagonal.
 template <typename HT, int HD, int NW>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int RP = HD + 8, TP = BLK + 4, NK = HD / 32, ND = HD / 16;
-  __shared__ __attribute__((aligned(16))) h16_t Ks[BLK * RP];
-  __shared__ __attribute__((aligned(16))) h16_t Vs[BLK * RP];
-  __shared__ __attribute__((aligned(16))) h16_t Kt[HD * TP];
+  constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
   const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
   const int kb_last = (q0 + NW * 16 - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -290,11 +393,19 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
   for (int d = 0; d < ND; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = a.scale * LOG2E;
 
+  TileCopy<HD, NT, 2> cp;
+  cp.load(0, a.k, a.ldk, tb, kvh * HD);
+  cp.load(1, a.v, a.ldv, tb, kvh * HD);
+  cp.template store<RP>(0, lds[0]);
+  cp.template store<RP>(1, lds[0] + TILE);
+  __syncthreads();
   for (int kb = 0; kb <= kb_last; kb++) {
-    __syncthreads();
-    stage_tile<HD, RP, TP, true, true, NW * 64>(a.k, a.ldk, tb + kb * BLK, kvh * HD, Ks, Kt);
-    stage_tile<HD, RP, TP, true, false, NW * 64>(a.v, a.ldv, tb + kb * BLK, kvh * HD, Vs, nullptr);
-    __syncthreads();
+    const int cur = kb & 1;
+    if (kb < kb_last) {
+      cp.load(0, a.k, a.ldk, tb + (kb + 1) * BLK, kvh * HD);
+      cp.load(1, a.v, a.ldv, tb + (kb + 1) * BLK, kvh * HD);
+    }
+    const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
     f32x4 sp[4], dp[4];
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {
@@ -317,10 +428,14 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
-      const int c0 = 2 * c * 16 + g * 4, c1 = (2 * c + 1) * 16 + g * 4;
 #pragma unroll
-      for (int d = 0; d < ND; d++) dq[d] = HT::mfma16(ld_pair4<HT>(Kt + (d * 16 + c16) * TP, c0, c1), sb, dq[d]);
+      for (int d = 0; d < ND; d++) dq[d] = HT::mfma16(tr8<HT, RP>(Ks, c, d * 16), sb, dq[d]);
     }
+    if (kb < kb_last) {
+      cp.template store<RP>(0, lds[cur ^ 1]);
+      cp.template store<RP>(1, lds[cur ^ 1] + TILE);
+    }
+    __syncthreads();
   }
   // dq[d][i] = dQ[query qi][dim d*16 + 4g + i]
 #pragma unroll
@@ -336,13 +451,9 @@ int check(const AttnArgs &a) {
   return 0;
 }
 
-}  // namespace
-
-namespace {
-
-// Single-wave blocks (NW=1) stage the same tiles with a quarter of the threads; measured
-// slower than 4-wave blocks even on short sequences, so 4 waves are used throughout.
-bool small_grid(const AttnArgs &a) { (void)a; return false; }
+// Waves per block: 4 while that still gives 256 work-groups, else 2 (short sequences would
+// leave most CUs idle; one wave would hold a whole tile pair in registers).
+int pick_nw(long units64) { return units64 >= 256 ? 4 : 2; }
 
 template <typename HT, int HD, int NW>
 int fwd_hd(const AttnArgs &a, hipStream_t s) {
@@ -351,19 +462,43 @@ int fwd_hd(const AttnArgs &a, hipStream_t s) {
   return ne_hip_status(hipGetLastError(), "attn_fwd");
 }
 
+template <typename HT, int HD>
+int fwd_nw(const AttnArgs &a, hipStream_t s) {
+  const int nw = pick_nw((long)(a.S / BLK) * a.NH * a.B);
+  if (nw == 4) return fwd_hd<HT, HD, 4>(a, s);
+  return fwd_hd<HT, HD, 2>(a, s);
+}
+
 template <typename HT>
 int fwd_t(const AttnArgs &a, hipStream_t s) {
-  const bool sm = small_grid(a);
-  if (a.HD == 128) return sm ? fwd_hd<HT, 128, 1>(a, s) : fwd_hd<HT, 128, 4>(a, s);
-  return sm ? fwd_hd<HT, 64, 1>(a, s) : fwd_hd<HT, 64, 4>(a, s);
+  if (a.HD == 128) return fwd_nw<HT, 128>(a, s);
+  return fwd_nw<HT, 64>(a, s);
 }
 
 template <typename HT, int HD, int NW>
 int bwd_hd(const AttnArgs &a, hipStream_t s) {
-  dim3 gkv(a.S / (16 * NW), a.NKV, a.B), gq(a.S / (16 * NW), a.NH, a.B);
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW>), gkv, dim3(NW * 64), 0, s, a);
+  const bool split = a.part && a.NH != a.NKV;
+  if (split) {
+    dim3 gkv(a.S / (16 * NW), a.NH, a.B);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, true>), gkv, dim3(NW * 64), 0, s, a);
+    NE_HIP(hipGetLastError());
+    const long n4 = (long)a.B * a.S * a.NKV * HD / 4;
+    hipLaunchKernelGGL(gqa_reduce_kernel<HT>, dim3((int)std::min<long>((n4 + 255) / 256, 4096)), dim3(256), 0, s, a);
+  } else {
+    dim3 gkv(a.S / (16 * NW), a.NKV, a.B);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, false>), gkv, dim3(NW * 64), 0, s, a);
+  }
+  NE_HIP(hipGetLastError());
+  dim3 gq(a.S / (16 * NW), a.NH, a.B);
   hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, HD, NW>), gq, dim3(NW * 64), 0, s, a);
   return ne_hip_status(hipGetLastError(), "attn_bwd");
+}
+
+template <typename HT, int HD>
+int bwd_nw(const AttnArgs &a, hipStream_t s) {
+  const int nw = pick_nw((long)(a.S / BLK) * a.NH * a.B);
+  if (nw == 4) return bwd_hd<HT, HD, 4>(a, s);
+  return bwd_hd<HT, HD, 2>(a, s);
 }
 
 template <typename HT>
@@ -373,9 +508,8 @@ int bwd_t(const AttnArgs &a, hipStream_t s) {
   if (a.HD == 128) hipLaunchKernelGGL((attn_delta_kernel<HT, 128>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   else hipLaunchKernelGGL((attn_delta_kernel<HT, 64>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   NE_HIP(hipGetLastError());
-  const bool sm = small_grid(a);
-  if (a.HD == 128) return sm ? bwd_hd<HT, 128, 1>(a, s) : bwd_hd<HT, 128, 4>(a, s);
-  return sm ? bwd_hd<HT, 64, 1>(a, s) : bwd_hd<HT, 64, 4>(a, s);
+  if (a.HD == 128) return bwd_nw<HT, 128>(a, s);
+  return bwd_nw<HT, 64>(a, s);
 }
 
 }  // namespace

@@ -59,7 +59,7 @@ struct ne_ctx {
   std::vector<LayerAct> act;
   float *xL, *rf;
   h16_t *xf;
-  float *dx, *dx2, *dtmp, *dq, *dk, *delta;
+  float *dx, *dx2, *dtmp, *dq, *dk, *delta, *attn_part;
   h16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
   float *ce_part, *ce_tgt, *ce_lse, *ce_rows, *loss;
   int32_t *tok_in, *tok_tgt, *tok_nxt, *tok_first;  // [T] each, one staging copy

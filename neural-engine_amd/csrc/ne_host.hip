@@ -222,6 +222,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->xL, T * D); pl.add(&c->rf, T); pl.add(&c->xf, T * D);
   pl.add(&c->dx, T * D); pl.add(&c->dx2, T * D); pl.add(&c->dtmp, T * D);
   pl.add(&c->dq, T * Q); pl.add(&c->dk, T * KV); pl.add(&c->delta, T * NH);
+  pl.add(&c->attn_part, c->NH != c->NKV ? 2 * T * Q : 1);
   pl.add(&c->dbf, T * D); pl.add(&c->dh13, T * 2 * H); pl.add(&c->dattn, T * Q); pl.add(&c->dqkv, T * QKV);
   pl.add(&c->dlogits, T * (size_t)c->V);
   pl.add(&c->ce_part, T * (size_t)(c->V / 64) * 2);
@@ -462,6 +463,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
       at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = c->dqkv + Q + KV; at.lddv = QKV;
+      at.part = c->NH != c->NKV ? c->attn_part : nullptr;
       at.ovf = ovf + OVF_DV;
       NE_CHECK(launch_attn_bwd(dt, at, c->st));
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,

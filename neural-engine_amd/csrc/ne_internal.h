@@ -104,6 +104,8 @@ struct AttnArgs {
   float *dq; long lddq;          // [T, NH*HD] fp32
   float *dk; long lddk;          // [T, NKV*HD] fp32
   h16_t *dv; long lddv;          // [T, NKV*HD] 16-bit
+  float *part;                   // nullable: [2][T, NH*HD] fp32 per-query-head dK/dV partials
+                                 // (GQA only: one block per query head, then a head-order sum)
   int *ovf;
   int B, S, NH, NKV, HD;
   float scale;
