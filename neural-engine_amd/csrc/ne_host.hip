@@ -476,8 +476,9 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
                   0, u));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, c->dbf, alpha, G + o.g_att,
-                                  u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
+      // the bottom layer needs no 16-bit copy (the embedding scatter reads the fp32 dx)
+      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, l > 0 ? c->dbf : nullptr,
+                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
     }
   }
   {

@@ -233,3 +233,27 @@ def test_decode_sampling_mfma_path():
     want = om.decode(cfg, P, prompt, 12, temperature=0.6, top_p=0.95, uniforms=u)
     np.testing.assert_array_equal(got, want)
     m.close()
+
+
+def test_step_identical_across_launch_modes():
+    """The step gives bit-identical losses and gradients over two accumulating micro-steps
+    whether its kernels are launched eagerly, replayed from a HIP graph, or launched with
+    per-kernel profiling events between them."""
+    cfg = om.tiny(**CASES["qwen3"], n_layers=2, dim=1024, hidden=4096, vocab=4096, seq=256)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2)]
+    out = []
+    for mode in ("profiled", "eager", "graph"):
+        m = ne.Model.from_oracle(cfg, batch=2)
+        m.use_graphs(mode == "graph")
+        if mode == "profiled":
+            m.prof_enable()
+        m.set_params(P)
+        losses = [m.train_step(t, 256.0) for t in toks]
+        out.append((losses, m.get_all(shapes(cfg), ne.NE_GRAD)))
+        m.close()
+    (l0, g0) = out[0]
+    for li, gi in out[1:]:
+        assert li == l0
+        for n in g0:
+            np.testing.assert_array_equal(gi[n], g0[n], err_msg=n)
