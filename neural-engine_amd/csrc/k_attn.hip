@@ -8,7 +8,8 @@
 // recomputes P per tile.  GQA: kv head = q head / (NH/NKV).
 //
 // Tiles of 64 keys (or queries) are staged row-major in LDS (16-byte copies, double
-// buffered through registers, one barrier per tile).  Operands that are needed transposed
+// buffered through registers, one barrier per tile).  A wave owns 16 or 32 rows (one or two
+// groups of 16 sharing every LDS operand read).  Operands that are needed transposed
 // (V^T for P.V, Q^T and dO^T for dK/dV, K^T for dQ) are read from the same row-major tiles
 // with gfx950's LDS transpose read (ds_read_b64_tr_b16): the 16 lanes of a group each give
 // the address of 4 consecutive elements, and lane i receives column i of the 4 rows.
@@ -95,27 +96,35 @@ struct TileCopy {
 
 // ---------------------------------------------------------------------------- forward ----
 
-// NW waves per block, 16 queries per wave; key tiles of 64.
-template <typename HT, int HD, int NW>
+// NW waves per block, RG groups of 16 queries per wave (the K/V fragments read from LDS
+// serve every group: RG = 2 halves LDS traffic per MFMA); key tiles of 64.
+template <typename HT, int HD, int NW, int RG>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  constexpr int ROWS = NW * 16 * RG;  // queries per block
   __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
-  const int kb_last = (q0 + NW * 16 - 1) / BLK;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * ROWS;  // longest rows first
+  const int kb_last = (q0 + ROWS - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (a.NH / a.NKV);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int qi = q0 + w * 16 + c16;  // this lane's query (position in sequence)
-  const long tq = tb + qi;
-  typename HT::v8 qf[NK];
+  const int qw = q0 + w * 16 * RG;  // first query of this wave
+  int qi[RG];
+  typename HT::v8 qf[RG][NK];
+  f32x4 acc[RG][ND];
+  float m_i[RG], l_i[RG];
 #pragma unroll
-  for (int kk = 0; kk < NK; kk++) qf[kk] = ld8<HT>(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
-  f32x4 acc[ND];
+  for (int r = 0; r < RG; r++) {
+    qi[r] = qw + r * 16 + c16;
 #pragma unroll
-  for (int d = 0; d < ND; d++) acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_i = -INFINITY, l_i = 0.f;
+    for (int kk = 0; kk < NK; kk++) qf[r][kk] = ld8<HT>(a.q + (tb + qi[r]) * a.ldq + h * HD + kk * 32 + g * 8);
+#pragma unroll
+    for (int d = 0; d < ND; d++) acc[r][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_i[r] = -INFINITY;
+    l_i[r] = 0.f;
+  }
   const float sl2 = a.scale * LOG2E;
 
   TileCopy<HD, NT, 2> cp;
@@ -130,47 +139,63 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
       cp.load(0, a.k, a.ldk, tb + (kb + 1) * BLK, kvh * HD);
       cp.load(1, a.v, a.ldv, tb + (kb + 1) * BLK, kvh * HD);
     }
-    const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
-    f32x4 s[4];
+    if (kb * BLK <= qw + 16 * RG - 1) {  // tiles wholly above this wave's queries add nothing
+      const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
+      f32x4 s[RG][4];
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++) {
-      s[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nb = 0; nb < 4; nb++) {
 #pragma unroll
-      for (int kk = 0; kk < NK; kk++)
-        s[nb] = HT::mfma16(ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], s[nb]);
-    }
-    // s[nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi)
-    float mx = -INFINITY;
+        for (int r = 0; r < RG; r++) s[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++)
+        for (int kk = 0; kk < NK; kk++) {
+          const typename HT::v8 kfrag = ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float v = s[nb][i] * sl2;
-        if (kb == kb_last && kb * BLK + nb * 16 + g * 4 + i > qi) v = -INFINITY;
-        s[nb][i] = v;
-        mx = fmaxf(mx, v);
+          for (int r = 0; r < RG; r++) s[r][nb] = HT::mfma16(kfrag, qf[r][kk], s[r][nb]);
+        }
       }
-    mx = quad16_max(mx);
-    const float m_new = fmaxf(m_i, mx);
-    const float alpha = exp2f(m_i - m_new);
-    m_i = m_new;
-    float ls = 0.f;
+      // s[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r])
+      typename HT::v8 pb[RG][2];
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++)
+      for (int r = 0; r < RG; r++) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float p = exp2f(s[nb][i] - m_new);
-        s[nb][i] = p;
-        ls += p;
+        for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float v = s[r][nb][i] * sl2;
+            if (kb * BLK + nb * 16 + g * 4 + i > qi[r]) v = -INFINITY;
+            s[r][nb][i] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = quad16_max(mx);
+        // every processed tile holds key kb*64 <= some query of the group's earlier tiles or
+        // key 0 (kb = 0), so m_new is finite
+        const float m_new = fmaxf(m_i[r], mx);
+        const float alpha = exp2f(m_i[r] - m_new);
+        m_i[r] = m_new;
+        float ls = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float p = exp2f(s[r][nb][i] - m_new);
+            s[r][nb][i] = p;
+            ls += p;
+          }
+        l_i[r] = l_i[r] * alpha + ls;
+#pragma unroll
+        for (int d = 0; d < ND; d++) acc[r][d] *= alpha;
+        pb[r][0] = pack_acc<HT>(s[r][0], s[r][1]);
+        pb[r][1] = pack_acc<HT>(s[r][2], s[r][3]);
       }
-    l_i = l_i * alpha + ls;
 #pragma unroll
-    for (int d = 0; d < ND; d++) acc[d] *= alpha;
+      for (int c = 0; c < 2; c++)
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const typename HT::v8 pb = pack_acc<HT>(s[2 * c], s[2 * c + 1]);
+        for (int d = 0; d < ND; d++) {
+          const typename HT::v8 vfrag = tr8<HT, RP>(Vs, c, d * 16);
 #pragma unroll
-      for (int d = 0; d < ND; d++) acc[d] = HT::mfma16(tr8<HT, RP>(Vs, c, d * 16), pb, acc[d]);
+          for (int r = 0; r < RG; r++) acc[r][d] = HT::mfma16(vfrag, pb[r][c], acc[r][d]);
+        }
     }
     if (kb < kb_last) {
       cp.template store<RP>(0, lds[cur ^ 1]);
@@ -178,16 +203,20 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
-  const float l_tot = quad16_sum(l_i);
-  const float inv = 1.f / l_tot;
 #pragma unroll
-  for (int d = 0; d < ND; d++) {
-    u16x4 o;
+  for (int r = 0; r < RG; r++) {
+    const long tq = tb + qi[r];
+    const float l_tot = quad16_sum(l_i[r]);
+    const float inv = 1.f / l_tot;
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[i] = HT::h(acc[d][i] * inv);
-    *(u16x4 *)(a.o + tq * a.ldo + h * HD + d * 16 + g * 4) = o;
+    for (int d = 0; d < ND; d++) {
+      u16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] = HT::h(acc[r][d][i] * inv);
+      *(u16x4 *)(a.o + tq * a.ldo + h * HD + d * 16 + g * 4) = o;
+    }
+    if (g == 0) a.lse[tq * a.NH + h] = (m_i[r] + log2f(l_tot)) * LN2;
   }
-  if (g == 0) a.lse[tq * a.NH + h] = (m_i + log2f(l_tot)) * LN2;
 }
 
 // --------------------------------------------------------------------------- backward ----
@@ -213,17 +242,19 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
   if (row < rows && j == 0) a.delta[row] = s;
 }
 
-// dK / dV of NW*16 keys (16 per wave) of one kv head.  SPLIT: the block handles one query
-// head (blockIdx.y) and writes fp32 per-query-head partials to a.part (reduced by
-// gqa_reduce_kernel); otherwise it loops over the query heads of its kv head (blockIdx.y)
-// and writes dK (fp32) and dV (16-bit) directly.  Query tiles of 64 from the diagonal on.
-template <typename HT, int HD, int NW, bool SPLIT>
+// dK / dV of NW*16*RG keys (RG groups of 16 per wave) of one kv head.  SPLIT: the block
+// handles one query head (blockIdx.y) and writes fp32 per-query-head partials to a.part
+// (reduced by gqa_reduce_kernel); otherwise it loops over the query heads of its kv head
+// (blockIdx.y) and writes dK (fp32) and dV (16-bit) directly.  Query tiles of 64 from the
+// block's diagonal on.
+template <typename HT, int HD, int NW, int RG, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  constexpr int ROWS = NW * 16 * RG;  // keys per block
   __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][Q tile, dO tile]
   __shared__ float lse_s[2][BLK], dl_s[2][BLK];
   const int nqb = a.S / BLK;
-  const int k0 = blockIdx.x * NW * 16;  // smallest keys have the most query tiles: launched first
+  const int k0 = blockIdx.x * ROWS;  // smallest keys have the most query tiles: launched first
   const int qb_first = k0 / BLK;
   const int ratio = a.NH / a.NKV;
   const int kvh = SPLIT ? blockIdx.y / ratio : blockIdx.y, b = blockIdx.z;
@@ -231,17 +262,22 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int ki = k0 + w * 16 + c16;  // this lane's key (as MFMA column)
-  const long tk = tb + ki;
-  typename HT::v8 kf[NK], vf[NK];
+  const int kw = k0 + w * 16 * RG;  // first key of this wave
+  int ki[RG];
+  typename HT::v8 kf[RG][NK], vf[RG][NK];
+  f32x4 dk[RG][ND], dv[RG][ND];
 #pragma unroll
-  for (int kk = 0; kk < NK; kk++) {
-    kf[kk] = ld8<HT>(a.k + tk * a.ldk + kvh * HD + kk * 32 + g * 8);
-    vf[kk] = ld8<HT>(a.v + tk * a.ldv + kvh * HD + kk * 32 + g * 8);
+  for (int r = 0; r < RG; r++) {
+    ki[r] = kw + r * 16 + c16;
+    const long tk = tb + ki[r];
+#pragma unroll
+    for (int kk = 0; kk < NK; kk++) {
+      kf[r][kk] = ld8<HT>(a.k + tk * a.ldk + kvh * HD + kk * 32 + g * 8);
+      vf[r][kk] = ld8<HT>(a.v + tk * a.ldv + kvh * HD + kk * 32 + g * 8);
+    }
+#pragma unroll
+    for (int d = 0; d < ND; d++) dk[r][d] = dv[r][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  f32x4 dk[ND], dv[ND];
-#pragma unroll
-  for (int d = 0; d < ND; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = a.scale * LOG2E;
 
   // flattened (head, query tile) iteration with a one-tile register prefetch
@@ -274,67 +310,90 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
     const int cur = it & 1;
     const int qb = qb_first + it % per_head;
     if (it + 1 < n_it) fetch(it + 1);
-    const h16_t *Qs = lds[cur], *dOs = lds[cur] + TILE;
-    f32x4 sp[4], dp[4];
+    if (qb * BLK + BLK - 1 >= kw) {  // tiles wholly below this wave's keys add nothing
+      const h16_t *Qs = lds[cur], *dOs = lds[cur] + TILE;
+      f32x4 sp[RG][4], dp[RG][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
-      sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mb = 0; mb < 4; mb++) {
 #pragma unroll
-      for (int kk = 0; kk < NK; kk++) {
-        sp[mb] = HT::mfma16(ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8), kf[kk], sp[mb]);
-        dp[mb] = HT::mfma16(ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8), vf[kk], dp[mb]);
+        for (int r = 0; r < RG; r++) sp[r][mb] = dp[r][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NK; kk++) {
+          const typename HT::v8 qfrag = ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8);
+          const typename HT::v8 ofrag = ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8);
+#pragma unroll
+          for (int r = 0; r < RG; r++) {
+            sp[r][mb] = HT::mfma16(qfrag, kf[r][kk], sp[r][mb]);
+            dp[r][mb] = HT::mfma16(ofrag, vf[r][kk], dp[r][mb]);
+          }
+        }
       }
-    }
-    // sp[mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki)
+      // sp[r][mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki[r])
+      typename HT::v8 pb[RG][2], sb[RG][2];
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++)
+      for (int r = 0; r < RG; r++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int ql = mb * 16 + g * 4 + i;
-        float p = exp2f(sp[mb][i] * sl2 - lse_s[cur][ql]);
-        if (qb == qb_first && ki > qb * BLK + ql) p = 0.f;
-        sp[mb][i] = p;
-        dp[mb][i] = p * (dp[mb][i] - dl_s[cur][ql]);
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int ql = mb * 16 + g * 4 + i;
+            float p = exp2f(sp[r][mb][i] * sl2 - lse_s[cur][ql]);
+            if (ki[r] > qb * BLK + ql) p = 0.f;
+            sp[r][mb][i] = p;
+            dp[r][mb][i] = p * (dp[r][mb][i] - dl_s[cur][ql]);
+          }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          pb[r][c] = pack_acc<HT>(sp[r][2 * c], sp[r][2 * c + 1]);
+          sb[r][c] = pack_acc<HT>(dp[r][2 * c], dp[r][2 * c + 1]);
+        }
       }
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const typename HT::v8 pb = pack_acc<HT>(sp[2 * c], sp[2 * c + 1]);
-      const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
+      for (int c = 0; c < 2; c++)
 #pragma unroll
-      for (int d = 0; d < ND; d++) {
-        dv[d] = HT::mfma16(tr8<HT, RP>(dOs, c, d * 16), pb, dv[d]);
-        dk[d] = HT::mfma16(tr8<HT, RP>(Qs, c, d * 16), sb, dk[d]);
-      }
+        for (int d = 0; d < ND; d++) {
+          const typename HT::v8 ot = tr8<HT, RP>(dOs, c, d * 16), qt = tr8<HT, RP>(Qs, c, d * 16);
+#pragma unroll
+          for (int r = 0; r < RG; r++) {
+            dv[r][d] = HT::mfma16(ot, pb[r][c], dv[r][d]);
+            dk[r][d] = HT::mfma16(qt, sb[r][c], dk[r][d]);
+          }
+        }
     }
     if (it + 1 < n_it) put(cur ^ 1);
     __syncthreads();
   }
-  // dv[d][i] = dV[key ki][dim d*16 + 4g + i]
-  if (SPLIT) {
-    const int h = blockIdx.y;
-    float *pk = a.part, *pv = a.part + (long)a.B * a.S * a.NH * HD;
+  // dv[r][d][i] = dV[key ki[r]][dim d*16 + 4g + i]
+  bool bad = false;
 #pragma unroll
-    for (int d = 0; d < ND; d++) {
-      const long o = tk * a.NH * HD + h * HD + d * 16 + g * 4;
-      *(float4 *)(pk + o) = make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
-      *(float4 *)(pv + o) = make_float4(dv[d][0], dv[d][1], dv[d][2], dv[d][3]);
-    }
-  } else {
-    bool bad = false;
+  for (int r = 0; r < RG; r++) {
+    const long tk = tb + ki[r];
+    if (SPLIT) {
+      const int h = blockIdx.y;
+      float *pk = a.part, *pv = a.part + (long)a.B * a.S * a.NH * HD;
 #pragma unroll
-    for (int d = 0; d < ND; d++) {
-      *(float4 *)(a.dk + tk * a.lddk + kvh * HD + d * 16 + g * 4) =
-          make_float4(dk[d][0] * a.scale, dk[d][1] * a.scale, dk[d][2] * a.scale, dk[d][3] * a.scale);
-      u16x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        o[i] = HT::h(dv[d][i]);
-        bad |= HT::bad(o[i]);
+      for (int d = 0; d < ND; d++) {
+        const long o = tk * a.NH * HD + h * HD + d * 16 + g * 4;
+        *(float4 *)(pk + o) = make_float4(dk[r][d][0] * a.scale, dk[r][d][1] * a.scale, dk[r][d][2] * a.scale,
+                                          dk[r][d][3] * a.scale);
+        *(float4 *)(pv + o) = make_float4(dv[r][d][0], dv[r][d][1], dv[r][d][2], dv[r][d][3]);
       }
-      *(u16x4 *)(a.dv + tk * a.lddv + kvh * HD + d * 16 + g * 4) = o;
+    } else {
+#pragma unroll
+      for (int d = 0; d < ND; d++) {
+        *(float4 *)(a.dk + tk * a.lddk + kvh * HD + d * 16 + g * 4) =
+            make_float4(dk[r][d][0] * a.scale, dk[r][d][1] * a.scale, dk[r][d][2] * a.scale, dk[r][d][3] * a.scale);
+        u16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          o[i] = HT::h(dv[r][d][i]);
+          bad |= HT::bad(o[i]);
+        }
+        *(u16x4 *)(a.dv + tk * a.lddv + kvh * HD + d * 16 + g * 4) = o;
+      }
     }
-    flag_overflow(a.ovf, bad);
   }
+  if (!SPLIT) flag_overflow(a.ovf, bad);
 }
 
 // Sum of the per-query-head dK / dV partials of each kv head, in head order: dK fp32,
@@ -366,31 +425,38 @@ __global__ void gqa_reduce_kernel(AttnArgs a) {
   flag_overflow(a.ovf, bad);
 }
 
-// NW waves per block, 16 queries per wave; key tiles of 64 up to the diagonal.
-template <typename HT, int HD, int NW>
+// NW waves per block, RG groups of 16 queries per wave; key tiles of 64 up to the diagonal.
+template <typename HT, int HD, int NW, int RG>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
+  constexpr int ROWS = NW * 16 * RG;  // queries per block
   __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * NW * 16;  // longest rows first
-  const int kb_last = (q0 + NW * 16 - 1) / BLK;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * ROWS;  // longest rows first
+  const int kb_last = (q0 + ROWS - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kvh = h / (a.NH / a.NKV);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
-  const int qi = q0 + w * 16 + c16;
-  const long tq = tb + qi;
-  typename HT::v8 qf[NK], df[NK];
+  const int qw = q0 + w * 16 * RG;
+  int qi[RG];
+  typename HT::v8 qf[RG][NK], df[RG][NK];
+  float lse2[RG], dl[RG];
+  f32x4 dq[RG][ND];
 #pragma unroll
-  for (int kk = 0; kk < NK; kk++) {
-    qf[kk] = ld8<HT>(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
-    df[kk] = ld8<HT>(a.dout + tq * a.lddo + h * HD + kk * 32 + g * 8);
+  for (int r = 0; r < RG; r++) {
+    qi[r] = qw + r * 16 + c16;
+    const long tq = tb + qi[r];
+#pragma unroll
+    for (int kk = 0; kk < NK; kk++) {
+      qf[r][kk] = ld8<HT>(a.q + tq * a.ldq + h * HD + kk * 32 + g * 8);
+      df[r][kk] = ld8<HT>(a.dout + tq * a.lddo + h * HD + kk * 32 + g * 8);
+    }
+    lse2[r] = a.lse[tq * a.NH + h] * LOG2E;
+    dl[r] = a.delta[tq * a.NH + h];
+#pragma unroll
+    for (int d = 0; d < ND; d++) dq[r][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const float lse2 = a.lse[tq * a.NH + h] * LOG2E;
-  const float dl = a.delta[tq * a.NH + h];
-  f32x4 dq[ND];
-#pragma unroll
-  for (int d = 0; d < ND; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float sl2 = a.scale * LOG2E;
 
   TileCopy<HD, NT, 2> cp;
@@ -405,31 +471,47 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
       cp.load(0, a.k, a.ldk, tb + (kb + 1) * BLK, kvh * HD);
       cp.load(1, a.v, a.ldv, tb + (kb + 1) * BLK, kvh * HD);
     }
-    const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
-    f32x4 sp[4], dp[4];
+    if (kb * BLK <= qw + 16 * RG - 1) {
+      const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
+      f32x4 sp[RG][4], dp[RG][4];
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++) {
-      sp[nb] = dp[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nb = 0; nb < 4; nb++) {
 #pragma unroll
-      for (int kk = 0; kk < NK; kk++) {
-        sp[nb] = HT::mfma16(ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8), qf[kk], sp[nb]);
-        dp[nb] = HT::mfma16(ld8<HT>(Vs + (nb * 16 + c16) * RP + kk * 32 + g * 8), df[kk], dp[nb]);
+        for (int r = 0; r < RG; r++) sp[r][nb] = dp[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NK; kk++) {
+          const typename HT::v8 kfrag = ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8);
+          const typename HT::v8 vfrag = ld8<HT>(Vs + (nb * 16 + c16) * RP + kk * 32 + g * 8);
+#pragma unroll
+          for (int r = 0; r < RG; r++) {
+            sp[r][nb] = HT::mfma16(kfrag, qf[r][kk], sp[r][nb]);
+            dp[r][nb] = HT::mfma16(vfrag, df[r][kk], dp[r][nb]);
+          }
+        }
       }
-    }
-    // sp[nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi)
+      // sp[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r])
+      typename HT::v8 sb[RG][2];
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++)
+      for (int r = 0; r < RG; r++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float p = exp2f(sp[nb][i] * sl2 - lse2);
-        if (kb == kb_last && kb * BLK + nb * 16 + g * 4 + i > qi) p = 0.f;
-        dp[nb][i] = p * (dp[nb][i] - dl);
+        for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float p = exp2f(sp[r][nb][i] * sl2 - lse2[r]);
+            if (kb * BLK + nb * 16 + g * 4 + i > qi[r]) p = 0.f;
+            dp[r][nb][i] = p * (dp[r][nb][i] - dl[r]);
+          }
+        sb[r][0] = pack_acc<HT>(dp[r][0], dp[r][1]);
+        sb[r][1] = pack_acc<HT>(dp[r][2], dp[r][3]);
       }
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const typename HT::v8 sb = pack_acc<HT>(dp[2 * c], dp[2 * c + 1]);
+      for (int c = 0; c < 2; c++)
 #pragma unroll
-      for (int d = 0; d < ND; d++) dq[d] = HT::mfma16(tr8<HT, RP>(Ks, c, d * 16), sb, dq[d]);
+        for (int d = 0; d < ND; d++) {
+          const typename HT::v8 kt = tr8<HT, RP>(Ks, c, d * 16);
+#pragma unroll
+          for (int r = 0; r < RG; r++) dq[r][d] = HT::mfma16(kt, sb[r][c], dq[r][d]);
+        }
     }
     if (kb < kb_last) {
       cp.template store<RP>(0, lds[cur ^ 1]);
@@ -437,11 +519,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
-  // dq[d][i] = dQ[query qi][dim d*16 + 4g + i]
+  // dq[r][d][i] = dQ[query qi[r]][dim d*16 + 4g + i]
 #pragma unroll
-  for (int d = 0; d < ND; d++)
-    *(float4 *)(a.dq + tq * a.lddq + h * HD + d * 16 + g * 4) =
-        make_float4(dq[d][0] * a.scale, dq[d][1] * a.scale, dq[d][2] * a.scale, dq[d][3] * a.scale);
+  for (int r = 0; r < RG; r++)
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+      *(float4 *)(a.dq + (tb + qi[r]) * a.lddq + h * HD + d * 16 + g * 4) =
+          make_float4(dq[r][d][0] * a.scale, dq[r][d][1] * a.scale, dq[r][d][2] * a.scale, dq[r][d][3] * a.scale);
 }
 
 int check(const AttnArgs &a) {
@@ -451,54 +535,70 @@ int check(const AttnArgs &a) {
   return 0;
 }
 
-// Waves per block: 4 while that still gives 256 work-groups, else 2 (short sequences would
-// leave most CUs idle; one wave would hold a whole tile pair in registers).
-int pick_nw(long units64) { return units64 >= 256 ? 4 : 2; }
+// Block shape (waves NW, 16-row groups per wave RG) by the work-group count it gives.
+// Two row groups per wave halve LDS reads per MFMA but double the accumulators: it pays for
+// the dK/dV kernel (already at one wave per SIMD) and costs the forward and dQ kernels half
+// their occupancy, so only dK/dV uses it (long sequences).  4 waves while 64-row blocks give
+// 256 work-groups, else 2 (short sequences would leave most CUs idle).
+enum { SHAPE_2x1 = 0, SHAPE_4x1 = 1, SHAPE_4x2 = 2 };
+int pick_shape(const AttnArgs &a, bool dkdv) {
+  const long units64 = (long)(a.S / BLK) * a.NH * a.B;
+  if (dkdv && a.S % 128 == 0 && units64 / 2 >= 512) return SHAPE_4x2;
+  if (units64 >= 256) return SHAPE_4x1;
+  return SHAPE_2x1;
+}
 
-template <typename HT, int HD, int NW>
+template <typename HT, int HD, int NW, int RG>
 int fwd_hd(const AttnArgs &a, hipStream_t s) {
-  dim3 grid(a.S / (16 * NW), a.NH, a.B);
-  hipLaunchKernelGGL((attn_fwd_kernel<HT, HD, NW>), grid, dim3(NW * 64), 0, s, a);
+  dim3 grid(a.S / (16 * NW * RG), a.NH, a.B);
+  hipLaunchKernelGGL((attn_fwd_kernel<HT, HD, NW, RG>), grid, dim3(NW * 64), 0, s, a);
   return ne_hip_status(hipGetLastError(), "attn_fwd");
 }
 
 template <typename HT, int HD>
-int fwd_nw(const AttnArgs &a, hipStream_t s) {
-  const int nw = pick_nw((long)(a.S / BLK) * a.NH * a.B);
-  if (nw == 4) return fwd_hd<HT, HD, 4>(a, s);
-  return fwd_hd<HT, HD, 2>(a, s);
+int fwd_shape(const AttnArgs &a, hipStream_t s) {
+  if (pick_shape(a, false) == SHAPE_4x1) return fwd_hd<HT, HD, 4, 1>(a, s);
+  return fwd_hd<HT, HD, 2, 1>(a, s);
 }
 
 template <typename HT>
 int fwd_t(const AttnArgs &a, hipStream_t s) {
-  if (a.HD == 128) return fwd_nw<HT, 128>(a, s);
-  return fwd_nw<HT, 64>(a, s);
+  if (a.HD == 128) return fwd_shape<HT, 128>(a, s);
+  return fwd_shape<HT, 64>(a, s);
 }
 
-template <typename HT, int HD, int NW>
-int bwd_hd(const AttnArgs &a, hipStream_t s) {
-  const bool split = a.part && a.NH != a.NKV;
-  if (split) {
-    dim3 gkv(a.S / (16 * NW), a.NH, a.B);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, true>), gkv, dim3(NW * 64), 0, s, a);
+template <typename HT, int HD, int NW, int RG>
+int dkdv_hd(const AttnArgs &a, hipStream_t s) {
+  const int nblk = a.S / (16 * NW * RG);
+  if (a.part && a.NH != a.NKV) {
+    dim3 gkv(nblk, a.NH, a.B);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, RG, true>), gkv, dim3(NW * 64), 0, s, a);
     NE_HIP(hipGetLastError());
     const long n4 = (long)a.B * a.S * a.NKV * HD / 4;
     hipLaunchKernelGGL(gqa_reduce_kernel<HT>, dim3((int)std::min<long>((n4 + 255) / 256, 4096)), dim3(256), 0, s, a);
   } else {
-    dim3 gkv(a.S / (16 * NW), a.NKV, a.B);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, false>), gkv, dim3(NW * 64), 0, s, a);
+    dim3 gkv(nblk, a.NKV, a.B);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, RG, false>), gkv, dim3(NW * 64), 0, s, a);
   }
-  NE_HIP(hipGetLastError());
-  dim3 gq(a.S / (16 * NW), a.NH, a.B);
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, HD, NW>), gq, dim3(NW * 64), 0, s, a);
-  return ne_hip_status(hipGetLastError(), "attn_bwd");
+  return ne_hip_status(hipGetLastError(), "attn_bwd dkdv");
+}
+
+template <typename HT, int HD, int NW, int RG>
+int dq_hd(const AttnArgs &a, hipStream_t s) {
+  dim3 gq(a.S / (16 * NW * RG), a.NH, a.B);
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, HD, NW, RG>), gq, dim3(NW * 64), 0, s, a);
+  return ne_hip_status(hipGetLastError(), "attn_bwd dq");
 }
 
 template <typename HT, int HD>
-int bwd_nw(const AttnArgs &a, hipStream_t s) {
-  const int nw = pick_nw((long)(a.S / BLK) * a.NH * a.B);
-  if (nw == 4) return bwd_hd<HT, HD, 4>(a, s);
-  return bwd_hd<HT, HD, 2>(a, s);
+int bwd_shape(const AttnArgs &a, hipStream_t s) {
+  switch (pick_shape(a, true)) {
+    case SHAPE_4x2: NE_CHECK((dkdv_hd<HT, HD, 4, 2>(a, s))); break;
+    case SHAPE_4x1: NE_CHECK((dkdv_hd<HT, HD, 4, 1>(a, s))); break;
+    default: NE_CHECK((dkdv_hd<HT, HD, 2, 1>(a, s)));
+  }
+  if (pick_shape(a, false) == SHAPE_4x1) return dq_hd<HT, HD, 4, 1>(a, s);
+  return dq_hd<HT, HD, 2, 1>(a, s);
 }
 
 template <typename HT>
@@ -508,8 +608,8 @@ int bwd_t(const AttnArgs &a, hipStream_t s) {
   if (a.HD == 128) hipLaunchKernelGGL((attn_delta_kernel<HT, 128>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   else hipLaunchKernelGGL((attn_delta_kernel<HT, 64>), dim3((thr + 255) / 256), dim3(256), 0, s, a, rows);
   NE_HIP(hipGetLastError());
-  if (a.HD == 128) return bwd_nw<HT, 128>(a, s);
-  return bwd_nw<HT, 64>(a, s);
+  if (a.HD == 128) return bwd_shape<HT, 128>(a, s);
+  return bwd_shape<HT, 64>(a, s);
 }
 
 }  // namespace

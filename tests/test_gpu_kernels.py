@@ -230,7 +230,8 @@ def _attn_ref(q, k, v, do, NH, NKV, scale):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("B,S,NH,NKV,HD", [(1, 64, 2, 2, 64), (2, 128, 4, 2, 64), (1, 256, 4, 2, 128),
-                                           (2, 192, 2, 1, 128)])
+                                           (2, 192, 2, 1, 128), (2, 512, 16, 4, 128),
+                                           (1, 1024, 64, 16, 128)])
 def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
     dt, tdt, rnd, u = FMT[fmt]
     T = B * S
