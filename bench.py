@@ -5,18 +5,21 @@ RoPE theta 1e6, SwiGLU 3072, vocab 151936, tied LM head), batch 1 x seq 256, fp3
 weights + fp16 activations, N(0, 0.02) weights from seed 0, fresh uniform token batches per
 step.  One step = ne_train_step + ne_optimizer_step (accumulation 1).
 
-Prints ONE JSON line.  `value` is training tokens/s; `roofline` is for the kernel family
-with the largest time share, timed with HIP events on the library's stream during the timed
-steps; `cpu_baseline` is the numpy oracle on this host (a bounded sample: 2 full steps of
-the same workload).  Extra keys: per-family kernel times, MFMA utilisation of the GEMM and
-attention kernels, decode tokens/s at batch 1 and 32.
+Prints ONE JSON line.  `value` is training tokens/s; `roofline` is for AdamW, the longest
+single kernel of the step, timed with HIP events on the library's stream during the timed
+steps; `cpu_baseline` is the numpy oracle on this host (a bounded sample: the median of 5
+full steps of the same workload after one warm-up).  Extra keys: per-family kernel times,
+MFMA utilisation of the GEMM and attention kernels, the same step at batch 8 x seq 2048
+(`at_scale`), decode tokens/s at batch 1 and 32.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-decode]
+                  [--no-scale] [--no-graphs] [--calib-copy]
 """
 import argparse
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -29,6 +32,9 @@ import ne  # noqa: E402
 
 PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_MFMA_16 = 2.5e15      # MI355X dense fp16/bf16 MFMA, flop/s
+# AdamW HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated)
+# on Qwen3-0.6B: equal to its algorithmic 30 B/param (profiles/adam_hbm_counters_qwen3-0.6b.md)
+ADAM_TRAFFIC_B_PER_PARAM = 30.0
 
 WORKLOADS = {
     "qwen3-0.6b-s256-b1": dict(dim=1024, hidden=3072, n_heads=16, kv_heads=8, head_dim=128, n_layers=28,
@@ -139,8 +145,9 @@ def calib_copy(nbytes=1 << 30):
     del src, dst
 
 
-def cpu_baseline(wname, w, n_steps=2):
-    """The numpy oracle (fwd + bwd + AdamW) on this host's cores for n_steps full steps."""
+def cpu_baseline(wname, w, n_runs=5):
+    """The numpy oracle (fwd + bwd + AdamW) on this host's cores: one warm-up step, then the
+    median of n_runs full steps of the same workload (about 20 s for Qwen3-0.6B, S=256)."""
     from oracle import model as om
     cfg = om.Config(dim=w["dim"], hidden=w["hidden"], n_heads=w["n_heads"], kv_heads=w["kv_heads"],
                     head_dim=w["head_dim"], n_layers=w["n_layers"], vocab=w["vocab"], seq=w["seq"],
@@ -149,19 +156,42 @@ def cpu_baseline(wname, w, n_steps=2):
     M = {k: np.zeros_like(v) for k, v in P.items()}
     V = {k: np.zeros_like(v) for k, v in P.items()}
     times = []
-    for i, tok in enumerate(batches(w, n_steps)):
+    for i, tok in enumerate(batches(w, n_runs + 1)):
         t0 = time.perf_counter()
         _, cache = om.forward(cfg, P, tok, loss_scale=256.0)
         G = om.backward(cfg, P, cache)
         del cache
         om.optimizer_step(P, G, M, V, i + 1, 3e-4, grad_scale=1.0 / 256, clip=1.0)
-        times.append(time.perf_counter() - t0)
+        if i > 0:
+            times.append(time.perf_counter() - t0)
         del G
     step_s = float(np.median(times))
-    threads = int(os.environ.get("OPENBLAS_NUM_THREADS", os.cpu_count() or 1))
+    threads, blas = os.cpu_count() or 1, "unknown"
+    try:
+        from threadpoolctl import threadpool_info
+        info = [d for d in threadpool_info() if d.get("user_api") == "blas"]
+        if info:
+            threads, blas = info[0]["num_threads"], f"{info[0]['internal_api']} {info[0].get('version')}"
+    except Exception:
+        pass
     return {"value": w["batch"] * w["seq"] / step_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n_steps} full steps (fwd+bwd+AdamW) of {wname} on the numpy oracle, "
-                      f"median {step_s:.2f} s/step, numpy BLAS threads={threads}"}
+            "sample": f"median of {n_runs} full steps (fwd+bwd+AdamW, after 1 warm-up) of {wname} on the numpy "
+                      f"oracle: {step_s:.2f} s/step; numpy BLAS {blas}, {threads} threads; "
+                      f"host CPU {platform.processor() or platform.machine()}"}
+
+
+def train_summary(w, r):
+    """Throughput, per-family kernel time and MFMA utilisation of one run_train result."""
+    fl = flops(w)
+    fam_ms = {k: v[0] / 2 for k, v in r["fam"].items()}   # ms per step (2 profiled steps)
+    mm_ms = sum(fam_ms.get(k, 0.0) for k in ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "ce"))
+    T = w["batch"] * w["seq"]
+    return {"tokens_per_s": T / (r["ms"] / 1e3), "ms_per_step": r["ms"],
+            "kernel_ms_per_step": {k: round(v, 4) for k, v in fam_ms.items()},
+            "mfma_util": {"flops_per_step": fl["total"], "gemm_attn_ms_per_step": mm_ms,
+                          "achieved_tflops": fl["total"] / (mm_ms / 1e3) / 1e12 if mm_ms else None,
+                          "frac_of_dense_peak": fl["total"] / (mm_ms / 1e3) / PEAK_MFMA_16 if mm_ms else None,
+                          "step_tflops": fl["total"] / (r["ms"] / 1e3) / 1e12}}
 
 
 def main():
@@ -172,6 +202,8 @@ def main():
     ap.add_argument("--workload", default="qwen3-0.6b-s256-b1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-scale", action="store_true",
+                    help="skip the extra Qwen3-0.6B batch 8 x seq 2048 step measurement")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a captured HIP graph "
                          "(for tracers that do not follow graph launches)")
@@ -188,17 +220,15 @@ def main():
     if a.calib_copy:
         calib_copy()
     r = run_train(w, a.steps, a.warmup, graphs=not a.no_graphs)
-    fl = flops(w)
+    summ = train_summary(w, r)
     npar = n_params(w)
-    # dominant family by time share
-    fam_ms = {k: v[0] / 2 for k, v in r["fam"].items()}   # ms per step
+    fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
     adam_ms = r["adam"][0] / max(r["adam"][1], 1)
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
-    mm_ms = sum(fam_ms.get(k, 0.0) for k in ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "ce"))
     out = {
         "metric": "Qwen3-0.6B train tokens/s + step ms on 1 MI355X; MFMA util %; decode tok/s",
-        "value": T / (r["ms"] / 1e3),
+        "value": summ["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -210,26 +240,36 @@ def main():
         "dtype": "fp16",
         "data": "synthetic: N(0,0.02) weights from seed 0, uniform token ids (fresh batch per step)",
         "config": {"workload": a.workload, "global_batch": w["batch"], "seq_len": w["seq"],
-                   "tokens_per_step": T, "params": npar, "parallelism": "single GPU",
+                   "tokens_per_step": w["batch"] * w["seq"], "params": npar, "parallelism": "single GPU",
                    "precision": "fp32 master weights + AdamW state, fp16 activations/operands, fp32 accumulate"},
-        "roofline": {"bound": "hbm", "kernel": "adam (fused AdamW over all parameters)",
+        "roofline": {"bound": "hbm", "kernel": "adam_kernel (fused AdamW over all parameters)",
                      "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM, "traffic": None,
+                     "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
+                     "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated "
+                                       "(profiles/adam_hbm_counters_qwen3-0.6b.md)",
                      "bytes_per_launch": adam_bytes, "avg_launch_ms": adam_ms},
         "dominant_family": dom,
-        "kernel_ms_per_step": {k: round(v, 4) for k, v in fam_ms.items()},
-        "mfma_util": {"flops_per_step": fl["total"], "gemm_attn_ms_per_step": mm_ms,
-                      "achieved_tflops": fl["total"] / (mm_ms / 1e3) / 1e12 if mm_ms else None,
-                      "frac_of_dense_peak": fl["total"] / (mm_ms / 1e3) / PEAK_MFMA_16 if mm_ms else None,
-                      "step_tflops": fl["total"] / (r["ms"] / 1e3) / 1e12},
+        "kernel_ms_per_step": fam_ms,
+        "mfma_util": summ["mfma_util"],
         "grad_scale": r["scale"], "skipped_steps": r["skipped"], "overflow_sites": r["sites"],
         "loss_last": r["loss"],
     }
+    if not a.no_scale and a.workload == "qwen3-0.6b-s256-b1":
+        ws = WORKLOADS["qwen3-0.6b-s2048-b8"]
+        rs = run_train(ws, 3, 1, graphs=not a.no_graphs)
+        out["at_scale"] = {"workload": "qwen3-0.6b-s2048-b8", "tokens_per_step": ws["batch"] * ws["seq"],
+                           **train_summary(ws, rs)}
     if not a.no_decode and a.workload.startswith("qwen3"):
         d1, _ = run_decode(w, 1, graphs=not a.no_graphs)
         d32, _ = run_decode(w, 32, graphs=not a.no_graphs)
+        gains = w["n_layers"] * (2 * w["dim"] + (2 * w["head_dim"] if w["qk_norm"] else 0)) + w["dim"]
+        wbytes = 2 * (npar - gains)                          # bf16 matrices read once per position
         out["decode"] = {"tokens_per_s_b1": d1, "tokens_per_s_b32": d32, "prompt": 32, "new_tokens": 200,
-                         "weights": "bf16"}
+                         "weights": "bf16",
+                         "roofline_b1": {"bound": "hbm", "bytes_per_token": wbytes,
+                                         "achieved_GBps": wbytes * d1 / 1e9,
+                                         "frac": wbytes * d1 / PEAK_HBM}}
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(a.workload, w)
     print(json.dumps(out), flush=True)
