@@ -67,24 +67,28 @@ enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2 };
 // AMX: also write the block's (max, first row) of each sequence to amv/ami [b][blockIdx.x].
 // The wave's weights (KC chunks of 512 per row, K <= 512*KC) are loaded before the input
 // prologue, so HBM latency overlaps the prologue.
-template <typename HT, int NB, int RPW, int KC, int PRO, bool AMX>
+// GATE (W1|W3 rows [2*gate_n, K]): the wave's rows are j..j+RPW/2-1 of W1 and the same j of
+// W3 (rows gate_n + j), and it writes gate[b, j] = silu(h1) * h3 (generate.py:190) instead of h1, h3.
+template <typename HT, int NB, int RPW, int KC, int PRO, bool AMX, bool GATE>
 __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict__ W, int K,
                                                         const float *__restrict__ in, long ldi,
                                                         const float *__restrict__ g, float eps, float *out, long ldo,
                                                         const float *resid, float alpha, int B, float *amv,
-                                                        int32_t *ami, int nblk) {
+                                                        int32_t *ami, int nblk, long gate_n) {
   extern __shared__ float xs[];  // [NB][K]
   __shared__ float red[4][NB];
   __shared__ float bmv[NB][4 * RPW];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const long row0 = ((long)blockIdx.x * 4 + w) * RPW;
+  constexpr int HALF = GATE ? RPW / 2 : RPW;
+  const long row0 = ((long)blockIdx.x * 4 + w) * HALF;
+  auto wrow = [&](int r) -> long { return GATE && r >= HALF ? gate_n + row0 + (r - HALF) : row0 + r; };
   u16x8 wv[RPW][KC];
 #pragma unroll
   for (int c = 0; c < KC; c++) {
     const int k = c * 512 + lane * 8;
 #pragma unroll
     for (int r = 0; r < RPW; r++)
-      if (k < K) wv[r][c] = __builtin_nontemporal_load((const u16x8 *)(W + (row0 + r) * K + k));
+      if (k < K) wv[r][c] = __builtin_nontemporal_load((const u16x8 *)(W + wrow(r) * K + k));
   }
   for (int b = 0; b < NB; b++) {
     const float *src = in + (long)b * ldi;
@@ -146,6 +150,22 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
   for (int r = 0; r < RPW; r++)
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
+  if (GATE) {
+    if (lane < HALF * NB) {
+      const int r = lane / NB, b = lane % NB;
+      float h1 = 0.f, h3 = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < HALF; rr++)
+#pragma unroll
+        for (int bb = 0; bb < NB; bb++)
+          if (rr == r && bb == b) {
+            h1 = acc[rr][bb];
+            h3 = acc[rr + HALF][bb];
+          }
+      if (b < B) out[(long)b * ldo + row0 + r] = h1 * (1.f / (1.f + expf(-h1))) * h3;
+    }
+    return;
+  }
   if (lane < RPW * NB) {
     const int r = lane / NB, b = lane % NB;
     float v = 0.f;
@@ -404,7 +424,24 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   float4 acc[RATIO];
 #pragma unroll
   for (int r = 0; r < RATIO; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int t = grp; t < npos; t += NG) {
+  // four positions per iteration: their V loads are in flight together
+  int t = grp;
+  for (; t + 3 * NG < npos; t += 4 * NG) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int tu = t + u * NG;
+      v[u] = tu == pos ? vn[c] : *(const float4 *)(V + (long)tu * HD + c * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int r = 0; r < RATIO; r++) {
+        const float p = sc[r * ctx + t + u * NG];
+        acc[r].x += p * v[u].x; acc[r].y += p * v[u].y; acc[r].z += p * v[u].z; acc[r].w += p * v[u].w;
+      }
+  }
+  for (; t < npos; t += NG) {
     const float4 v = t == pos ? vn[c] : *(const float4 *)(V + (long)t * HD + c * 4);
 #pragma unroll
     for (int r = 0; r < RATIO; r++) {
@@ -451,16 +488,16 @@ __device__ double block_sum_d(double v, double *red) {
 __device__ __forceinline__ int gen_step(const DecState *st) { return st->pos - (st->P - 1); }
 
 // Greedy from per-block partials: first index of the maximum logit (np.argmax).  One block
-// (256 threads) per sequence.
-__global__ __launch_bounds__(256) void dec_argmax_kernel(const float *__restrict__ amv, const int32_t *__restrict__ ami,
-                                                         int nblk, const DecState *__restrict__ st, int ctx,
-                                                         int32_t *tok, int32_t *out) {
-  __shared__ float rv[4];
-  __shared__ int ri[4];
+// (1024 threads) per sequence.
+__global__ __launch_bounds__(1024) void dec_argmax_kernel(const float *__restrict__ amv, const int32_t *__restrict__ ami,
+                                                          int nblk, const DecState *__restrict__ st, int ctx,
+                                                          int32_t *tok, int32_t *out) {
+  __shared__ float rv[16];
+  __shared__ int ri[16];
   const int b = blockIdx.x, tid = threadIdx.x;
   float best = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < nblk; i += 256) {
+  for (int i = tid; i < nblk; i += 1024) {
     const float v = amv[(long)b * nblk + i];
     const int j = ami[(long)b * nblk + i];
     if (v > best || (v == best && j < bi)) { best = v; bi = j; }
@@ -474,7 +511,7 @@ __global__ __launch_bounds__(256) void dec_argmax_kernel(const float *__restrict
   __syncthreads();
   if (tid == 0) {
     best = rv[0]; bi = ri[0];
-    for (int w = 1; w < 4; w++)
+    for (int w = 1; w < 16; w++)
       if (rv[w] > best || (rv[w] == best && ri[w] < bi)) { best = rv[w]; bi = ri[w]; }
     tok[b] = bi;
     out[(long)b * ctx + gen_step(st)] = bi;
@@ -605,48 +642,56 @@ int pick_rpw(int N) {
   return 1;
 }
 
-template <typename HT, int NB, int RPW, int PRO, bool AMX>
+template <typename HT, int NB, int RPW, int PRO, bool AMX, bool GATE>
 int gemv_valu_kc(const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps, float *out,
                  long ldo, const float *resid, float alpha, int B, float *amv, int32_t *ami, hipStream_t s) {
-  const int nblk = N / (4 * RPW);
+  // GATE: N counts gate outputs, each from two weight rows
+  const int nblk = GATE ? N / (4 * RPW / 2) : N / (4 * RPW);
   const size_t sh = (size_t)NB * K * sizeof(float);
+  const long gate_n = N;
   if (K <= 1024)
-    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 2, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
-                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 2, PRO, AMX, GATE>), dim3(nblk), dim3(256), sh, s, W, K, in,
+                       ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, nblk, gate_n);
   else if (K <= 2048)
-    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 4, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
-                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 4, PRO, AMX, GATE>), dim3(nblk), dim3(256), sh, s, W, K, in,
+                       ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, nblk, gate_n);
   else
-    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 6, PRO, AMX>), dim3(nblk), dim3(256), sh, s, W, K, in, ldi, g,
-                       eps, out, ldo, resid, alpha, B, amv, ami, nblk);
+    hipLaunchKernelGGL((gemv_valu_kernel<HT, NB, RPW, 6, PRO, AMX, GATE>), dim3(nblk), dim3(256), sh, s, W, K, in,
+                       ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, nblk, gate_n);
   return ne_hip_status(hipGetLastError(), "decode gemv");
 }
 
-template <typename HT, int NB, int PRO, bool AMX>
+template <typename HT, int NB, int PRO, bool AMX, bool GATE = false>
 int gemv_valu_nb(const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps, float *out,
                  long ldo, const float *resid, float alpha, int B, float *amv, int32_t *ami, hipStream_t s) {
+  if (GATE) {  // two weight rows (W1 j, W3 j) per gate output; 2 outputs per wave
+    if (N % 8) return ne_fail(NE_ERR_ARG, "decode gate gemv: hidden %d not a multiple of 8", N);
+    return gemv_valu_kc<HT, NB, 4, PRO, AMX, true>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  }
   const int rpw = pick_rpw(N);
-  if (rpw == 4) return gemv_valu_kc<HT, NB, 4, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
-  if (rpw == 2) return gemv_valu_kc<HT, NB, 2, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
-  return gemv_valu_kc<HT, NB, 1, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (rpw == 4) return gemv_valu_kc<HT, NB, 4, PRO, AMX, false>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (rpw == 2) return gemv_valu_kc<HT, NB, 2, PRO, AMX, false>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  return gemv_valu_kc<HT, NB, 1, PRO, AMX, false>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
 }
 
-template <typename HT, int PRO, bool AMX>
+template <typename HT, int PRO, bool AMX, bool GATE = false>
 int gemv_valu_pro(int B, const h16_t *W, int N, int K, const float *in, long ldi, const float *g, float eps,
                   float *out, long ldo, const float *resid, float alpha, float *amv, int32_t *ami, hipStream_t s) {
-  if (B == 1) return gemv_valu_nb<HT, 1, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
-  if (B == 2) return gemv_valu_nb<HT, 2, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
-  return gemv_valu_nb<HT, 4, PRO, AMX>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (B == 1) return gemv_valu_nb<HT, 1, PRO, AMX, GATE>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  if (B == 2) return gemv_valu_nb<HT, 2, PRO, AMX, GATE>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
+  return gemv_valu_nb<HT, 4, PRO, AMX, GATE>(W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, B, amv, ami, s);
 }
 
 // Batch <= 4: out = alpha * W . pro(in) + resid.  Requires N % 4 == 0, K % 8 == 0.
 int gemv_small(ne_ctx *c, int B, int pro, bool amx, const h16_t *W, int N, int K, const float *in, long ldi,
-               const float *g, float *out, long ldo, const float *resid, float alpha) {
+               const float *g, float *out, long ldo, const float *resid, float alpha, bool gate = false) {
   Dec *d = (Dec *)c->dec;
   if (N % 4 || K % 8 || K > 3072)
     return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%4, K%%8, K <= 3072)", N, K);
   const float eps = c->c.norm_eps;
   return DISPATCH_H16(c->dt, [&] {
+    if (pro == PRO_RMSNORM && gate)
+      return gemv_valu_pro<HT, PRO_RMSNORM, false, true>(B, W, N, K, in, ldi, g, eps, out, ldo, nullptr, 1.f, nullptr, nullptr, c->st);
     if (pro == PRO_RMSNORM) {
       if (amx) return gemv_valu_pro<HT, PRO_RMSNORM, true>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, d->amv, d->ami, c->st);
       return gemv_valu_pro<HT, PRO_RMSNORM, false>(B, W, N, K, in, ldi, g, eps, out, ldo, resid, alpha, nullptr, nullptr, c->st);
@@ -744,8 +789,10 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
     NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl));
     if (small) {
       NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.wo, D, Q, d->att, Q, nullptr, d->x, D, d->x, alpha));
-      NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.w13, 2 * H, D, d->x, D, Pf + o.g_ffn, d->h13, 2 * H, nullptr, 1.f));
-      NE_CHECK(gemv_small(c, B, PRO_SWIGLU, false, Pb + o.w2, D, H, d->h13, 2 * H, nullptr, d->x, D, d->x, alpha));
+      // W1|W3 with the SwiGLU gate in its epilogue (gate -> xn), then W2 + residual
+      NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.w13, H, D, d->x, D, Pf + o.g_ffn, d->xn, H, nullptr, 1.f,
+                          true));
+      NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.w2, D, H, d->xn, H, nullptr, d->x, D, d->x, alpha));
     } else {
       NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, d->x, D, d->x, alpha));
       hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_ffn, d->xn, D, eps);
@@ -758,7 +805,7 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
       NE_CHECK(gemv_small(c, B, PRO_RMSNORM, greedy, Pb + c->off_E, V, D, d->x, D, Pf + c->off_gfinal, d->logits, V,
                           nullptr, 1.f));
       if (greedy)
-        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(256), 0, c->st, d->amv, d->ami, V / (4 * pick_rpw(V)),
+        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(1024), 0, c->st, d->amv, d->ami, V / (4 * pick_rpw(V)),
                            d->st, d->ctx, d->tok, d->out);
     } else {
       hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + c->off_gfinal, d->xn, D, eps);
@@ -766,7 +813,7 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
       if (greedy) {
         hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(BIG_ARGMAX, B), dim3(256), 0, c->st, d->logits, V, BIG_ARGMAX,
                            d->amv, d->ami);
-        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(256), 0, c->st, d->amv, d->ami, BIG_ARGMAX, d->st, d->ctx,
+        hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(1024), 0, c->st, d->amv, d->ami, BIG_ARGMAX, d->st, d->ctx,
                            d->tok, d->out);
       }
     }
