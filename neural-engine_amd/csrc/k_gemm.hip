@@ -302,7 +302,7 @@ int launch_t(GemmArgs g, hipStream_t s) {
   dim3 grid(g.N / BN, g.M / BM, g.split);
   hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
   NE_HIP(hipGetLastError());
-  if (g.split > 1) {
+  if (g.split > 1 && !g.defer_reduce) {
     if constexpr (EPI != EPI_CE_FWD) {
       const long n4 = (long)g.M * g.N / 4;
       const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
@@ -361,7 +361,7 @@ int gemm_tile_n(int M, int N, int K, int epi) {
   return 64;
 }
 
-int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s) {
+int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
     return ne_fail(NE_ERR_ARG, "gemm: M=%d N=%d K=%d must be positive multiples of 64", g.M, g.N, g.K);
   if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
@@ -377,5 +377,6 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s) {
            (long)g.M * g.N * g.split * 2 <= g.ws_elems)
       g.split *= 2;
   }
+  if (split_out) *split_out = g.split;
   return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, bn, s));
 }

@@ -68,35 +68,106 @@ __global__ __launch_bounds__(256) void embed_bwd_chain_kernel(float *__restrict_
   }
 }
 
-// y = x * r * g, r = (mean(x^2) + eps)^-1/2   (TD/cpu_ops.h:20-60 rmsnorm)
-template <typename HT>
-__global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ g,
-                                   h16_t *__restrict__ y, float *__restrict__ rr, int T, int D,
-                                   float eps, int *ovf) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= T) return;
-  const float4 *xr = (const float4 *)(x + (long)row * D);
-  float ss = 0.f;
-  for (int i = lane; i < D / 4; i += 64) {
-    float4 v = xr[i];
-    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+// One 256-thread block per row (in flight), each thread owning float4 columns t and t + 256:
+// rows of D <= 2048 floats.  Per-row sums go through a fixed-order block reduction.
+constexpr int RMS_NT = 256, RMS_VPT = 2;
+
+// Sum over the block of one value per thread: wave sums, then the 4 wave totals in wave order.
+// `red` alternates between two slots by row parity so consecutive rows need one barrier each.
+__device__ __forceinline__ float block_sum_row(float v, float (*red)[RMS_NT / 64], int slot) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[slot][threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[slot][0] + red[slot][1] + red[slot][2] + red[slot][3];
+}
+
+// Row `row` of a split-K result, columns t and t + 256 (as float4): base + alpha * sum_z part[z].
+// The partials are added in z order (the GEMM's own reduction order) with the loads of four
+// consecutive z issued together.
+__device__ __forceinline__ void split_row(const SplitIn &sp, long row, int D, float4 (&o)[RMS_VPT]) {
+  const int D4 = D / 4, t = threadIdx.x;
+  const float4 *p = (const float4 *)(sp.part + row * D);
+  const long sl = sp.slice / 4;
+#pragma unroll
+  for (int j = 0; j < RMS_VPT; j++) o[j] = t + RMS_NT * j < D4 ? p[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  int z = 1;
+  for (; z + 3 < sp.n; z += 4) {
+    float4 q[4][RMS_VPT];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int j = 0; j < RMS_VPT; j++)
+        q[u][j] = t + RMS_NT * j < D4 ? p[(z + u) * sl + t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int j = 0; j < RMS_VPT; j++) {
+        o[j].x += q[u][j].x; o[j].y += q[u][j].y; o[j].z += q[u][j].z; o[j].w += q[u][j].w;
+      }
   }
-  ss = wave_sum(ss);
+  for (; z < sp.n; z++)
+#pragma unroll
+    for (int j = 0; j < RMS_VPT; j++)
+      if (t + RMS_NT * j < D4) {
+        const float4 q = p[z * sl + t + RMS_NT * j];
+        o[j].x += q.x; o[j].y += q.y; o[j].z += q.z; o[j].w += q.w;
+      }
+  const float4 *b = sp.base ? (const float4 *)(sp.base + row * D) : nullptr;
+#pragma unroll
+  for (int j = 0; j < RMS_VPT; j++) {
+    const float a = sp.alpha;
+    float4 v = make_float4(a * o[j].x, a * o[j].y, a * o[j].z, a * o[j].w);
+    if (b && t + RMS_NT * j < D4) {
+      const float4 q = b[t + RMS_NT * j];
+      v.x = q.x + v.x; v.y = q.y + v.y; v.z = q.z + v.z; v.w = q.w + v.w;
+    }
+    o[j] = v;
+  }
+}
+
+// y = x * r * g, r = (mean(x^2) + eps)^-1/2   (TD/cpu_ops.h:20-60 rmsnorm).  With split-K
+// partials (sp.n > 0) the row x is formed from them and written to x first.
+template <typename HT>
+__global__ __launch_bounds__(RMS_NT) void rmsnorm_fwd_kernel(float *__restrict__ x, const float *__restrict__ g,
+                                                             h16_t *__restrict__ y, float *__restrict__ rr, int D,
+                                                             float eps, int *ovf, SplitIn sp) {
+  __shared__ float red[1][RMS_NT / 64];
+  const long row = blockIdx.x;
+  const int t = threadIdx.x, D4 = D / 4;
+  float4 *xr = (float4 *)(x + row * D);
+  float4 xv[RMS_VPT];
+  if (sp.n > 0) {
+    split_row(sp, row, D, xv);
+#pragma unroll
+    for (int j = 0; j < RMS_VPT; j++)
+      if (t + RMS_NT * j < D4) xr[t + RMS_NT * j] = xv[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < RMS_VPT; j++)
+      xv[j] = t + RMS_NT * j < D4 ? xr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < RMS_VPT; j++) ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+  ss = block_sum_row(ss, red, 0);
   const float r = 1.0f / sqrtf(ss / (float)D + eps);
-  if (lane == 0) rr[row] = r;
-  u16x4 *yr = (u16x4 *)(y + (long)row * D);
+  if (t == 0) rr[row] = r;
+  u16x4 *yr = (u16x4 *)(y + row * D);
   const float4 *gv = (const float4 *)g;
   bool bad = false;
-  for (int i = lane; i < D / 4; i += 64) {
-    float4 v = xr[i], w = gv[i];
-    u16x4 o;
-    o[0] = HT::h(v.x * r * w.x);
-    o[1] = HT::h(v.y * r * w.y);
-    o[2] = HT::h(v.z * r * w.z);
-    o[3] = HT::h(v.w * r * w.w);
-    bad |= HT::bad(o[0]) | HT::bad(o[1]) | HT::bad(o[2]) | HT::bad(o[3]);
-    yr[i] = o;
+#pragma unroll
+  for (int j = 0; j < RMS_VPT; j++) {
+    const int i = t + RMS_NT * j;
+    if (i < D4) {
+      const float4 v = xv[j], w = gv[i];
+      u16x4 o;
+      o[0] = HT::h(v.x * r * w.x);
+      o[1] = HT::h(v.y * r * w.y);
+      o[2] = HT::h(v.z * r * w.z);
+      o[3] = HT::h(v.w * r * w.w);
+      bad |= HT::bad(o[0]) | HT::bad(o[1]) | HT::bad(o[2]) | HT::bad(o[3]);
+      yr[i] = o;
+    }
   }
   flag_overflow(ovf, bad);
 }
@@ -105,59 +176,65 @@ __global__ void rmsnorm_fwd_kernel(const float *__restrict__ x, const float *__r
 //   dx = r*g*dy - x*r^3*sum(dy*x*g)/D (+ resid);  dg += sum_t dy*x*r
 //   dxb = 16-bit(bscale * dx)  (the alpha-scaled operand of the next GEMM); the gain
 //   gradient is accumulated times dg_scale (removes the backward's internal scale)
-// Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).
-constexpr int RMSB_MAXV = 8;  // float4 per lane: D <= 2048
+// Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).  A block walks
+// rows_per_block rows; each thread keeps the gain-gradient sums of its own columns and
+// writes them as the block's partial row (or adds them atomically without `part`).  With
+// split-K partials (sp.n > 0) dy is formed from them.
 template <typename HT>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
+__global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
     const float *__restrict__ dy, const float *__restrict__ x, const float *__restrict__ g,
     const float *__restrict__ rr, const float *__restrict__ resid, float *__restrict__ dx,
     h16_t *__restrict__ dxb, float bscale, float *__restrict__ dg, float dg_scale, int T, int D,
-    int rows_per_block, int *ovf, float *__restrict__ part) {
-  __shared__ float red[4][2048];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int D4 = D / 4;
-  const int nv = (D4 + 63) / 64;  // float4 per lane
-  float4 acc[RMSB_MAXV];
-  for (int j = 0; j < RMSB_MAXV; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    int rows_per_block, int *ovf, float *__restrict__ part, SplitIn sp) {
+  __shared__ float red[2][RMS_NT / 64];
+  const int t = threadIdx.x, D4 = D / 4;
+  float4 acc[RMS_VPT], gw[RMS_VPT];
   const float4 *gv = (const float4 *)g;
+#pragma unroll
+  for (int j = 0; j < RMS_VPT; j++) {
+    acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    gw[j] = t + RMS_NT * j < D4 ? gv[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const float invD = 1.0f / (float)D;
   const int r0 = blockIdx.x * rows_per_block;
   const int r1 = min(T, r0 + rows_per_block);
   bool bad = false;
-  for (int row = r0 + wave; row < r1; row += 4) {
-    const float4 *dyr = (const float4 *)(dy + (long)row * D);
+  for (int row = r0; row < r1; row++) {
     const float4 *xr = (const float4 *)(x + (long)row * D);
-    const float r = rr[row];
-    float dot = 0.f;
-    float4 dyv[RMSB_MAXV], xv[RMSB_MAXV];
+    float4 dyv[RMS_VPT], xv[RMS_VPT];
+    if (sp.n > 0) {
+      split_row(sp, row, D, dyv);
+    } else {
+      const float4 *dyr = (const float4 *)(dy + (long)row * D);
 #pragma unroll
-    for (int j = 0; j < RMSB_MAXV; j++) {
-      dyv[j] = xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (j < nv && lane + 64 * j < D4) {
-        dyv[j] = dyr[lane + 64 * j];
-        xv[j] = xr[lane + 64 * j];
-        float4 w = gv[lane + 64 * j];
-        dot += dyv[j].x * xv[j].x * w.x + dyv[j].y * xv[j].y * w.y + dyv[j].z * xv[j].z * w.z +
-               dyv[j].w * xv[j].w * w.w;
-      }
+      for (int j = 0; j < RMS_VPT; j++)
+        dyv[j] = t + RMS_NT * j < D4 ? dyr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    dot = wave_sum(dot);
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < RMS_VPT; j++) {
+      xv[j] = t + RMS_NT * j < D4 ? xr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      dot += dyv[j].x * xv[j].x * gw[j].x + dyv[j].y * xv[j].y * gw[j].y + dyv[j].z * xv[j].z * gw[j].z +
+             dyv[j].w * xv[j].w * gw[j].w;
+    }
+    const float r = rr[row];
+    dot = block_sum_row(dot, red, row & 1);
     const float c = r * r * r * dot * invD;
     float4 *dxr = (float4 *)(dx + (long)row * D);
     const float4 *rsr = resid ? (const float4 *)(resid + (long)row * D) : nullptr;
     u16x4 *dbr = dxb ? (u16x4 *)(dxb + (long)row * D) : nullptr;
 #pragma unroll
-    for (int j = 0; j < RMSB_MAXV; j++) {
-      if (j < nv && lane + 64 * j < D4) {
-        const int i = lane + 64 * j;
-        float4 w = gv[i];
+    for (int j = 0; j < RMS_VPT; j++) {
+      const int i = t + RMS_NT * j;
+      if (i < D4) {
+        const float4 w = gw[j];
         float4 o;
         o.x = r * w.x * dyv[j].x - xv[j].x * c;
         o.y = r * w.y * dyv[j].y - xv[j].y * c;
         o.z = r * w.z * dyv[j].z - xv[j].z * c;
         o.w = r * w.w * dyv[j].w - xv[j].w * c;
         if (rsr) {
-          float4 q = rsr[i];
+          const float4 q = rsr[i];
           o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
         }
         dxr[i] = o;
@@ -178,22 +255,20 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     }
   }
   flag_overflow(ovf, bad);
-  // reduce the 4 waves' gain gradients, one atomic per channel per block
 #pragma unroll
-  for (int j = 0; j < RMSB_MAXV; j++) {
-    if (j < nv && lane + 64 * j < D4) {
-      const int i = (lane + 64 * j) * 4;
-      red[wave][i] = acc[j].x;
-      red[wave][i + 1] = acc[j].y;
-      red[wave][i + 2] = acc[j].z;
-      red[wave][i + 3] = acc[j].w;
+  for (int j = 0; j < RMS_VPT; j++) {
+    const int i = t + RMS_NT * j;
+    if (i < D4) {
+      const float4 v = make_float4(dg_scale * acc[j].x, dg_scale * acc[j].y, dg_scale * acc[j].z, dg_scale * acc[j].w);
+      if (part) {
+        *(float4 *)(part + (long)blockIdx.x * D + 4 * i) = v;  // reduced in block order by colsum_kernel
+      } else {
+        atomicAdd(dg + 4 * i, v.x);
+        atomicAdd(dg + 4 * i + 1, v.y);
+        atomicAdd(dg + 4 * i + 2, v.z);
+        atomicAdd(dg + 4 * i + 3, v.w);
+      }
     }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float v = dg_scale * (red[0][i] + red[1][i] + red[2][i] + red[3][i]);
-    if (part) part[(long)blockIdx.x * D + i] = v;  // reduced in block order by colsum_kernel
-    else atomicAdd(dg + i, v);
   }
 }
 
@@ -398,16 +473,18 @@ int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, co
 }
 
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D, float eps,
-                       int *ovf, hipStream_t s) {
-  if (D % 4) return ne_fail(NE_ERR_ARG, "rmsnorm: D %% 4 != 0");
+                       int *ovf, hipStream_t s, const SplitIn &sp) {
+  if (D % 4 || D > 4 * RMS_NT * RMS_VPT)
+    return ne_fail(NE_ERR_ARG, "rmsnorm: D=%d must be a multiple of 4 <= 2048", D);
+  if (T <= 0) return 0;
   return DISPATCH_H16(dt, [&] {
-    hipLaunchKernelGGL(rmsnorm_fwd_kernel<HT>, dim3((T + 3) / 4), dim3(256), 0, s, x, g, y, r, T, D, eps, ovf);
+    hipLaunchKernelGGL(rmsnorm_fwd_kernel<HT>, dim3(T), dim3(RMS_NT), 0, s, (float *)x, g, y, r, D, eps, ovf, sp);
     return ne_hip_status(hipGetLastError(), "rmsnorm_fwd");
   }());
 }
 
 namespace {
-int rms_rows(int T) { return T <= 4096 ? 4 : 32; }  // rows per block
+int rms_rows(int T) { return std::max(1, (T + 1023) / 1024); }  // rows per block: <= 1024 blocks
 int qk_tpb(int T) { return T <= 4096 ? 16 : 128; }   // tokens per block
 }  // namespace
 
@@ -418,13 +495,15 @@ long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD) {
 
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
-                       int D, int *ovf, float *part, hipStream_t s) {
-  if (D % 4 || D > 2048) return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
+                       int D, int *ovf, float *part, hipStream_t s, const SplitIn &sp) {
+  if (D % 4 || D > 4 * RMS_NT * RMS_VPT)
+    return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
+  if (T <= 0) return 0;
   const int rows = rms_rows(T);
   const int nb = (T + rows - 1) / rows;
   NE_CHECK(DISPATCH_H16(dt, [&] {
-    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3(nb), dim3(256), 0, s, dy, x, g, r, resid, dx, dxb, bscale, dg,
-                       dg_scale, T, D, rows, ovf, part);
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3(nb), dim3(RMS_NT), 0, s, dy, x, g, r, resid, dx, dxb, bscale, dg,
+                       dg_scale, T, D, rows, ovf, part, sp);
     return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
   }()));
   if (part) {

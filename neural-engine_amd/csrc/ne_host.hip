@@ -112,6 +112,32 @@ int gemm(ne_ctx *c, int fam, int site, int layout, int epi, int M, int N, int K,
   return gemm_launch(c->dt, layout, epi, g, c->st);
 }
 
+// GEMM whose split-K reduction, when it splits, is left to the kernel that consumes C:
+// *sp then describes the partials in c->ws (C unwritten), else has n = 0 (C written).  C must
+// be [M, N] row-major with ldc = N; R (EPI_RESID) is the residual added after the sum.
+int gemm_split(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, const void *A, long lda,
+               const void *B, long ldb, void *C, SplitIn *sp, const float *R = nullptr, float alpha = 1.f) {
+  ProfScope ps(c, fam);
+  GemmArgs g = {};
+  g.M = M; g.N = N; g.K = K;
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = N; g.R = R; g.ldr = N;
+  g.alpha = alpha;
+  g.ws = c->ws;
+  g.ws_elems = c->ws_elems;
+  g.defer_reduce = 1;
+  int split = 1;
+  NE_CHECK(gemm_launch(c->dt, layout, epi, g, c->st, &split));
+  *sp = SplitIn();
+  if (split > 1) {
+    sp->part = c->ws;
+    sp->n = split;
+    sp->slice = (long)M * N;
+    sp->base = R;
+    sp->alpha = alpha;
+  }
+  return 0;
+}
+
 int validate(const ne_config *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null config");
   if (c->dim <= 0 || c->hidden <= 0 || c->n_heads <= 0 || c->kv_heads <= 0 || c->head_dim <= 0 ||
@@ -390,13 +416,16 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
     ProfScope ps(c, NE_PROF_EMBED);
     NE_CHECK(launch_embed_fwd(P + c->off_E, c->tok_in, c->act[0].x_in, T, D, c->st));
   }
+  // The residual-producing GEMMs (Wo, W2) leave their split-K partials to the RMSNorm that
+  // reads their output; sp_x describes the pending partials of the next norm's input.
+  SplitIn sp_x;
   for (int l = 0; l < c->L; l++) {
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
     float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf + OVF_NORM_FWD, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_QKV, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
     {
@@ -408,21 +437,24 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       NE_CHECK(launch_attn_fwd(dt, at, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, -1, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, D, a.x_in, D, alpha));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, Q, a.attn, Q, Pb + o.wo, Q, a.x2, &sp_x,
+                        a.x_in, alpha));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf + OVF_NORM_FWD, c->st));
+      NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_H13, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf + OVF_SWIGLU, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, -1, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, D, a.x2, D, alpha));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, &sp_x,
+                        a.x2, alpha));
   }
   {
     ProfScope ps(c, NE_PROF_NORM);
-    NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf + OVF_NORM_FWD, c->st));
+    NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf + OVF_NORM_FWD, c->st,
+                                sp_x));
   }
   {
     ProfScope ps(c, NE_PROF_CE);
@@ -432,12 +464,15 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
   }
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
-  NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, D));
+  // The dX GEMMs feeding an RMSNorm backward leave their split-K partials to it (sp_d); the
+  // weight-gradient GEMM beside each runs first, since both split into the one workspace.
+  SplitIn sp_d;
   NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
+  NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, &sp_d));
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
+                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
@@ -446,13 +481,14 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DH13, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
                   a.h13, 2 * H));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H, nullptr, 0, u));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp, D));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D,
                   nullptr, 0, u));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp,
+                        &sp_d));
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
-                                  T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
+                                  T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
     }
     // attention: dbf = alpha * dx2
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DATTN, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
@@ -471,14 +507,15 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
                                   c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->gpart, c->st));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp, D));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
                   0, u));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp,
+                        &sp_d));
     {
       ProfScope ps(c, NE_PROF_NORM);
       // the bottom layer needs no 16-bit copy (the embedding scatter reads the fp32 dx)
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, l > 0 ? c->dbf : nullptr,
-                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st));
+                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
     }
   }
   {

@@ -60,9 +60,23 @@ struct GemmArgs {
   long ws_elems;             // its capacity in floats
   int n_tiles;               // set by the launcher: N / BN
   int split;                 // set by the launcher: K splits (grid.z)
+  int defer_reduce;          // with K splits, leave the fp32 partials in ws for the consumer
 };
 
-int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s);
+// Split-K partials of a GEMM whose reduction is folded into its consumer: element e of the
+// result is base[e] + alpha * sum_{z < n} part[z * slice + e] (z ascending, the order of the
+// GEMM's own reduction).  n = 0: no partials.
+struct SplitIn {
+  const float *part = nullptr;
+  int n = 0;
+  long slice = 0;
+  const float *base = nullptr;  // nullable
+  float alpha = 1.f;
+};
+
+// *split_out (nullable) receives the K splits used; with a.defer_reduce and more than one
+// split, C is not written and the partials stay in a.ws (M*N floats per split).
+int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
 int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this shape
 
 // ---- embedding / normalisation / elementwise (k_norm.hip) ----
@@ -72,15 +86,18 @@ int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale
 // Deterministic scatter over per-id row chains (nxt / first arrays built on the host).
 int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, const int32_t *first,
                            const float *dx, float scale, int T, int D, hipStream_t s);
+// With sp.n > 0, x is formed from split-K partials (SplitIn) and written to x before use.
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D,
-                       float eps, int *ovf, hipStream_t s);
+                       float eps, int *ovf, hipStream_t s, const SplitIn &sp = SplitIn());
 // Gain gradients: with `part` (scratch of *_part_elems floats) per-block partials are summed
 // in a second, ordered pass (deterministic); without it blocks add atomically.
 long rmsnorm_bwd_part_elems(int T, int D);
 long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD);
+// With sp.n > 0, dy is formed from split-K partials (SplitIn) instead of read.
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg,
-                       float dg_scale, int T, int D, int *ovf, float *part, hipStream_t s);
+                       float dg_scale, int T, int D, int *ovf, float *part, hipStream_t s,
+                       const SplitIn &sp = SplitIn());
 int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s);
 int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
                        const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq, float *rk,
