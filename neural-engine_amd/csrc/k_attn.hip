@@ -54,6 +54,15 @@ __device__ __forceinline__ typename HT::v8 tr8(const h16_t *tile, int c, int col
   return HT::op(r);
 }
 
+// 2^x by v_exp_f32 alone.  Every argument here is a score minus a running max or the row
+// log-sum-exp (<= 8, or -inf for masked keys): results below 2^-126 may flush to zero, which
+// is below the resolution of the 16-bit P and of the fp32 row sums they join.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The forward's running row max moves only when a tile's max exceeds it by more than this
+// (log2 units), so P <= 2^8 and the accumulator rescale is rare.
+constexpr float RESCALE_SLACK = 8.f;
+
 template <typename HT>
 __device__ __forceinline__ typename HT::v8 pack_acc(const f32x4 &x, const f32x4 &y) {
   u16x8 r;
@@ -66,31 +75,27 @@ __device__ __forceinline__ typename HT::v8 pack_acc(const f32x4 &x, const f32x4 
 }
 
 // Register-staged copy of 64-row x HD tiles (row-major, pitch RP) of up to two sources.
+// Thread t copies the 16-byte chunks of rows t/CPR + i*RSTEP at column (t%CPR)*8: its
+// offset within a tile is fixed, and the tile's origin is a uniform (scalar) address.
 template <int HD, int NT, int NSRC>
 struct TileCopy {
-  static constexpr int CH = BLK * HD / 8;       // 16-byte chunks per tile
-  static constexpr int PER = (CH + NT - 1) / NT;
+  static constexpr int CPR = HD / 8;      // 16-byte chunks per row
+  static constexpr int CH = BLK * CPR;    // chunks per tile
+  static constexpr int PER = CH / NT;     // chunks per thread
+  static constexpr int RSTEP = NT / CPR;  // rows between a thread's chunks
+  static_assert(NT % CPR == 0 && CH % NT == 0, "tile copy: threads must tile the 64 x HD tile");
   u16x8 v[NSRC][PER];
   __device__ __forceinline__ void load(int s, const h16_t *__restrict__ src, long ld, long t0, int col) {
+    const h16_t *b = src + t0 * ld + col;
+    const long off = (long)(threadIdx.x / CPR) * ld + (threadIdx.x % CPR) * 8;
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = threadIdx.x + i * NT;
-      if (CH % NT == 0 || c < CH) {
-        const int r = c / (HD / 8), d8 = c % (HD / 8);
-        v[s][i] = *(const u16x8 *)(src + (t0 + r) * ld + col + d8 * 8);
-      }
-    }
+    for (int i = 0; i < PER; i++) v[s][i] = *(const u16x8 *)(b + off + (long)i * RSTEP * ld);
   }
   template <int RP>
   __device__ __forceinline__ void store(int s, h16_t *dst) {
+    h16_t *d = dst + (threadIdx.x / CPR) * RP + (threadIdx.x % CPR) * 8;
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = threadIdx.x + i * NT;
-      if (CH % NT == 0 || c < CH) {
-        const int r = c / (HD / 8), d8 = c % (HD / 8);
-        *(u16x8 *)(dst + r * RP + d8 * 8) = v[s][i];
-      }
-    }
+    for (int i = 0; i < PER; i++) *(u16x8 *)(d + i * RSTEP * RP) = v[s][i];
   }
 };
 
@@ -143,48 +148,58 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
       const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
       f32x4 s[RG][4];
 #pragma unroll
-      for (int nb = 0; nb < 4; nb++) {
+      for (int nb = 0; nb < 4; nb++)
 #pragma unroll
         for (int r = 0; r < RG; r++) s[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // four independent accumulator chains per K step
 #pragma unroll
-        for (int kk = 0; kk < NK; kk++) {
+      for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
           const typename HT::v8 kfrag = ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8);
 #pragma unroll
           for (int r = 0; r < RG; r++) s[r][nb] = HT::mfma16(kfrag, qf[r][kk], s[r][nb]);
         }
-      }
-      // s[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r])
+      // s[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r]); keys above a query are
+      // masked on the tiles that cross this wave's diagonal only
+      const bool diag = kb * BLK + BLK - 1 > qw;
       typename HT::v8 pb[RG][2];
 #pragma unroll
       for (int r = 0; r < RG; r++) {
+        if (diag) {
+#pragma unroll
+          for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              if (kb * BLK + nb * 16 + g * 4 + i > qi[r]) s[r][nb][i] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int nb = 0; nb < 4; nb++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float v = s[r][nb][i] * sl2;
-            if (kb * BLK + nb * 16 + g * 4 + i > qi[r]) v = -INFINITY;
-            s[r][nb][i] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = quad16_max(mx);
+          for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[r][nb][i]);
+        mx = quad16_max(mx) * sl2;
         // every processed tile holds key kb*64 <= some query of the group's earlier tiles or
-        // key 0 (kb = 0), so m_new is finite
-        const float m_new = fmaxf(m_i[r], mx);
-        const float alpha = exp2f(m_i[r] - m_new);
-        m_i[r] = m_new;
+        // key 0 (kb = 0), so the reference max is finite after the first tile
+        if (__any(mx > m_i[r] + RESCALE_SLACK)) {
+          const float m_new = fmaxf(m_i[r], mx);
+          const float alpha = fexp2(m_i[r] - m_new);
+          m_i[r] = m_new;
+          l_i[r] *= alpha;
+#pragma unroll
+          for (int d = 0; d < ND; d++) acc[r][d] *= alpha;
+        }
+        const float nm = -m_i[r];
         float ls = 0.f;
 #pragma unroll
         for (int nb = 0; nb < 4; nb++)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const float p = exp2f(s[r][nb][i] - m_new);
+            const float p = fexp2(fmaf(s[r][nb][i], sl2, nm));
             s[r][nb][i] = p;
             ls += p;
           }
-        l_i[r] = l_i[r] * alpha + ls;
-#pragma unroll
-        for (int d = 0; d < ND; d++) acc[r][d] *= alpha;
+        l_i[r] += ls;
         pb[r][0] = pack_acc<HT>(s[r][0], s[r][1]);
         pb[r][1] = pack_acc<HT>(s[r][2], s[r][3]);
       }
@@ -314,11 +329,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
       const h16_t *Qs = lds[cur], *dOs = lds[cur] + TILE;
       f32x4 sp[RG][4], dp[RG][4];
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++) {
+      for (int mb = 0; mb < 4; mb++)
 #pragma unroll
         for (int r = 0; r < RG; r++) sp[r][mb] = dp[r][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; kk++) {
+      for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) {
           const typename HT::v8 qfrag = ld8<HT>(Qs + (mb * 16 + c16) * RP + kk * 32 + g * 8);
           const typename HT::v8 ofrag = ld8<HT>(dOs + (mb * 16 + c16) * RP + kk * 32 + g * 8);
 #pragma unroll
@@ -327,8 +344,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
             dp[r][mb] = HT::mfma16(ofrag, vf[r][kk], dp[r][mb]);
           }
         }
-      }
       // sp[r][mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki[r])
+      const bool diag = kw + 16 * RG - 1 > qb * BLK;  // some key of this wave above some query
       typename HT::v8 pb[RG][2], sb[RG][2];
 #pragma unroll
       for (int r = 0; r < RG; r++) {
@@ -337,8 +354,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const int ql = mb * 16 + g * 4 + i;
-            float p = exp2f(sp[r][mb][i] * sl2 - lse_s[cur][ql]);
-            if (ki[r] > qb * BLK + ql) p = 0.f;
+            float p = fexp2(fmaf(sp[r][mb][i], sl2, -lse_s[cur][ql]));
+            if (diag && ki[r] > qb * BLK + ql) p = 0.f;
             sp[r][mb][i] = p;
             dp[r][mb][i] = p * (dp[r][mb][i] - dl_s[cur][ql]);
           }
@@ -475,11 +492,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
       const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
       f32x4 sp[RG][4], dp[RG][4];
 #pragma unroll
-      for (int nb = 0; nb < 4; nb++) {
+      for (int nb = 0; nb < 4; nb++)
 #pragma unroll
         for (int r = 0; r < RG; r++) sp[r][nb] = dp[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; kk++) {
+      for (int kk = 0; kk < NK; kk++)
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
           const typename HT::v8 kfrag = ld8<HT>(Ks + (nb * 16 + c16) * RP + kk * 32 + g * 8);
           const typename HT::v8 vfrag = ld8<HT>(Vs + (nb * 16 + c16) * RP + kk * 32 + g * 8);
 #pragma unroll
@@ -488,8 +507,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
             dp[r][nb] = HT::mfma16(vfrag, df[r][kk], dp[r][nb]);
           }
         }
-      }
       // sp[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r])
+      const bool diag = kb * BLK + BLK - 1 > qw;  // some key of the tile above some query
       typename HT::v8 sb[RG][2];
 #pragma unroll
       for (int r = 0; r < RG; r++) {
@@ -497,8 +516,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
         for (int nb = 0; nb < 4; nb++)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            float p = exp2f(sp[r][nb][i] * sl2 - lse2[r]);
-            if (kb * BLK + nb * 16 + g * 4 + i > qi[r]) p = 0.f;
+            float p = fexp2(fmaf(sp[r][nb][i], sl2, -lse2[r]));
+            if (diag && kb * BLK + nb * 16 + g * 4 + i > qi[r]) p = 0.f;
             dp[r][nb][i] = p * (dp[r][nb][i] - dl[r]);
           }
         sb[r][0] = pack_acc<HT>(dp[r][0], dp[r][1]);
@@ -536,14 +555,15 @@ int check(const AttnArgs &a) {
 }
 
 // Block shape (waves NW, 16-row groups per wave RG) by the work-group count it gives.
-// Two row groups per wave halve LDS reads per MFMA but double the accumulators: it pays for
-// the dK/dV kernel (already at one wave per SIMD) and costs the forward and dQ kernels half
-// their occupancy, so only dK/dV uses it (long sequences).  4 waves while 64-row blocks give
-// 256 work-groups, else 2 (short sequences would leave most CUs idle).
+// Two row groups per wave halve the LDS reads per MFMA and double the accumulators: the
+// forward still fits two waves per SIMD with them (used for long sequences); the dK/dV and
+// dQ kernels would drop to one, which costs more than the LDS traffic saves, so they keep
+// one group.  4 waves while 64-row blocks give 256 work-groups, else 2 (short sequences
+// would leave most CUs idle).
 enum { SHAPE_2x1 = 0, SHAPE_4x1 = 1, SHAPE_4x2 = 2 };
-int pick_shape(const AttnArgs &a, bool dkdv) {
+int pick_shape(const AttnArgs &a) {
   const long units64 = (long)(a.S / BLK) * a.NH * a.B;
-  if (dkdv && a.S % 128 == 0 && units64 / 2 >= 512) return SHAPE_4x2;
+  if (a.S % 128 == 0 && units64 / 2 >= 512) return SHAPE_4x2;
   if (units64 >= 256) return SHAPE_4x1;
   return SHAPE_2x1;
 }
@@ -557,8 +577,11 @@ int fwd_hd(const AttnArgs &a, hipStream_t s) {
 
 template <typename HT, int HD>
 int fwd_shape(const AttnArgs &a, hipStream_t s) {
-  if (pick_shape(a, false) == SHAPE_4x1) return fwd_hd<HT, HD, 4, 1>(a, s);
-  return fwd_hd<HT, HD, 2, 1>(a, s);
+  switch (pick_shape(a)) {
+    case SHAPE_4x2: return fwd_hd<HT, HD, 4, 2>(a, s);
+    case SHAPE_4x1: return fwd_hd<HT, HD, 4, 1>(a, s);
+    default: return fwd_hd<HT, HD, 2, 1>(a, s);
+  }
 }
 
 template <typename HT>
@@ -592,12 +615,11 @@ int dq_hd(const AttnArgs &a, hipStream_t s) {
 
 template <typename HT, int HD>
 int bwd_shape(const AttnArgs &a, hipStream_t s) {
-  switch (pick_shape(a, true)) {
-    case SHAPE_4x2: NE_CHECK((dkdv_hd<HT, HD, 4, 2>(a, s))); break;
-    case SHAPE_4x1: NE_CHECK((dkdv_hd<HT, HD, 4, 1>(a, s))); break;
-    default: NE_CHECK((dkdv_hd<HT, HD, 2, 1>(a, s)));
+  if (pick_shape(a) != SHAPE_2x1) {
+    NE_CHECK((dkdv_hd<HT, HD, 4, 1>(a, s)));
+    return dq_hd<HT, HD, 4, 1>(a, s);
   }
-  if (pick_shape(a, false) == SHAPE_4x1) return dq_hd<HT, HD, 4, 1>(a, s);
+  NE_CHECK((dkdv_hd<HT, HD, 2, 1>(a, s)));
   return dq_hd<HT, HD, 2, 1>(a, s);
 }
 
