@@ -6,8 +6,9 @@
 // weight-gradient GEMM); both are staged into LDS K-contiguous so every MFMA operand is
 // one 16-byte LDS read.  M/N-contiguous tiles are transposed in registers in 4x8 blocks on
 // the way into LDS, with a thread mapping that keeps those 8-byte LDS writes free of bank
-// conflicts.  Double-buffered LDS, one barrier per K step.  Block tiles: 256x256 with 8 waves
-// (64x128 each) for large shapes, 128x128 or 64x64 with 4 waves (64x64 / 32x32) otherwise.
+// conflicts.  Double-buffered LDS, one barrier per K step.  Block tiles: 256x256 or 256x128
+// with 8 waves (64x128 / 64x64 each) for large shapes, 128x128 or 64x64 with 4 waves
+// (64x64 / 32x32) otherwise.
 //
 // Small-M shapes (a 256-token step) leave too few output tiles to fill 256 CUs, so the
 // launcher splits K over grid.z: each split writes its fp32 partial tile to a workspace
@@ -313,52 +314,64 @@ int launch_t(GemmArgs g, hipStream_t s) {
   return 0;
 }
 
+// Block tiles: 256x256 (8 waves of 64x128), 256x128 (8 waves of 64x64), 128x128 (4 waves of
+// 64x64), 64x64 (4 waves of 32x32).  The 8-wave tiles take most of a CU's LDS (one work-group
+// per CU), the 4-wave tiles fit two.
+enum { TILE_256 = 0, TILE_256x128 = 1, TILE_128 = 2, TILE_64 = 3 };
+constexpr int tile_bm(int t) { return t == TILE_256 || t == TILE_256x128 ? 256 : t == TILE_128 ? 128 : 64; }
+constexpr int tile_bn(int t) { return t == TILE_256 ? 256 : t == TILE_64 ? 64 : 128; }
+
 template <typename HT, bool AKC, bool BKC, int EPI>
-int launch_e(GemmArgs g, int bm, hipStream_t s) {
-  if (bm == 256) return launch_t<HT, 256, 256, 4, 2, AKC, BKC, EPI>(g, s);
-  if (bm == 128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
+int launch_e(GemmArgs g, int tile, hipStream_t s) {
+  if (tile == TILE_256) return launch_t<HT, 256, 256, 4, 2, AKC, BKC, EPI>(g, s);
+  if (tile == TILE_256x128) return launch_t<HT, 256, 128, 4, 2, AKC, BKC, EPI>(g, s);
+  if (tile == TILE_128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
   return launch_t<HT, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
 }
 
 template <typename HT, bool AKC, bool BKC>
-int launch_l(int epi, GemmArgs g, int bm, hipStream_t s) {
+int launch_l(int epi, GemmArgs g, int tile, hipStream_t s) {
   switch (epi) {
-    case EPI_H16: return launch_e<HT, AKC, BKC, EPI_H16>(g, bm, s);
-    case EPI_F32: return launch_e<HT, AKC, BKC, EPI_F32>(g, bm, s);
-    case EPI_F32_ACC: return launch_e<HT, AKC, BKC, EPI_F32_ACC>(g, bm, s);
-    case EPI_RESID: return launch_e<HT, AKC, BKC, EPI_RESID>(g, bm, s);
-    case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, bm, s);
-    case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, bm, s);
-    case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, bm, s);
+    case EPI_H16: return launch_e<HT, AKC, BKC, EPI_H16>(g, tile, s);
+    case EPI_F32: return launch_e<HT, AKC, BKC, EPI_F32>(g, tile, s);
+    case EPI_F32_ACC: return launch_e<HT, AKC, BKC, EPI_F32_ACC>(g, tile, s);
+    case EPI_RESID: return launch_e<HT, AKC, BKC, EPI_RESID>(g, tile, s);
+    case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, tile, s);
+    case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, tile, s);
+    case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, tile, s);
   }
   return ne_fail(NE_ERR_ARG, "gemm: unknown epilogue %d", epi);
 }
 
 template <typename HT>
-int launch_dt(int layout, int epi, GemmArgs g, int bm, hipStream_t s) {
+int launch_dt(int layout, int epi, GemmArgs g, int tile, hipStream_t s) {
   switch (layout) {
-    case 0: return launch_l<HT, true, true>(epi, g, bm, s);
-    case 1: return launch_l<HT, false, true>(epi, g, bm, s);
-    case 2: return launch_l<HT, true, false>(epi, g, bm, s);
-    case 3: return launch_l<HT, false, false>(epi, g, bm, s);
+    case 0: return launch_l<HT, true, true>(epi, g, tile, s);
+    case 1: return launch_l<HT, false, true>(epi, g, tile, s);
+    case 2: return launch_l<HT, true, false>(epi, g, tile, s);
+    case 3: return launch_l<HT, false, false>(epi, g, tile, s);
   }
   return ne_fail(NE_ERR_ARG, "gemm: unknown layout %d", layout);
 }
 
-// Work-groups wanted per GEMM: two per CU on the 256-CU MI355X.
-constexpr long TARGET_WG = 512;
+// Block tile for a shape.  256x256 when that still gives a full wave of work-groups over the
+// 256 CUs; 256x128 when that does (about), or when the output is small and K very long (the
+// LM-head dX of a short step: split-K fills the CUs and each weight tile is read once);
+// else 128x128 when that gives at least half a wave (split-K fills the rest); else 64x64.
+int gemm_tile(int M, int N, int K) {
+  const long t256 = (long)(M / 256) * (N / 256), t256x128 = (long)(M / 256) * (N / 128);
+  const long t128 = (long)(M / 128) * (N / 128);
+  if (M % 256 == 0 && N % 256 == 0 && t256 >= 256) return TILE_256;
+  if (M % 256 == 0 && N % 128 == 0 && (t256x128 >= 200 || (t128 < 128 && K >= 8192))) return TILE_256x128;
+  if (M % 128 == 0 && N % 128 == 0 && t128 >= 128) return TILE_128;
+  return TILE_64;
+}
 
 }  // namespace
 
-// Square block tile for a shape: 256 (8 waves of 64x128) when that still gives a full wave
-// of work-groups over the 256 CUs, else 128 (4 waves of 64x64) when that gives at least
-// half a wave (split-K fills the rest), else 64.
 int gemm_tile_n(int M, int N, int K, int epi) {
-  (void)K;
   (void)epi;
-  if (M % 256 == 0 && N % 256 == 0 && (long)(M / 256) * (N / 256) >= 256) return 256;
-  if (M % 128 == 0 && N % 128 == 0 && (long)(M / 128) * (N / 128) >= 128) return 128;
-  return 64;
+  return tile_bn(gemm_tile(M, N, K));
 }
 
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {
@@ -367,16 +380,18 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
   if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
     return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
-  const int bn = gemm_tile_n(g.M, g.N, g.K, epi);
-  // split K while there are too few output tiles, keeping >= 4 K steps per split
+  const int tile = gemm_tile(g.M, g.N, g.K);
+  // split K while there are too few work-groups for the 256 CUs (one per CU for the 8-wave
+  // tiles, two for the others), keeping >= 4 K steps per split
   g.split = 1;
   if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD) {
-    const long tiles = (long)(g.M / bn) * (g.N / bn);
+    const long tiles = (long)(g.M / tile_bm(tile)) * (g.N / tile_bn(tile));
+    const long target = tile_bm(tile) == 256 ? 256 : 512;
     const int nkt = g.K / 64;
-    while (tiles * g.split < TARGET_WG && nkt / (g.split * 2) >= 4 && g.split < 64 &&
+    while (tiles * g.split < target && nkt / (g.split * 2) >= 4 && g.split < 64 &&
            (long)g.M * g.N * g.split * 2 <= g.ws_elems)
       g.split *= 2;
   }
   if (split_out) *split_out = g.split;
-  return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, bn, s));
+  return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, tile, s));
 }

@@ -257,7 +257,8 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
   pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 64 MB, enough for a 256-token step's narrow GEMMs
-  c->ws_elems = std::min<long>(16L << 20, std::max<long>(4L << 20, (long)T * D * 16));
+  // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
+  c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
   pl.add(&c->gpart, (size_t)std::max(rmsnorm_bwd_part_elems(c->T, c->D),
                                      qk_prep_bwd_part_elems(c->T, c->NH, c->NKV, c->HD)));

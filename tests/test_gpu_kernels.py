@@ -37,7 +37,7 @@ def _operands(rng, M, N, K, layout, fmt):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("layout", [0, 2, 3, 1])
 @pytest.mark.parametrize("shape", [(64, 64, 64), (128, 192, 320), (256, 4096, 1024), (1024, 1024, 256),
-                                   (2048, 1024, 4096), (4096, 4096, 128)])
+                                   (2048, 1024, 4096), (4096, 4096, 128), (256, 1024, 16384), (512, 12800, 256)])
 def test_gemm_f32_layouts(fmt, layout, shape):
     M, N, K = shape
     rng = np.random.default_rng(M + N + K + layout)
