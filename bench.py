@@ -9,7 +9,8 @@ Prints ONE JSON line.  `value` is training tokens/s; `roofline` is for AdamW, th
 single kernel of the step, timed with HIP events on the library's stream during the timed
 steps; `cpu_baseline` is the numpy oracle on this host (a bounded sample: the median of 5
 full steps of the same workload after one warm-up).  Extra keys: per-family kernel times,
-MFMA utilisation of the GEMM and attention kernels, the same step at batch 8 x seq 2048
+MFMA utilisation of the GEMM and attention kernels (against the datasheet peak and the
+measured MFMA issue ceiling of ne_k_mfma_ceiling), the same step at batch 8 x seq 2048
 (`at_scale`), decode tokens/s at batch 1 and 32.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-decode]
@@ -145,6 +146,33 @@ def calib_copy(nbytes=1 << 30):
     del src, dst
 
 
+def mfma_ceiling(blocks=1024, iters=4096):
+    """Measured MFMA issue ceiling (TFLOP/s) of the fp16 32x32x16 and 16x16x32 instructions:
+    ne_k_mfma_ceiling, 4 waves per block x 8 independent chains, no memory traffic."""
+    import ctypes
+    import torch
+    L = ne.lib()
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    res = {}
+    for shape, name, fl in ((0, "mfma_32x32x16_tflops", 2 * 32 * 32 * 16), (1, "mfma_16x16x32_tflops", 2 * 16 * 16 * 32)):
+        def go():
+            rc = L.ne_k_mfma_ceiling(ne.NE_FP16, shape, blocks, iters, ctypes.c_void_p(out.data_ptr()), None)
+            if rc != 0:
+                raise ne.NEError(L.ne_last_error().decode())
+        go()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            go()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 3
+        res[name] = blocks * 4 * 8 * iters * fl / (ms / 1e3) / 1e12
+    del out
+    return res
+
+
 def cpu_baseline(wname, w, n_runs=5):
     """The numpy oracle (fwd + bwd + AdamW) on this host's cores: one warm-up step, then the
     median of n_runs full steps of the same workload (about 20 s for Qwen3-0.6B, S=256)."""
@@ -180,8 +208,9 @@ def cpu_baseline(wname, w, n_runs=5):
                       f"host CPU {platform.processor() or platform.machine()}"}
 
 
-def train_summary(w, r):
-    """Throughput, per-family kernel time and MFMA utilisation of one run_train result."""
+def train_summary(w, r, ceiling=None):
+    """Throughput, per-family kernel time and MFMA utilisation of one run_train result (against
+    the datasheet peak and, when given, the measured 32x32x16 issue ceiling in TFLOP/s)."""
     fl = flops(w)
     fam_ms = {k: v[0] / 2 for k, v in r["fam"].items()}   # ms per step (2 profiled steps)
     mm_ms = sum(fam_ms.get(k, 0.0) for k in ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "ce"))
@@ -191,6 +220,8 @@ def train_summary(w, r):
             "mfma_util": {"flops_per_step": fl["total"], "gemm_attn_ms_per_step": mm_ms,
                           "achieved_tflops": fl["total"] / (mm_ms / 1e3) / 1e12 if mm_ms else None,
                           "frac_of_dense_peak": fl["total"] / (mm_ms / 1e3) / PEAK_MFMA_16 if mm_ms else None,
+                          "frac_of_measured_ceiling": (fl["total"] / (mm_ms / 1e3) / (ceiling * 1e12)
+                                                       if mm_ms and ceiling else None),
                           "step_tflops": fl["total"] / (r["ms"] / 1e3) / 1e12}}
 
 
@@ -217,10 +248,12 @@ def main():
         sys.exit(2)
     w = WORKLOADS[a.workload]
     T = w["batch"] * w["seq"]
+    # torch (its own HIP runtime) must initialise the device before the library does
     if a.calib_copy:
         calib_copy()
+    ceil = mfma_ceiling()
     r = run_train(w, a.steps, a.warmup, graphs=not a.no_graphs)
-    summ = train_summary(w, r)
+    summ = train_summary(w, r, ceil["mfma_32x32x16_tflops"])
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
@@ -252,6 +285,9 @@ def main():
         "dominant_family": dom,
         "kernel_ms_per_step": fam_ms,
         "mfma_util": summ["mfma_util"],
+        "mfma_ceiling": {**ceil, "datasheet_tflops": PEAK_MFMA_16 / 1e12,
+                         "how": "ne_k_mfma_ceiling: 1024 blocks x 4 waves x 8 independent fp16 MFMA chains, "
+                                "no memory traffic"},
         "grad_scale": r["scale"], "skipped_steps": r["skipped"], "overflow_sites": r["sites"],
         "loss_last": r["loss"],
     }
@@ -259,7 +295,7 @@ def main():
         ws = WORKLOADS["qwen3-0.6b-s2048-b8"]
         rs = run_train(ws, 3, 1, graphs=not a.no_graphs)
         out["at_scale"] = {"workload": "qwen3-0.6b-s2048-b8", "tokens_per_step": ws["batch"] * ws["seq"],
-                           **train_summary(ws, rs)}
+                           **train_summary(ws, rs, ceil["mfma_32x32x16_tflops"])}
     if not a.no_decode and a.workload.startswith("qwen3"):
         d1, _ = run_decode(w, 1, graphs=not a.no_graphs)
         d32, _ = run_decode(w, 32, graphs=not a.no_graphs)

@@ -241,6 +241,13 @@ int ne_k_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, 
                    void *stream);
 /* gate[T,H] = silu(h1)*h3 with h13 = [h1 | h3] rows [T,2H] (TD/mil_dynamic.h:276-281). */
 int ne_k_swiglu_fwd(int dtype, const void *h13, void *gate, int T, int H, void *stream);
+/* MFMA issue ceiling, a measurement kernel with no counterpart in the reference (its
+ * roofline figures are quoted against it next to the datasheet peak): `blocks` work-groups
+ * of 4 waves, each wave running 8 independent accumulator chains of `iters` MFMAs of the
+ * 16-bit format with no memory traffic in the loop; shape 0 = 32x32x16, 1 = 16x16x32.
+ * out: blocks*256 floats (written so the work is kept).  Flops per launch:
+ * blocks * 4 * 8 * iters * (2*32*32*16 or 2*16*16*32). */
+int ne_k_mfma_ceiling(int dtype, int shape, int blocks, int iters, float *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -173,3 +173,8 @@ extern "C" int ne_k_swiglu_fwd(int dtype, const void *h13, void *gate, int T, in
   CHECK_DT(dtype);
   return launch_swiglu_fwd(dtype, (const h16_t *)h13, (h16_t *)gate, T, H, nullptr, S(stream));
 }
+
+extern "C" int ne_k_mfma_ceiling(int dtype, int shape, int blocks, int iters, float *out, void *stream) {
+  CHECK_DT(dtype);
+  return launch_mfma_ceiling(dtype, shape, blocks, iters, out, S(stream));
+}

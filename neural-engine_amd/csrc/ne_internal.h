@@ -78,6 +78,8 @@ struct SplitIn {
 // split, C is not written and the partials stay in a.ws (M*N floats per split).
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
 int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this shape
+// Measurement kernel: MFMA chains without memory traffic (shape 0 = 32x32x16, 1 = 16x16x32).
+int launch_mfma_ceiling(int dt, int shape, int blocks, int iters, float *out, hipStream_t s);
 
 // ---- embedding / normalisation / elementwise (k_norm.hip) ----
 int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D, hipStream_t s);

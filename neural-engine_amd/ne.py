@@ -32,7 +32,7 @@ EXPORTS = (
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
-    "ne_k_embed_bwd", "ne_k_swiglu_fwd",
+    "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
 )
 
 
@@ -102,6 +102,7 @@ def lib():
         "ne_k_embed_fwd": (I, [P, P, P, I, I, P]),
         "ne_k_embed_bwd": (I, [P, P, P, F, I, I, P]),
         "ne_k_swiglu_fwd": (I, [I, P, P, I, I, P]),
+        "ne_k_mfma_ceiling": (I, [I, I, I, I, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(h, name)
