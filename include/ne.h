@@ -142,6 +142,16 @@ int ne_save_ckpt_v4(ne_ctx *ctx, const char *path, const ne_train_state *st);
 
 /* ------------------------------------------------------------- token loop ---- */
 
+/* Vocabulary compaction (TD/cpu_ops.h:384-431; used at TD/train.m:286-292, 401, 497-523,
+ * 802): the classifier and the softmax run over the embedding rows ids[0..cv) only (compact
+ * id c stands for full id ids[c]); every target must be among them; the compact embedding
+ * gradient is added back to its rows of the full one.  The reference builds ids from the
+ * training data: the distinct ids in ascending order.  ids must be distinct and in
+ * [0, vocab).  cv = 0 (ids NULL) restores the full vocabulary.  Call before a step that
+ * starts an accumulation window (after ne_optimizer_step or ne_zero_grads); returns
+ * NE_ERR_STATE otherwise. */
+int ne_set_vocab_map(ne_ctx *ctx, const int32_t *ids, int cv);
+
 /* KV-cached autoregressive generation (TD/tools/generate.py:113-228) for B sequences
  * sharing one prompt length P: prompt is [B, P] int32, out_tokens receives [B, n_new].
  * temperature < 1e-6 selects greedy argmax; otherwise softmax(logits/temperature), an

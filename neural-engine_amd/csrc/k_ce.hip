@@ -43,7 +43,45 @@ __global__ void mean_kernel(const float *__restrict__ x, int n, float *__restric
   }
 }
 
+// dst[r, :] = src[ids[r], :], 16-bit rows of D (D % 8 == 0): one block per row.
+__global__ void gather_rows16_kernel(const h16_t *__restrict__ src, const int32_t *__restrict__ ids,
+                                     h16_t *__restrict__ dst, int D) {
+  const long r = blockIdx.x;
+  const u16x8 *s8 = (const u16x8 *)(src + (long)ids[r] * D);
+  u16x8 *d8 = (u16x8 *)(dst + r * D);
+  for (int i = threadIdx.x; i < D / 8; i += blockDim.x) d8[i] = s8[i];
+}
+
+// G[ids[r], :] += src[r, :], fp32 rows of D (D % 4 == 0): one block per row; the ids are
+// distinct, so no two blocks touch the same row.
+__global__ void scatter_add_rows_kernel(float *__restrict__ G, const float *__restrict__ src,
+                                        const int32_t *__restrict__ ids, int D) {
+  const long r = blockIdx.x;
+  float4 *g4 = (float4 *)(G + (long)ids[r] * D);
+  const float4 *s4 = (const float4 *)(src + r * D);
+  for (int i = threadIdx.x; i < D / 4; i += blockDim.x) {
+    float4 a = g4[i];
+    const float4 b = s4[i];
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    g4[i] = a;
+  }
+}
+
 }  // namespace
+
+int launch_gather_rows16(const h16_t *src, const int32_t *ids, h16_t *dst, int n, int D, hipStream_t s) {
+  if (D % 8) return ne_fail(NE_ERR_ARG, "gather_rows16: D=%d must be a multiple of 8", D);
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(gather_rows16_kernel, dim3(n), dim3(128), 0, s, src, ids, dst, D);
+  return ne_hip_status(hipGetLastError(), "gather_rows16");
+}
+
+int launch_scatter_add_rows(float *G, const float *src, const int32_t *ids, int n, int D, hipStream_t s) {
+  if (D % 4) return ne_fail(NE_ERR_ARG, "scatter_add_rows: D=%d must be a multiple of 4", D);
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(scatter_add_rows_kernel, dim3(n), dim3(256), 0, s, G, src, ids, D);
+  return ne_hip_status(hipGetLastError(), "scatter_add_rows");
+}
 
 int launch_ce_reduce(const float *part, int n_tiles, const float *tgt_logit, float *lse,
                      float *loss_rows, float *loss, int T, hipStream_t s) {

@@ -116,7 +116,7 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
     d[col] = o1;
     d[g.N + col] = o3;
   } else if constexpr (EPI == EPI_CE_BWD) {
-    float p = __expf(v - g.lse[row]);
+    float p = col < g.n_valid ? __expf(v - g.lse[row]) : 0.f;  // padding columns: no gradient
     if (col == g.targets[row]) p -= 1.f;
     const h16_t o = HT::h(p * g.scale);
     bad |= HT::bad(o);
@@ -206,17 +206,21 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-          const float v = acc[i][j][e] * alpha;
-          mx = fmaxf(mx, v);
           const int col = n0 + wn * TN + j * 32 + (lane & 31);
+          // padding columns (>= n_valid) take no part in the softmax
+          const float v = col < g.n_valid ? acc[i][j][e] * alpha : -INFINITY;
+          acc[i][j][e] = v;
+          mx = fmaxf(mx, v);
           if (col == tgt) g.tgt_logit[row] = v;
         }
         // reduce over the 32 lanes sharing this row (lanes with equal lane>>5)
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
         float s = 0.f;
+        if (mx > -INFINITY) {
 #pragma unroll
-        for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] * alpha - mx);
+          for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] - mx);
+        }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         if ((lane & 31) == 0) {
@@ -232,7 +236,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
       for (int w = 1; w < WN; w++) mx = fmaxf(mx, red_m[w][r]);
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < WN; w++) s += red_s[w][r] * __expf(red_m[w][r] - mx);
+      for (int w = 0; w < WN; w++)
+        if (red_m[w][r] > -INFINITY) s += red_s[w][r] * __expf(red_m[w][r] - mx);
       float *p = g.part + ((long)(m0 + r) * g.n_tiles + blockIdx.x) * 2;
       p[0] = mx;
       p[1] = s;

@@ -104,25 +104,29 @@ extern "C" int ne_k_attn_bwd(int dtype, const void *q, int64_t ldq, const void *
   return launch_attn_bwd(dtype, a, S(stream));
 }
 
-int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, float *part,
-               float *tgt_logit, float *lse, float *loss_rows, float *loss, hipStream_t s) {
+int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, int n_valid,
+               float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss, hipStream_t s) {
+  if (n_valid <= 0 || n_valid > V) return ne_fail(NE_ERR_ARG, "ce: %d valid columns of %d", n_valid, V);
   GemmArgs g = {};
   g.M = T; g.N = V; g.K = D;
   g.A = x; g.lda = D; g.B = E; g.ldb = D;
   g.alpha = 1.f;
   g.targets = targets; g.part = part; g.tgt_logit = tgt_logit;
+  g.n_valid = n_valid;
   NE_CHECK(gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s));
   return launch_ce_reduce(part, V / gemm_tile_n(T, V, D, EPI_CE_FWD), tgt_logit, lse, loss_rows, loss, T, s);
 }
 
 int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D,
-                int V, float scale, void *dlogits, int *ovf, hipStream_t s) {
+                int V, int n_valid, float scale, void *dlogits, int *ovf, hipStream_t s) {
+  if (n_valid <= 0 || n_valid > V) return ne_fail(NE_ERR_ARG, "ce: %d valid columns of %d", n_valid, V);
   GemmArgs g = {};
   g.M = T; g.N = V; g.K = D;
   g.A = x; g.lda = D; g.B = E; g.ldb = D;
   g.C = dlogits; g.ldc = V;
   g.alpha = 1.f; g.scale = scale;
   g.targets = targets; g.lse = lse; g.ovf = ovf;
+  g.n_valid = n_valid;
   return gemm_launch(dt, GEMM_NT, EPI_CE_BWD, g, s);
 }
 
@@ -130,13 +134,13 @@ extern "C" int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_
                            float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                            void *stream) {
   CHECK_DT(dtype);
-  return ce_forward(dtype, x, E, targets, T, D, V, part, tgt_logit, lse, loss_rows, loss, S(stream));
+  return ce_forward(dtype, x, E, targets, T, D, V, V, part, tgt_logit, lse, loss_rows, loss, S(stream));
 }
 
 extern "C" int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_t *targets, const float *lse,
                            int T, int D, int V, float scale, void *dlogits, void *stream) {
   CHECK_DT(dtype);
-  return ce_backward(dtype, x, E, targets, lse, T, D, V, scale, dlogits, nullptr, S(stream));
+  return ce_backward(dtype, x, E, targets, lse, T, D, V, V, scale, dlogits, nullptr, S(stream));
 }
 
 extern "C" int ne_k_adam(int dtype, float *p, float *g, float *m, float *v, void *pb, int64_t n,

@@ -85,6 +85,13 @@ struct ne_ctx {
   int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};
   Prof prof;
+  // vocabulary compaction: the classifier covers cv embedding rows (cvp = cv rounded up to
+  // 64, the padding columns masked out of the softmax)
+  int cv = 0, cvp = 0;
+  int32_t *cids = nullptr;   // device [cvp] full ids of the compact rows (padding repeats ids[0])
+  h16_t *cE = nullptr;       // device [cvp, D] 16-bit compact embedding, gathered each step
+  float *gcE = nullptr;      // device [cvp, D] compact embedding gradient
+  std::vector<int32_t> f2c;  // host [V] full -> compact id, -1 outside
   // token loop (k_decode.hip)
   void *dec = nullptr;
 };

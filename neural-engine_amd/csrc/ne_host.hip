@@ -320,6 +320,9 @@ extern "C" void ne_destroy(ne_ctx *c) {
   }
   for (auto e : c->prof.pool) hipEventDestroy(e);
   if (c->arena) hipFree(c->arena);
+  if (c->cids) hipFree(c->cids);
+  if (c->cE) hipFree(c->cE);
+  if (c->gcE) hipFree(c->gcE);
   if (c->h_tok) hipHostFree(c->h_tok);
   if (c->h_scalar) hipHostFree(c->h_scalar);
   if (c->h_ovf) hipHostFree(c->h_ovf);
@@ -457,19 +460,35 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
     NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf + OVF_NORM_FWD, c->st,
                                 sp_x));
   }
+  // classifier: the tied embedding, or its compact rows (vocabulary compaction; padding
+  // columns cv..cvp are masked out of the softmax)
+  const bool compact = c->cv > 0;
+  const int Vc = compact ? c->cvp : V, Vvalid = compact ? c->cv : V;
+  const h16_t *Ecls = compact ? c->cE : Pb + c->off_E;
   {
     ProfScope ps(c, NE_PROF_CE);
-    NE_CHECK(ce_forward(dt, c->xf, Pb + c->off_E, c->tok_tgt, T, D, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
+    if (compact) NE_CHECK(launch_gather_rows16(Pb + c->off_E, c->cids, c->cE, c->cvp, D, c->st));
+    NE_CHECK(ce_forward(dt, c->xf, Ecls, c->tok_tgt, T, D, Vc, Vvalid, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
                         c->loss, c->st));
-    NE_CHECK(ce_backward(dt, c->xf, Pb + c->off_E, c->tok_tgt, c->ce_lse, T, D, V, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
+    NE_CHECK(ce_backward(dt, c->xf, Ecls, c->tok_tgt, c->ce_lse, T, D, Vc, Vvalid, c->gs, c->dlogits,
+                         ovf + OVF_DLOGITS, c->st));
   }
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
   // The dX GEMMs feeding an RMSNorm backward leave their split-K partials to it (sp_d); the
   // weight-gradient GEMM beside each runs first, since both split into the one workspace.
   SplitIn sp_d;
-  NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
-  NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, V, c->dlogits, V, Pb + c->off_E, D, c->dtmp, &sp_d));
+  if (compact) {
+    // compact embedding gradient, then added to its rows (TD/cpu_ops.h:425-431); the rows
+    // outside the compact vocabulary get only the input-embedding gradient
+    NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_F32, Vc, D, T, c->dlogits, Vc, c->xf, D, c->gcE, D, nullptr, 0, u));
+    ProfScope ps(c, NE_PROF_CE);
+    if (fresh) NE_CHECK(launch_fill_f32(G + c->off_E, 0.f, (long)V * D, c->st));
+    NE_CHECK(launch_scatter_add_rows(G + c->off_E, c->gcE, c->cids, c->cv, D, c->st));
+  } else {
+    NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
+  }
+  NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, Vc, c->dlogits, Vc, Ecls, D, c->dtmp, &sp_d));
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
@@ -568,7 +587,8 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
       const int32_t ti = tokens[(long)b * (S + 1) + s], tt = tokens[(long)b * (S + 1) + s + 1];
       if (ti < 0 || ti >= V || tt < 0 || tt >= V) return ne_fail(NE_ERR_ARG, "token id out of [0, %d)", V);
       h[(long)b * S + s] = ti;
-      h[T + (long)b * S + s] = tt;
+      h[T + (long)b * S + s] = c->cv ? c->f2c[tt] : tt;
+      if (c->cv && c->f2c[tt] < 0) return ne_fail(NE_ERR_ARG, "target id %d is not in the compact vocabulary", tt);
     }
   // per-id chains of input rows in token order, for the deterministic embedding scatter
   int32_t *nxt = h + 2 * T, *first = h + 3 * T;
@@ -599,6 +619,40 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
 extern "C" int ne_use_graphs(ne_ctx *c, int on) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   c->use_graphs = on != 0;
+  return 0;
+}
+
+extern "C" int ne_set_vocab_map(ne_ctx *c, const int32_t *ids, int cv) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  if (cv < 0 || cv > c->V || (cv > 0 && !ids)) return ne_fail(NE_ERR_ARG, "vocab map: %d ids of %d", cv, c->V);
+  if (!c->grads_fresh) return ne_fail(NE_ERR_STATE, "vocab map: change it between accumulation windows");
+  std::vector<int32_t> f2c(cv ? c->V : 0, -1);
+  for (int i = 0; i < cv; i++) {
+    if (ids[i] < 0 || ids[i] >= c->V) return ne_fail(NE_ERR_ARG, "vocab map: id %d out of [0, %d)", ids[i], c->V);
+    if (f2c[ids[i]] >= 0) return ne_fail(NE_ERR_ARG, "vocab map: id %d repeated", ids[i]);
+    f2c[ids[i]] = i;
+  }
+  NE_HIP(hipStreamSynchronize(c->st));
+  // the captured steps bake the classifier in
+  for (auto &e : c->graphs) (void)hipGraphExecDestroy(e.exec);
+  c->graphs.clear();
+  if (c->cids) (void)hipFree(c->cids);
+  if (c->cE) (void)hipFree(c->cE);
+  if (c->gcE) (void)hipFree(c->gcE);
+  c->cids = nullptr; c->cE = nullptr; c->gcE = nullptr;
+  c->cv = c->cvp = 0;
+  c->f2c.clear();
+  if (cv == 0) return 0;
+  const int cvp = (cv + 63) / 64 * 64;
+  std::vector<int32_t> padded(ids, ids + cv);
+  padded.resize(cvp, ids[0]);
+  NE_HIP(hipMalloc((void **)&c->cids, (size_t)cvp * sizeof(int32_t)));
+  NE_HIP(hipMalloc((void **)&c->cE, (size_t)cvp * c->D * sizeof(h16_t)));
+  NE_HIP(hipMalloc((void **)&c->gcE, (size_t)cvp * c->D * sizeof(float)));
+  NE_HIP(hipMemcpy(c->cids, padded.data(), (size_t)cvp * sizeof(int32_t), hipMemcpyHostToDevice));
+  c->cv = cv;
+  c->cvp = cvp;
+  c->f2c.swap(f2c);
   return 0;
 }
 

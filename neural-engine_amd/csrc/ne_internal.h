@@ -61,6 +61,7 @@ struct GemmArgs {
   int n_tiles;               // set by the launcher: N / BN
   int split;                 // set by the launcher: K splits (grid.z)
   int defer_reduce;          // with K splits, leave the fp32 partials in ws for the consumer
+  int n_valid;               // CE epilogues: columns >= n_valid are outside the softmax (0: N)
 };
 
 // Split-K partials of a GEMM whose reduction is folded into its consumer: element e of the
@@ -135,11 +136,17 @@ int launch_attn_bwd(int dt, const AttnArgs &a, hipStream_t s);
 // ---- cross-entropy (k_ce.hip over the EPI_CE_* GEMM epilogues) ----
 int launch_ce_reduce(const float *part, int n_tiles, const float *tgt_logit, float *lse,
                      float *loss_rows, float *loss, int T, hipStream_t s);
+// V columns of which the first n_valid take part in the softmax (n_valid <= V; the rest
+// are padding: no probability, zero gradient).
 int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
-               float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+               int n_valid, float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                hipStream_t s);
 int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse,
-                int T, int D, int V, float scale, void *dlogits, int *ovf, hipStream_t s);
+                int T, int D, int V, int n_valid, float scale, void *dlogits, int *ovf, hipStream_t s);
+// Vocabulary compaction: dst[r] = src[ids[r]] (16-bit rows of D); G[ids[r]] += src[r] for
+// r < n (fp32 rows of D; the ids are distinct).
+int launch_gather_rows16(const h16_t *src, const int32_t *ids, h16_t *dst, int n, int D, hipStream_t s);
+int launch_scatter_add_rows(float *G, const float *src, const int32_t *ids, int n, int D, hipStream_t s);
 
 // ---- optimizer (k_optim.hip) ----
 struct AdamArgs {

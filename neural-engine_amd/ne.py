@@ -28,7 +28,7 @@ EXPORTS = (
     "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_optimizer_step",
     "ne_zero_grads",
     "ne_grad_scale_info", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
-    "ne_decode",
+    "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
@@ -85,6 +85,7 @@ def lib():
         "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
         "ne_save_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
         "ne_decode": (I, [P, P, I, I, I, F, F, P, P]),
+        "ne_set_vocab_map": (I, [P, P, I]),
         "ne_prof_enable": (I, [P, I]),
         "ne_prof_reset": (I, [P]),
         "ne_prof_get": (I, [P, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
@@ -214,6 +215,14 @@ class Model:
 
     def use_graphs(self, on=True):
         check(lib().ne_use_graphs(self._h, int(on)), "use_graphs")
+
+    def set_vocab_map(self, ids):
+        """Vocabulary compaction: classifier + softmax over these embedding rows (None: all)."""
+        if ids is None:
+            check(lib().ne_set_vocab_map(self._h, None, 0), "set_vocab_map")
+            return
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().ne_set_vocab_map(self._h, a.ctypes.data_as(C.c_void_p), len(a)), "set_vocab_map")
 
     def zero_grads(self):
         check(lib().ne_zero_grads(self._h), "zero_grads")

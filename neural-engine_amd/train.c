@@ -7,13 +7,15 @@
  * and AdamW cadence (TD/train.m:782-903), the same checkpoint file and save rule
  * (TD/train.m:97-165, 907-915) and the same stdout lines that TR/dashboard.py parses.
  *
+ * As in the reference, the classifier and the softmax cover only the token ids present in the
+ * data file (vocabulary compaction, TD/cpu_ops.h:384-431, TD/train.m:286-292).
+ *
  * Differences, all on purpose: weights, gradients and Adam state live on the GPU and never
- * cross to the host during training; the loss is the full-vocabulary cross-entropy (the
- * reference compacts the softmax to the ids present in the data file, TD/cpu_ops.h:384-431);
- * the RMSNorm backward is the exact gradient.  Extensions: --tokens32 reads int32 token
- * ids (uint16 cannot hold Qwen3's vocabulary), --qk-norm and --rope-theta select Qwen3's
- * per-head QK-RMSNorm and RoPE base, --ckpt overrides the checkpoint path, --bf16 selects
- * bf16 instead of fp16 activations.
+ * cross to the host during training; the RMSNorm backward is the exact gradient.
+ * Extensions: --full-vocab runs the full-vocabulary softmax instead of the compaction,
+ * --tokens32 reads int32 token ids (uint16 cannot hold Qwen3's vocabulary), --qk-norm and
+ * --rope-theta select Qwen3's per-head QK-RMSNorm and RoPE base, --ckpt overrides the
+ * checkpoint path, --bf16 selects bf16 instead of fp16 activations.
  */
 #define _DEFAULT_SOURCE
 #include <fcntl.h>
@@ -85,7 +87,7 @@ int main(int argc, char *argv[]) {
   const float loss_scale = 256.0f;
   const float res_alpha = 1.0f / sqrtf(2.0f * NLAYERS);
   const float min_lr_frac = 0.1f;
-  int do_resume = 0, from_scratch = 0, tokens32 = 0, qk_norm = QK_NORM, bf16 = 0;
+  int do_resume = 0, from_scratch = 0, tokens32 = 0, qk_norm = QK_NORM, bf16 = 0, full_vocab = 0;
   float rope_theta = ROPE_THETA;
   const char *data_path = DEFAULT_DATA_PATH;
   const char *ckpt_path = CKPT_PATH;
@@ -103,6 +105,7 @@ int main(int argc, char *argv[]) {
     else if (strcmp(argv[i], "--qk-norm") == 0) qk_norm = 1;
     else if (strcmp(argv[i], "--tokens32") == 0) tokens32 = 1;
     else if (strcmp(argv[i], "--bf16") == 0) bf16 = 1;
+    else if (strcmp(argv[i], "--full-vocab") == 0) full_vocab = 1;
   }
   if (accum_steps < 1) accum_steps = 1;
   float lr = max_lr;
@@ -184,7 +187,33 @@ int main(int argc, char *argv[]) {
     ne_destroy(ctx);
     return 1;
   }
-  printf("Vocab: full %d-way softmax (no compaction)\n", VOCAB);
+  if (full_vocab) {
+    printf("Vocab: full %d-way softmax (no compaction)\n", VOCAB);
+  } else {
+    /* vocab_map_build (TD/cpu_ops.h:391-414): the distinct ids in ascending order */
+    unsigned char *used = (unsigned char *)calloc(VOCAB, 1);
+    int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * VOCAB);
+    int cv = 0, bad = 0;
+    for (size_t i = 0; i < n_tokens; i++) {
+      const int64_t t = tokens32 ? ((const int32_t *)data)[i] : ((const uint16_t *)data)[i];
+      if (t < 0 || t >= VOCAB) bad = 1;
+      else used[t] = 1;
+    }
+    for (int v = 0; v < VOCAB; v++)
+      if (used[v]) ids[cv++] = v;
+    const int vrc = bad ? -1 : ne_set_vocab_map(ctx, ids, cv);
+    free(used);
+    free(ids);
+    if (bad || vrc) {
+      if (bad) printf("Token data holds ids outside [0, %d)\n", VOCAB);
+      else printf("ERROR: ne_set_vocab_map: %s\n", ne_last_error());
+      munmap(data, data_len);
+      close(fd);
+      ne_destroy(ctx);
+      return 1;
+    }
+    printf("Vocab compaction: %d \u2192 %d active tokens (%.1fx reduction)\n", VOCAB, cv, (float)VOCAB / cv);
+  }
   printf("Context created in %.0fms\n\n", create_ms);
 
   int32_t tok[SEQ + 1];

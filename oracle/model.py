@@ -16,6 +16,10 @@ TD = ane-training/training/training_dynamic):
 * SwiGLU fwd/bwd          TD/mil_dynamic.h:238-306, 320-409
 * cross-entropy           TD/cpu_ops.h:348-382: loss = mean(-log(p_tgt + 1e-10)),
                           dlogits = (softmax - onehot) * loss_scale / T
+* vocab compaction        TD/cpu_ops.h:384-431, TD/train.m:286-292, 401, 497-523, 802:
+                          optional; the classifier and the softmax cover only the ids
+                          present in the data (ascending full id = compact id), and the
+                          compact embedding gradient is scattered back to its rows
 * RMSNorm bwd             exact gradient of TD/cpu_ops.h:20-60 (the reference's
                           TD/cpu_ops.h:108-261 carries an extra gain factor on the
                           projection term; identical while gains are 1.0)
@@ -222,10 +226,22 @@ def softmax_rows(x):
 # training step
 
 
-def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, want_grad_cache=True):
+def vocab_map_build(data: np.ndarray, vocab: int) -> np.ndarray:
+    """Compact vocabulary of a token stream (TD/cpu_ops.h:391-414): the distinct ids in
+    ascending order; compact id c stands for full id ids[c]."""
+    used = np.zeros(vocab, bool)
+    used[np.asarray(data, np.int64).reshape(-1)] = True
+    return np.flatnonzero(used).astype(np.int32)
+
+
+def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, want_grad_cache=True,
+            vocab_ids: np.ndarray | None = None):
     """Batched forward + CE.  tokens [B, S+1] int: inputs [:, :S], targets [:, 1:].
 
-    Returns (loss, cache).  cache carries everything the backward needs.
+    vocab_ids (optional, from vocab_map_build): the classifier and the softmax run over
+    those embedding rows only and the targets are mapped to their compact ids
+    (TD/train.m:401, 497-503).  Returns (loss, cache).  cache carries everything the
+    backward needs.
     """
     B, S1 = tokens.shape
     S = S1 - 1
@@ -278,7 +294,8 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
         layers.append(c)
     xL = x
     xf, rf = rmsnorm(xL, P["rms_final"], cfg.eps)
-    logits = xf @ P["embed"].T                            # [B,S,V]
+    E_cls = P["embed"] if vocab_ids is None else P["embed"][vocab_ids]
+    logits = xf @ E_cls.T                                 # [B,S,V] (or [B,S,CV])
     T = B * S
     lg = logits.reshape(T, -1)
     m = np.max(lg, axis=1, keepdims=True)
@@ -286,6 +303,11 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
     ssum = np.sum(e, axis=1, keepdims=True, dtype=F32)
     probs_v = (e / ssum).astype(F32)
     t_flat = tgt.reshape(T)
+    if vocab_ids is not None:
+        pos = np.searchsorted(vocab_ids, t_flat)
+        if np.any(pos >= len(vocab_ids)) or np.any(vocab_ids[np.minimum(pos, len(vocab_ids) - 1)] != t_flat):
+            raise ValueError("target id outside the compact vocabulary")
+        t_flat = pos
     p_tgt = probs_v[np.arange(T), t_flat]
     losses = -np.log(p_tgt + F32(1e-10))
     loss = float(np.sum(losses, dtype=F32) / F32(T))
@@ -294,7 +316,7 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
         dlog = probs_v * F32(loss_scale / T)
         dlog[np.arange(T), t_flat] -= F32(loss_scale / T)
         cache = dict(inp=inp, tgt=tgt, layers=layers, xL=xL, xf=xf, rf=rf, dlogits=dlog.astype(F32),
-                     cos=cos, sin=sin, B=B, S=S)
+                     cos=cos, sin=sin, B=B, S=S, vocab_ids=vocab_ids)
     return loss, cache
 
 
@@ -310,8 +332,14 @@ def backward(cfg: Config, P: dict, cache: dict) -> dict:
 
     dlog = cache["dlogits"].reshape(B, S, -1)
     xf = cache["xf"]
-    G["embed"] += (dlog.reshape(B * S, -1).T @ xf.reshape(B * S, D)).astype(F32)
-    dxf = dlog @ P["embed"]
+    ids = cache.get("vocab_ids")
+    dE_cls = (dlog.reshape(B * S, -1).T @ xf.reshape(B * S, D)).astype(F32)
+    if ids is None:
+        G["embed"] += dE_cls
+        dxf = dlog @ P["embed"]
+    else:                                                 # vocab_scatter_grads, TD/cpu_ops.h:425-431
+        G["embed"][ids] += dE_cls
+        dxf = dlog @ P["embed"][ids]
     dx, dg = rmsnorm_bwd(dxf, cache["xL"], P["rms_final"], cache["rf"])
     G["rms_final"] += dg
 

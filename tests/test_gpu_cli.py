@@ -42,32 +42,40 @@ def run_cli(args, cwd):
     return r.stdout
 
 
-def write_data(path, cfg, n=5000, seed=5):
-    data = np.random.default_rng(seed).integers(0, cfg.vocab, n).astype(np.uint16)
+def write_data(path, cfg, n=5000, seed=5, n_ids=None):
+    data = np.random.default_rng(seed).integers(0, n_ids or cfg.vocab, n).astype(np.uint16)
     data.tofile(path)
     return data
 
 
-def test_resume_one_step_matches_oracle(tmp_path):
+@pytest.mark.parametrize("compact", [True, False])
+def test_resume_one_step_matches_oracle(tmp_path, compact):
     """--resume from an oracle-written checkpoint at step 99 of 100: one sampled window,
-    one AdamW step at the cosine LR of step 99, checkpoint saved at step 100."""
+    one AdamW step at the cosine LR of step 99, checkpoint saved at step 100.  The data use
+    300 of the 512 ids: by default the classifier is compacted to them (TD/train.m:286-292);
+    --full-vocab keeps the full softmax."""
     cfg = tiny_cfg()
     P = om.init_params(cfg, seed=0, std=0.02)
     M = {k: np.zeros_like(v) for k, v in P.items()}
     V = {k: np.zeros_like(v) for k, v in P.items()}
     ck = str(tmp_path / "ck.bin")
     ock.write(ck, cfg, P, M, V, step=99, total_steps=100, lr=3e-4, loss=0.0)
-    data = write_data(tmp_path / "data.bin", cfg)
+    data = write_data(tmp_path / "data.bin", cfg, n_ids=300)
+    ids = om.vocab_map_build(data, cfg.vocab) if compact else None
     out = run_cli(["--resume", "--ckpt", ck, "--data", str(tmp_path / "data.bin"), "--accum", "1",
-                   "--warmup", "1", "--lr", "3e-4"], tmp_path)
+                   "--warmup", "1", "--lr", "3e-4"] + ([] if compact else ["--full-vocab"]), tmp_path)
     assert "[RESUMED step 99, loss=0.0000]" in out
+    if compact:
+        assert f"Vocab compaction: {cfg.vocab} \u2192 {len(ids)} active tokens" in out
+    else:
+        assert f"Vocab: full {cfg.vocab}-way softmax" in out
     m = RE_STEP.search(out)
     assert m and int(m.group(1)) == 99
     assert "[ckpt saved" in out
 
     (pos,) = od.window_positions(len(data), cfg.seq, 99, 1)
     tok = data[pos:pos + cfg.seq + 1].astype(np.int32)[None]
-    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
     G = om.backward(cfg, P, cache)
     lr = om.lr_at(99, 3e-4, 1, 100)
     Po = {k: v.copy() for k, v in P.items()}

@@ -257,3 +257,65 @@ def test_step_identical_across_launch_modes():
         assert li == l0
         for n in g0:
             np.testing.assert_array_equal(gi[n], g0[n], err_msg=n)
+
+
+def _compact_case(vocab=1024, seed=5):
+    cfg = om.tiny(qk_norm=True, rope_theta=1e6, res_alpha=om.train_alpha(2), vocab=vocab)
+    rng = np.random.default_rng(seed)
+    data = rng.choice(np.arange(100, 900, 7), size=4096).astype(np.int32)   # 115 distinct ids
+    ids = om.vocab_map_build(data, cfg.vocab)
+    starts = rng.integers(0, len(data) - cfg.seq - 1, 2)
+    tok = np.stack([data[s:s + cfg.seq + 1] for s in starts]).astype(np.int32)
+    return cfg, data, ids, tok
+
+
+@pytest.mark.parametrize("dtype", [ne.NE_FP16, ne.NE_BF16])
+def test_compact_vocab_step_matches_oracle(dtype):
+    """Vocabulary compaction (TD/cpu_ops.h:384-431): classifier and softmax over the ids of
+    the data (115 of 1024, padded to 128 columns), compact gradient added back to its rows;
+    two accumulated micro-steps, then back to the full vocabulary.  Gradients are checked in
+    the training format (fp16); with bf16 activations the loss is checked (bf16's 8-bit
+    mantissa puts the small QK-norm gain reductions at the 1e-2 bar by itself)."""
+    cfg, data, ids, tok = _compact_case()
+    P = om.init_params(cfg, seed=0, std=0.02)
+    m = ne.Model.from_oracle(cfg, batch=2, dtype=dtype)
+    m.set_params(P)
+    m.set_vocab_map(ids)
+    tok2 = np.roll(tok, 7, axis=1)
+    loss = m.train_step(tok, 256.0)
+    loss2 = m.train_step(tok2, 256.0)
+    G = m.get_all(shapes(cfg), ne.NE_GRAD)
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
+    Go = om.backward(cfg, P, cache)
+    lo2, cache2 = om.forward(cfg, P, tok2, loss_scale=256.0, vocab_ids=ids)
+    Go2 = om.backward(cfg, P, cache2)
+    print(f"\n  compact loss gpu={loss:.6f}/{loss2:.6f} oracle={lo:.6f}/{lo2:.6f} (ln CV = {np.log(len(ids)):.4f})")
+    assert abs(loss - lo) <= LOSS_RTOL * abs(lo) and abs(loss2 - lo2) <= LOSS_RTOL * abs(lo2)
+    for n in P if dtype == ne.NE_FP16 else ("embed", "rms_final"):
+        assert rel_l2(G[n], Go[n] + Go2[n]) <= GRAD_RL2, (n, rel_l2(G[n], Go[n] + Go2[n]))
+    unused = np.setdiff1d(np.arange(cfg.vocab), ids)
+    assert np.abs(G["embed"].reshape(cfg.vocab, -1)[unused]).max() == 0
+    # the map is fixed inside an accumulation window
+    with pytest.raises(ne.NEError):
+        m.set_vocab_map(None)
+    m.zero_grads()
+    m.set_vocab_map(None)
+    loss_f = m.train_step(tok, 256.0)
+    lf, _ = om.forward(cfg, P, tok, loss_scale=256.0, want_grad_cache=False)
+    assert abs(loss_f - lf) <= LOSS_RTOL * abs(lf)
+    m.close()
+
+
+def test_compact_vocab_rejects_bad_maps_and_targets():
+    cfg, data, ids, tok = _compact_case()
+    m = ne.Model.from_oracle(cfg, batch=2)
+    with pytest.raises(ne.NEError):
+        m.set_vocab_map(np.array([3, 5, 3], np.int32))        # repeated id
+    with pytest.raises(ne.NEError):
+        m.set_vocab_map(np.array([3, cfg.vocab], np.int32))   # out of range
+    m.set_vocab_map(ids[1:])
+    bad = tok.copy()
+    bad[0, 5] = ids[0]                                       # a target outside the map
+    with pytest.raises(ne.NEError):
+        m.train_step(bad, 256.0)
+    m.close()

@@ -23,14 +23,16 @@ def _gpu():
     need_gpu()
 
 
-def _compare_grads(cfg, P, tok, label):
+def _compare_grads(cfg, P, tok, label, vocab_ids=None):
     m = ne.Model.from_oracle(cfg, batch=tok.shape[0])
     m.set_params(P)
+    if vocab_ids is not None:
+        m.set_vocab_map(vocab_ids)
     t0 = time.time()
     loss = m.train_step(tok, 256.0)
     G = m.get_all(dict(om.tensor_list(cfg)), ne.NE_GRAD)
     t1 = time.time()
-    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=vocab_ids)
     Go = om.backward(cfg, P, cache)
     del cache
     t2 = time.time()
@@ -48,6 +50,18 @@ def test_stories110m_step_parity():
     P = om.init_params(cfg, seed=0, std=0.02)
     tok = om.tokens_for_step(cfg, 1, 256, seed=1)
     _compare_grads(cfg, P, tok, "stories110m B=1 S=256").close()
+
+
+def test_stories110m_compact_vocab_step_parity():
+    """Vocabulary compaction at the Stories110M shape: the classifier over the ~3k distinct
+    ids of a data stream drawn from 3500 of the 32000 ids (TD/train.m:286-292)."""
+    cfg = om.stories110m(res_alpha=om.train_alpha(12))
+    P = om.init_params(cfg, seed=0, std=0.02)
+    rng = np.random.default_rng(11)
+    data = rng.choice(rng.choice(cfg.vocab, 3500, replace=False), 20000).astype(np.int32)
+    ids = om.vocab_map_build(data, cfg.vocab)
+    tok = data[1000:1000 + cfg.seq + 1][None]
+    _compare_grads(cfg, P, tok, f"stories110m compact vocab {len(ids)}", vocab_ids=ids).close()
 
 
 def test_qwen3_step_parity():

@@ -122,6 +122,50 @@ def test_backward_matches_float64_autograd(kw):
         assert rel_l2(G[n], TG[n]) < 2e-4, n
 
 
+def test_compact_vocab_backward_matches_float64_autograd():
+    """Vocab compaction (TD/cpu_ops.h:384-431): classifier over the ids present in the data,
+    gradient scattered back to those embedding rows; pinned by autograd of the sub-matrix."""
+    pytest.importorskip("torch")
+    import torch_ref
+    cfg = om.tiny(qk_norm=True, res_alpha=om.train_alpha(2), rope_theta=1e6, dim=64, hidden=128,
+                  head_dim=16, vocab=97)
+    P = om.init_params(cfg, seed=5, std=0.1)
+    rng = np.random.default_rng(3)
+    tok = rng.choice(np.arange(10, 60, 3), size=(2, 13)).astype(np.int32)   # 17 distinct ids
+    ids = om.vocab_map_build(tok, cfg.vocab)
+    assert list(ids) == sorted(set(tok.reshape(-1).tolist()))
+    loss, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
+    G = om.backward(cfg, P, cache)
+    tl, TG = torch_ref.grads(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
+    assert abs(loss - tl) < 1e-5 * abs(tl)
+    for n in P:
+        assert rel_l2(G[n], TG[n]) < 2e-4, n
+    # rows outside the compact vocabulary and never used as inputs get no gradient
+    unused = np.setdiff1d(np.arange(cfg.vocab), ids)
+    assert np.abs(G["embed"][unused]).max() == 0
+
+
+def test_compact_vocab_known_answers():
+    cfg = om.tiny(vocab=300)
+    tok = om.tokens_for_step(cfg, 2, 16, seed=7) % 50 + 100
+    ids = om.vocab_map_build(tok, cfg.vocab)
+    # zero weights: every logit is 0, so the loss is ln(CV)
+    P0 = om.init_params(cfg, seed=0, zero=True)
+    l0, _ = om.forward(cfg, P0, tok, vocab_ids=ids)
+    assert abs(l0 - np.log(len(ids))) < 1e-5
+    # the identity map is the full-vocabulary path
+    P = om.init_params(cfg, seed=1, std=0.05)
+    lf, cf = om.forward(cfg, P, tok, loss_scale=4.0)
+    li, ci = om.forward(cfg, P, tok, loss_scale=4.0, vocab_ids=np.arange(cfg.vocab, dtype=np.int32))
+    assert abs(lf - li) <= 1e-6 * abs(lf)
+    Gf, Gi = om.backward(cfg, P, cf), om.backward(cfg, P, ci)
+    for n in P:
+        np.testing.assert_allclose(Gi[n], Gf[n], rtol=1e-5, atol=1e-7)
+    # a target outside the map is an error
+    with pytest.raises(ValueError):
+        om.forward(cfg, P, tok, vocab_ids=ids[1:])
+
+
 def test_torch_ref_matches_finite_differences():
     torch = pytest.importorskip("torch")
     import torch_ref

@@ -11,8 +11,10 @@ import numpy as np
 import torch
 
 
-def loss_fn(cfg, params: dict, tokens: np.ndarray, loss_scale: float = 1.0):
-    """params: name -> float64 torch tensor (requires_grad as the caller wishes)."""
+def loss_fn(cfg, params: dict, tokens: np.ndarray, loss_scale: float = 1.0, vocab_ids=None):
+    """params: name -> float64 torch tensor (requires_grad as the caller wishes).  With
+    vocab_ids the classifier is the sub-matrix of those embedding rows and each target is
+    replaced by its position in vocab_ids (found with a dictionary)."""
     tok = torch.as_tensor(tokens, dtype=torch.long)
     inp, tgt = tok[:, :-1], tok[:, 1:]
     B, S = inp.shape
@@ -55,14 +57,19 @@ def loss_fn(cfg, params: dict, tokens: np.ndarray, loss_scale: float = 1.0):
         h3 = xn @ p("W3").T
         x = x + a * ((torch.nn.functional.silu(h1) * h3) @ p("W2").T)
     xf = norm(x, params["rms_final"])
-    logits = xf @ params["embed"].T
+    if vocab_ids is None:
+        logits = xf @ params["embed"].T
+    else:
+        where = {int(v): i for i, v in enumerate(vocab_ids)}
+        tgt = torch.tensor([[where[int(t)] for t in row] for row in tgt.tolist()], dtype=torch.long)
+        logits = xf @ params["embed"][torch.as_tensor(np.asarray(vocab_ids), dtype=torch.long)].T
     logp = logits.log_softmax(-1)
     nll = -logp.gather(-1, tgt[..., None]).squeeze(-1)
     return nll.mean() * loss_scale
 
 
-def grads(cfg, P: dict, tokens, loss_scale=1.0):
+def grads(cfg, P: dict, tokens, loss_scale=1.0, vocab_ids=None):
     params = {k: torch.tensor(v, dtype=torch.float64, requires_grad=True) for k, v in P.items()}
-    loss = loss_fn(cfg, params, tokens, loss_scale)
+    loss = loss_fn(cfg, params, tokens, loss_scale, vocab_ids)
     loss.backward()
     return float(loss) / loss_scale, {k: t.grad.numpy() for k, t in params.items()}
