@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import struct
 
 import numpy as np
 
@@ -38,6 +39,35 @@ EXPORTS = (
 
 class NEError(RuntimeError):
     pass
+
+
+CKPT_MAGIC = 0x424C5A54
+_CKPT_HDR = struct.Struct("<10i2f3d6i")   # 96 bytes, TD/config.h:82-91
+
+
+def read_ckpt_header(path):
+    """Model dims and counters of a v4 checkpoint (TD/config.h:82-91), plus whether the
+    QK-norm gain trailer follows the body (detected from the file size)."""
+    with open(path, "rb") as f:
+        raw = f.read(_CKPT_HDR.size)
+    if len(raw) != _CKPT_HDR.size:
+        raise NEError(f"{path}: short header")
+    (magic, version, step, total_steps, n_layers, vocab, dim, hidden, n_heads, seq, lr, loss,
+     cum_compile, cum_train, cum_wall, cum_steps, cum_batches, adam_t, kv_heads, head_dim, q_dim) = _CKPT_HDR.unpack(raw)
+    if magic != CKPT_MAGIC or version != 4:
+        raise NEError(f"{path}: not a v4 checkpoint")
+    if kv_heads <= 0:                           # files of the MHA trainer leave the GQA slots empty
+        kv_heads, head_dim, q_dim = n_heads, dim // n_heads, dim
+    kv_dim = kv_heads * head_dim
+    n = n_layers * (q_dim * dim + 2 * kv_dim * dim + dim * q_dim + 3 * hidden * dim + 2 * dim) + dim + vocab * dim
+    base = _CKPT_HDR.size + 3 * 4 * n
+    size = os.path.getsize(path)
+    qkn = size == base + 12 + n_layers * 6 * head_dim * 4
+    if size != base and not qkn:
+        raise NEError(f"{path}: size {size}, expected {base}")
+    return dict(step=step, total_steps=total_steps, n_layers=n_layers, vocab=vocab, dim=dim, hidden=hidden,
+                n_heads=n_heads, kv_heads=kv_heads, head_dim=head_dim, q_dim=q_dim, seq=seq, lr=lr, loss=loss,
+                adam_t=adam_t, qk_norm=qkn)
 
 
 class Config(C.Structure):
