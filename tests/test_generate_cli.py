@@ -96,3 +96,34 @@ def test_cli_streams_match_oracle(tmp_path, qk_norm):
     got, n, _ = _run([path, "--prompt-ids", "5,17,99,3,200", "-n", "40", "-t", "0", "--eos", str(eos)] + theta)
     k = want.index(eos) + 1
     assert got == want[:k] and n == k
+
+
+@pytest.mark.gpu
+def test_hf_directory_to_tokens(tmp_path):
+    """A local HF-format model directory -> convert_hf.py -> generate.py on the GPU: the
+    greedy stream of the oracle on the same (QK-norm, fp16-exact) weights."""
+    if not __import__("torch").cuda.is_available():
+        pytest.skip("no GPU")
+    import json
+    from safetensors.numpy import save_file
+    import convert_hf
+    cfg, P, _ = _ckpt(tmp_path, True)
+    hf = {"Wq": "self_attn.q_proj", "Wk": "self_attn.k_proj", "Wv": "self_attn.v_proj", "Wo": "self_attn.o_proj",
+          "W1": "mlp.gate_proj", "W2": "mlp.down_proj", "W3": "mlp.up_proj", "rms_att": "input_layernorm",
+          "rms_ffn": "post_attention_layernorm", "q_norm": "self_attn.q_norm", "k_norm": "self_attn.k_norm"}
+    t = {"model.embed_tokens.weight": P["embed"], "model.norm.weight": P["rms_final"]}
+    for n, a in P.items():
+        if n.startswith("layers."):
+            _, l, name = n.split(".")
+            t[f"model.layers.{l}.{hf[name]}.weight"] = a
+    d = tmp_path / "hf"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps(dict(
+        model_type="qwen3", hidden_size=cfg.dim, intermediate_size=cfg.hidden, num_attention_heads=cfg.n_heads,
+        num_key_value_heads=cfg.kv_heads, head_dim=cfg.head_dim, num_hidden_layers=cfg.n_layers,
+        vocab_size=cfg.vocab)))
+    ck = str(tmp_path / "converted.bin")
+    assert convert_hf.main([str(d), "-o", ck]) == 0
+    got, n, _ = _run([ck, "--prompt-ids", "9,8,7", "-n", "32", "-t", "0", "--rope-theta", "1e6"])
+    assert got == om.decode(cfg, P, np.array([[9, 8, 7]], np.int32), 32)[0].tolist()
