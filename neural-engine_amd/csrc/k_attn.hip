@@ -236,7 +236,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
 
 // --------------------------------------------------------------------------- backward ----
 
-// delta[t, h] = sum_d dO[t,h,d] * O[t,h,d]
+// delta[t, h] = sum_d dO[t,h,d] * O[t,h,d].  With split-K partials of dO (a.dsp.n > 0, dO of
+// row pitch lddo = NH*HD) dO is summed in split order, scaled, rounded to 16 bits and written
+// (the dK/dV and dQ kernels read it) before use.
 template <typename HT, int HD>
 __global__ void attn_delta_kernel(AttnArgs a, long rows) {
   constexpr int L = HD / 8;  // lanes per row
@@ -248,7 +250,26 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
     const long t = row / a.NH;
     const int h = row % a.NH;
     const u16x8 o = *(const u16x8 *)(a.o + t * a.ldo + h * HD + j * 8);
-    const u16x8 d = *(const u16x8 *)(a.dout + t * a.lddo + h * HD + j * 8);
+    u16x8 d;
+    if (a.dsp.n > 0) {
+      const float *p = a.dsp.part + t * a.lddo + h * HD + j * 8;
+      float4 lo = *(const float4 *)p, hi = *(const float4 *)(p + 4);
+      for (int z = 1; z < a.dsp.n; z++) {
+        const float4 ql = *(const float4 *)(p + z * a.dsp.slice), qh = *(const float4 *)(p + z * a.dsp.slice + 4);
+        lo.x += ql.x; lo.y += ql.y; lo.z += ql.z; lo.w += ql.w;
+        hi.x += qh.x; hi.y += qh.y; hi.z += qh.z; hi.w += qh.w;
+      }
+      const float al = a.dsp.alpha;
+      d[0] = HT::h(lo.x * al); d[1] = HT::h(lo.y * al); d[2] = HT::h(lo.z * al); d[3] = HT::h(lo.w * al);
+      d[4] = HT::h(hi.x * al); d[5] = HT::h(hi.y * al); d[6] = HT::h(hi.z * al); d[7] = HT::h(hi.w * al);
+      bool bad = false;
+#pragma unroll
+      for (int e = 0; e < 8; e++) bad |= HT::bad(d[e]);
+      flag_overflow(a.ovf_dout, bad);
+      *(u16x8 *)((h16_t *)a.dout + t * a.lddo + h * HD + j * 8) = d;
+    } else {
+      d = *(const u16x8 *)(a.dout + t * a.lddo + h * HD + j * 8);
+    }
 #pragma unroll
     for (int e = 0; e < 8; e++) s += HT::f(o[e]) * HT::f(d[e]);
   }
@@ -548,6 +569,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
 }
 
 int check(const AttnArgs &a) {
+  if (a.dsp.n > 0 && a.lddo != (long)a.NH * a.HD)
+    return ne_fail(NE_ERR_ARG, "attention: split-K dout needs a dense [T, NH*HD] layout");
   if (a.HD != 64 && a.HD != 128) return ne_fail(NE_ERR_ARG, "attention: head_dim %d not in {64,128}", a.HD);
   if (a.S % BLK) return ne_fail(NE_ERR_ARG, "attention: seq %d must be a multiple of %d", a.S, BLK);
   if (a.NKV <= 0 || a.NH % a.NKV) return ne_fail(NE_ERR_ARG, "attention: heads %d not a multiple of kv heads %d", a.NH, a.NKV);

@@ -310,17 +310,70 @@ __global__ __launch_bounds__(CS_COLS * CS_GROUPS) void colsum_kernel(const float
   }
 }
 
+// colsum_kernel over a table of jobs (blockIdx.y = job), the same summation order.
+__global__ __launch_bounds__(CS_COLS * CS_GROUPS) void colsum_batch_kernel(const ColsumJob *__restrict__ jobs) {
+  __shared__ float red[CS_GROUPS][CS_COLS];
+  const ColsumJob jb = jobs[blockIdx.y];
+  const float *part = jb.part;
+  const int rows = jb.rows, n = jb.n;
+  const int c = threadIdx.x % CS_COLS, grp = threadIdx.x / CS_COLS;
+  const int j = blockIdx.x * CS_COLS + c;
+  if (blockIdx.x * CS_COLS >= n) return;  // uniform: this job has fewer columns
+  float s = 0.f;
+  if (j < n) {
+    int r = grp;
+    for (; r + 3 * CS_GROUPS < rows; r += 4 * CS_GROUPS) {
+      const float a = part[(long)r * n + j], b = part[(long)(r + CS_GROUPS) * n + j];
+      const float d = part[(long)(r + 2 * CS_GROUPS) * n + j], e = part[(long)(r + 3 * CS_GROUPS) * n + j];
+      s += a;
+      s += b;
+      s += d;
+      s += e;
+    }
+    for (; r < rows; r += CS_GROUPS) s += part[(long)r * n + j];
+  }
+  red[grp][c] = s;
+  __syncthreads();
+  if (grp == 0 && j < n) {
+    float t = red[0][c];
+#pragma unroll
+    for (int g = 1; g < CS_GROUPS; g++) t += red[g][c];
+    jb.out[j] += t;
+  }
+}
+
 // gate = silu(h1) * h3, h13 = [h1 | h3] per row   (TD/mil_dynamic.h:276-281)
+// With split-K partials of the W1|W3 GEMM (sp.n > 0) h1 and h3 are summed in split order,
+// scaled, rounded to 16 bits and written to h13 (read by the backward) before use.
 template <typename HT>
-__global__ void swiglu_fwd_kernel(const h16_t *__restrict__ h13, h16_t *__restrict__ gate, int T,
-                                  int H, int *ovf) {
-  bool bad = false;
+__global__ void swiglu_fwd_kernel(h16_t *__restrict__ h13, h16_t *__restrict__ gate, int T,
+                                  int H, int *ovf, SplitIn sp, int *ovf_h13) {
+  bool bad = false, bad13 = false;
   const long n4 = (long)T * H / 4;
   for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n4; i += (long)gridDim.x * blockDim.x) {
     const long e = i * 4;
     const long t = e / H, c = e % H;
-    u16x4 a = *(const u16x4 *)(h13 + t * 2 * H + c);
-    u16x4 b = *(const u16x4 *)(h13 + t * 2 * H + H + c);
+    u16x4 a, b;
+    if (sp.n > 0) {
+      const float *p = sp.part + t * 2 * H + c;
+      float4 s1 = *(const float4 *)p, s3 = *(const float4 *)(p + H);
+      for (int z = 1; z < sp.n; z++) {
+        const float4 q1 = *(const float4 *)(p + z * sp.slice), q3 = *(const float4 *)(p + z * sp.slice + H);
+        s1.x += q1.x; s1.y += q1.y; s1.z += q1.z; s1.w += q1.w;
+        s3.x += q3.x; s3.y += q3.y; s3.z += q3.z; s3.w += q3.w;
+      }
+      a[0] = HT::h(s1.x * sp.alpha); a[1] = HT::h(s1.y * sp.alpha);
+      a[2] = HT::h(s1.z * sp.alpha); a[3] = HT::h(s1.w * sp.alpha);
+      b[0] = HT::h(s3.x * sp.alpha); b[1] = HT::h(s3.y * sp.alpha);
+      b[2] = HT::h(s3.z * sp.alpha); b[3] = HT::h(s3.w * sp.alpha);
+#pragma unroll
+      for (int j = 0; j < 4; j++) bad13 |= HT::bad(a[j]) | HT::bad(b[j]);
+      *(u16x4 *)(h13 + t * 2 * H + c) = a;
+      *(u16x4 *)(h13 + t * 2 * H + H + c) = b;
+    } else {
+      a = *(const u16x4 *)(h13 + t * 2 * H + c);
+      b = *(const u16x4 *)(h13 + t * 2 * H + H + c);
+    }
     u16x4 o;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -331,6 +384,7 @@ __global__ void swiglu_fwd_kernel(const h16_t *__restrict__ h13, h16_t *__restri
     *(u16x4 *)(gate + e) = o;
   }
   flag_overflow(ovf, bad);
+  flag_overflow(ovf_h13, bad13);
 }
 
 // Per (token, head, pair): optional per-head RMSNorm with gain g[HD], then interleaved
@@ -338,24 +392,44 @@ __global__ void swiglu_fwd_kernel(const h16_t *__restrict__ h13, h16_t *__restri
 // Head slots 0..NH-1 are q heads (qkv columns h*HD), NH..NH+NKV-1 are k heads
 // (columns NH*HD + (h-NH)*HD).  Replaces the RoPE of gen_sdpa_fwd_dynamic
 // (TD/mil_dynamic.h:133-169).
+// With split-K partials of the QKV GEMM (sp.n > 0, qkv row pitch ld = q|k|v width) the
+// threads also cover the v heads: each pair is summed in split order, scaled, rounded to 16
+// bits and written to qkv (the GEMM's own output, read by attention and the backward), and
+// the q/k pairs continue from the rounded values.
 template <typename HT, bool QKN>
-__global__ void qk_prep_fwd_kernel(const h16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
+__global__ void qk_prep_fwd_kernel(h16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
                                    const float *__restrict__ sinb, const float *__restrict__ gq,
                                    const float *__restrict__ gk, h16_t *__restrict__ qr,
                                    h16_t *__restrict__ kr, float *__restrict__ rq, float *__restrict__ rk,
-                                   int T, int S, int NH, int NKV, int HD, float eps) {
+                                   int T, int S, int NH, int NKV, int HD, float eps, SplitIn sp, int *ovf_qkv) {
   const int half = HD / 2;
+  const int slots = sp.n > 0 ? NH + 2 * NKV : NH + NKV;
   const long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
-  const long total = (long)T * (NH + NKV) * half;
+  const long total = (long)T * slots * half;
   if (gid >= total) return;  // total is a multiple of 64: whole waves exit together
   const int i = gid % half;
   const long th = gid / half;
-  const int h = th % (NH + NKV);
-  const long t = th / (NH + NKV);
-  const bool isq = h < NH;
-  const int hh = isq ? h : h - NH;
-  const long col = (isq ? 0 : (long)NH * HD) + (long)hh * HD + 2 * i;
-  const uint32_t pr = *(const uint32_t *)(qkv + t * ld + col);
+  const int h = th % slots;
+  const long t = th / slots;
+  const bool isq = h < NH, isv = h >= NH + NKV;
+  const int hh = isq ? h : isv ? h - NH - NKV : h - NH;
+  const long col = (isq ? 0 : isv ? (long)(NH + NKV) * HD : (long)NH * HD) + (long)hh * HD + 2 * i;
+  uint32_t pr;
+  if (sp.n > 0) {
+    const float *p = sp.part + t * ld + col;
+    float s0 = p[0], s1 = p[1];
+    for (int z = 1; z < sp.n; z++) {
+      s0 += p[z * sp.slice];
+      s1 += p[z * sp.slice + 1];
+    }
+    const h16_t o0 = HT::h(s0 * sp.alpha), o1 = HT::h(s1 * sp.alpha);
+    flag_overflow(ovf_qkv, HT::bad(o0) | HT::bad(o1));
+    pr = (uint32_t)o0 | ((uint32_t)o1 << 16);
+    *(uint32_t *)(qkv + t * ld + col) = pr;
+    if (isv) return;  // uniform per wave (a head slot spans whole waves)
+  } else {
+    pr = *(const uint32_t *)(qkv + t * ld + col);
+  }
   float x0 = HT::f((h16_t)(pr & 0xFFFF)), x1 = HT::f((h16_t)(pr >> 16));
   if (QKN) {
     float ss = x0 * x0 + x1 * x1;
@@ -489,13 +563,26 @@ int qk_tpb(int T) { return T <= 4096 ? 16 : 128; }   // tokens per block
 }  // namespace
 
 long rmsnorm_bwd_part_elems(int T, int D) { return (long)((T + rms_rows(T) - 1) / rms_rows(T)) * D; }
+int rmsnorm_bwd_part_rows(int T) { return (T + rms_rows(T) - 1) / rms_rows(T); }
+void qk_prep_bwd_part_rows(int T, int NH, int NKV, int *rows_q, int *rows_k) {
+  const int nbx = (T + qk_tpb(T) - 1) / qk_tpb(T);
+  *rows_q = NH * nbx;
+  *rows_k = NKV * nbx;
+}
+
+int launch_colsum_batch(const ColsumJob *jobs_dev, int njobs, int max_n, hipStream_t s) {
+  if (njobs <= 0) return 0;
+  hipLaunchKernelGGL(colsum_batch_kernel, dim3((max_n + CS_COLS - 1) / CS_COLS, njobs), dim3(CS_COLS * CS_GROUPS), 0,
+                     s, jobs_dev);
+  return ne_hip_status(hipGetLastError(), "colsum_batch");
+}
 long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD) {
   return (long)((T + qk_tpb(T) - 1) / qk_tpb(T)) * (NH + NKV) * HD;
 }
 
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
-                       int D, int *ovf, float *part, hipStream_t s, const SplitIn &sp) {
+                       int D, int *ovf, float *part, hipStream_t s, const SplitIn &sp, bool defer_colsum) {
   if (D % 4 || D > 4 * RMS_NT * RMS_VPT)
     return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
   if (T <= 0) return 0;
@@ -506,7 +593,7 @@ int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, 
                        dg_scale, T, D, rows, ovf, part, sp);
     return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
   }()));
-  if (part) {
+  if (part && !defer_colsum) {
     hipLaunchKernelGGL(colsum_kernel, dim3((D + CS_COLS - 1) / CS_COLS, 1), dim3(CS_COLS * CS_GROUPS), 0, s, part, nb,
                        dg, part, nb, dg, D);
     NE_HIP(hipGetLastError());
@@ -514,25 +601,30 @@ int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, 
   return 0;
 }
 
-int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s) {
+int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s,
+                      const SplitIn &sp, int *ovf_h13) {
   if (H % 4) return ne_fail(NE_ERR_ARG, "swiglu: H %% 4 != 0");
   const long n4 = (long)T * H / 4;
   const int blocks = (int)std::min<long>((n4 + 255) / 256, 8192);
   return DISPATCH_H16(dt, [&] {
-    hipLaunchKernelGGL(swiglu_fwd_kernel<HT>, dim3(blocks), dim3(256), 0, s, h13, gate, T, H, ovf);
+    hipLaunchKernelGGL(swiglu_fwd_kernel<HT>, dim3(blocks), dim3(256), 0, s, (h16_t *)h13, gate, T, H, ovf, sp,
+                       ovf_h13);
     return ne_hip_status(hipGetLastError(), "swiglu_fwd");
   }());
 }
 
 int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
                        const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq,
-                       float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s) {
+                       float *rk, int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s,
+                       const SplitIn &sp, int *ovf_qkv) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
-  const long total = (long)T * (NH + NKV) * (HD / 2);
+  if (sp.n > 0 && ld != (long)(NH + 2 * NKV) * HD) return ne_fail(NE_ERR_ARG, "qk_prep: split input needs a dense qkv");
+  const long total = (long)T * (sp.n > 0 ? NH + 2 * NKV : NH + NKV) * (HD / 2);
   const int blocks = (int)((total + 255) / 256);
+  h16_t *q = (h16_t *)qkv;
   return DISPATCH_H16(dt, [&] {
-    if (gq) hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, true>), dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
-    else hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, false>), dim3(blocks), dim3(256), 0, s, qkv, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps);
+    if (gq) hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, true>), dim3(blocks), dim3(256), 0, s, q, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps, sp, ovf_qkv);
+    else hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, false>), dim3(blocks), dim3(256), 0, s, q, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps, sp, ovf_qkv);
     return ne_hip_status(hipGetLastError(), "qk_prep_fwd");
   }());
 }
@@ -540,7 +632,8 @@ int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, con
 int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk, float dg_scale,
-                       int T, int S, int NH, int NKV, int HD, int *ovf, float *part, hipStream_t s) {
+                       int T, int S, int NH, int NKV, int HD, int *ovf, float *part, hipStream_t s,
+                       bool defer_colsum) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
   const int tpb = qk_tpb(T);
   const int nbx = (T + tpb - 1) / tpb;
@@ -550,7 +643,7 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
     else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part);
     return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
   }()));
-  if (gq && part) {
+  if (gq && part && !defer_colsum) {
     hipLaunchKernelGGL(colsum_kernel, dim3((HD + CS_COLS - 1) / CS_COLS, 2), dim3(CS_COLS * CS_GROUPS), 0, s, part,
                        NH * nbx, dgq, part + (long)NH * nbx * HD, NKV * nbx, dgk, HD);
     NE_HIP(hipGetLastError());

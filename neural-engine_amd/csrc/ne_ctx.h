@@ -73,7 +73,10 @@ struct ne_ctx {
   bool grads_fresh = true;     // G holds no accumulation yet: the next step overwrites it
   float *ws = nullptr;         // split-K workspace
   long ws_elems = 0;
-  float *gpart = nullptr;      // per-block gain-gradient partials
+  float *gpart = nullptr;      // per-block gain-gradient partials: one slab per norm site
+  long rms_slab = 0, qk_slab = 0;  // floats per RMSNorm / QK-norm site
+  ColsumJob *cs_jobs = nullptr;    // device table: every site's ordered partial sum, one launch
+  int cs_njobs = 0;
   int32_t *h_tok = nullptr;  // pinned [2][4T] (double-buffered token staging)
   hipEvent_t tok_ev[2] = {nullptr, nullptr};
   int tok_slot = 0;

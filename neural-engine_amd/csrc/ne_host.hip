@@ -116,12 +116,14 @@ int gemm(ne_ctx *c, int fam, int site, int layout, int epi, int M, int N, int K,
 // *sp then describes the partials in c->ws (C unwritten), else has n = 0 (C written).  C must
 // be [M, N] row-major with ldc = N; R (EPI_RESID) is the residual added after the sum.
 int gemm_split(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, const void *A, long lda,
-               const void *B, long ldb, void *C, SplitIn *sp, const float *R = nullptr, float alpha = 1.f) {
+               const void *B, long ldb, void *C, SplitIn *sp, const float *R = nullptr, float alpha = 1.f,
+               int *ovf = nullptr) {
   ProfScope ps(c, fam);
   GemmArgs g = {};
   g.M = M; g.N = N; g.K = K;
   g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = N; g.R = R; g.ldr = N;
   g.alpha = alpha;
+  g.ovf = ovf;  // 16-bit C written here (no split); with a split the consumer raises it
   g.ws = c->ws;
   g.ws_elems = c->ws_elems;
   g.defer_reduce = 1;
@@ -137,6 +139,11 @@ int gemm_split(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, con
   }
   return 0;
 }
+
+// Gain-gradient partial slab of an RMSNorm site (0: final norm; 1 + 2l: layer l's FFN norm;
+// 2 + 2l: its attention norm) and of layer l's QK-norm pair.
+float *norm_part(ne_ctx *c, int site) { return c->gpart + (long)site * c->rms_slab; }
+float *qk_part(ne_ctx *c, int l) { return c->gpart + (long)(2 * c->L + 1) * c->rms_slab + (long)l * c->qk_slab; }
 
 int validate(const ne_config *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null config");
@@ -256,12 +263,16 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->tok_in, 4 * T);  // inputs, targets, id chains: filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
   pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
-  // split-K partials: up to 64 MB, enough for a 256-token step's narrow GEMMs
   // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
   c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
-  pl.add(&c->gpart, (size_t)std::max(rmsnorm_bwd_part_elems(c->T, c->D),
-                                     qk_prep_bwd_part_elems(c->T, c->NH, c->NKV, c->HD)));
+  // gain-gradient partials of every norm site (2L+1 RMSNorms, L QK-norm pairs), summed by one
+  // ordered launch at the end of the backward
+  c->rms_slab = rmsnorm_bwd_part_elems(c->T, c->D);
+  c->qk_slab = c->c.qk_norm ? qk_prep_bwd_part_elems(c->T, c->NH, c->NKV, c->HD) : 0;
+  pl.add(&c->gpart, (size_t)(2 * c->L + 1) * c->rms_slab + (size_t)c->L * c->qk_slab);
+  c->cs_njobs = 2 * c->L + 1 + (c->c.qk_norm ? 2 * c->L : 0);
+  pl.add(&c->cs_jobs, (size_t)c->cs_njobs);
 
   int rc = 0;
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
@@ -271,6 +282,26 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   c->tok_nxt = c->tok_in + 2 * T;
   c->tok_first = c->tok_in + 3 * T;
   c->tok_last.assign(c->V, -1);
+  {
+    std::vector<ColsumJob> jobs;
+    const int rows = rmsnorm_bwd_part_rows(c->T);
+    for (int site = 0; site < 2 * c->L + 1; site++) {
+      float *out = site == 0 ? c->G + c->off_gfinal
+                             : c->G + ((site & 1) ? c->lo[(site - 1) / 2].g_ffn : c->lo[(site - 2) / 2].g_att);
+      jobs.push_back({norm_part(c, site), out, rows, c->D});
+    }
+    if (c->c.qk_norm) {
+      int rq, rk;
+      qk_prep_bwd_part_rows(c->T, c->NH, c->NKV, &rq, &rk);
+      for (int l = 0; l < c->L; l++) {
+        jobs.push_back({qk_part(c, l), c->G + c->lo[l].gq, rq, c->HD});
+        jobs.push_back({qk_part(c, l) + (long)rq * c->HD, c->G + c->lo[l].gk, rk, c->HD});
+      }
+    }
+    if ((rc = ne_hip_status(hipMemcpy(c->cs_jobs, jobs.data(), jobs.size() * sizeof(ColsumJob),
+                                      hipMemcpyHostToDevice), "colsum jobs")))
+      goto fail;
+  }
   if ((rc = ne_hip_status(hipHostMalloc((void **)&c->h_tok, 8 * T * sizeof(int32_t), 0), "hipHostMalloc"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[0], hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->tok_ev[1], hipEventDisableTiming), "event"))) goto fail;
@@ -431,12 +462,16 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_QKV, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, QKV));
+    // QKV, W1|W3 and (backward) dO GEMMs leave their split-K partials to the kernel that
+    // reads their output first (QK-prep, SwiGLU, the attention delta)
+    SplitIn sp_h;
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, QKV, D, a.xn, D, Pb + o.wqkv, D, a.qkv, &sp_h,
+                        nullptr, 1.f, ovf + OVF_QKV));
     {
       ProfScope ps(c, NE_PROF_ATTN_FWD);
       NE_CHECK(launch_qk_prep_fwd(dt, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.qr, a.kr, a.rq, a.rk, T, S, c->NH, c->NKV,
-                                  c->HD, eps, c->st));
+                                  c->HD, eps, c->st, sp_h, ovf + OVF_QKV));
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       NE_CHECK(launch_attn_fwd(dt, at, c->st));
@@ -447,10 +482,11 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_FWD, OVF_H13, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, 2 * H));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, &sp_h,
+                        nullptr, 1.f, ovf + OVF_H13));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf + OVF_SWIGLU, c->st));
+      NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf + OVF_SWIGLU, c->st, sp_h, ovf + OVF_H13));
     }
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, &sp_x,
                         a.x2, alpha));
@@ -492,7 +528,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
+                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
@@ -508,13 +544,17 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
-                                  T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
+                                  T, D, ovf + OVF_NORM_BWD, norm_part(c, 1 + 2 * l), c->st, sp_d, true));
     }
     // attention: dbf = alpha * dx2
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DATTN, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, Q));
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q, nullptr, 0, u));
+    SplitIn sp_o;
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, &sp_o,
+                        nullptr, 1.f, ovf + OVF_DATTN));
     {
       ProfScope ps(c, NE_PROF_ATTN_BWD);
+      at.dsp = sp_o;
+      at.ovf_dout = ovf + OVF_DATTN;
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
@@ -525,7 +565,8 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
-                                  c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->gpart, c->st));
+                                  c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->c.qk_norm ? qk_part(c, l) : nullptr,
+                                  c->st, true));
     }
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
                   0, u));
@@ -535,8 +576,13 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       ProfScope ps(c, NE_PROF_NORM);
       // the bottom layer needs no 16-bit copy (the embedding scatter reads the fp32 dx)
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, l > 0 ? c->dbf : nullptr,
-                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, c->gpart, c->st, sp_d));
+                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st,
+                                  sp_d, true));
     }
+  }
+  {
+    ProfScope ps(c, NE_PROF_NORM);
+    NE_CHECK(launch_colsum_batch(c->cs_jobs, c->cs_njobs, std::max(c->D, c->HD), c->st));
   }
   {
     ProfScope ps(c, NE_PROF_EMBED);

@@ -96,20 +96,35 @@ int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *
 // in a second, ordered pass (deterministic); without it blocks add atomically.
 long rmsnorm_bwd_part_elems(int T, int D);
 long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD);
-// With sp.n > 0, dy is formed from split-K partials (SplitIn) instead of read.
+// With sp.n > 0, dy is formed from split-K partials (SplitIn) instead of read.  With
+// defer_colsum the partials are left for one colsum_batch launch (ColsumJob) later.
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg,
                        float dg_scale, int T, int D, int *ovf, float *part, hipStream_t s,
-                       const SplitIn &sp = SplitIn());
-int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s);
+                       const SplitIn &sp = SplitIn(), bool defer_colsum = false);
+// Ordered column sums of per-block partial rows: out[j] += sum_r part[r * n + j], r ascending
+// in the fixed grouping of colsum_kernel, for several independent jobs in one launch.
+struct ColsumJob {
+  const float *part;
+  float *out;
+  int rows, n;
+};
+int rmsnorm_bwd_part_rows(int T);                              // partial rows of one rmsnorm_bwd
+void qk_prep_bwd_part_rows(int T, int NH, int NKV, int *rows_q, int *rows_k);
+int launch_colsum_batch(const ColsumJob *jobs_dev, int njobs, int max_n, hipStream_t s);
+// With sp.n > 0 the 16-bit input (h13 / qkv, the GEMM's output) is formed from split-K
+// partials and written before use; ovf_h13 / ovf_qkv take the GEMM's overflow flag.
+int launch_swiglu_fwd(int dt, const h16_t *h13, h16_t *gate, int T, int H, int *ovf, hipStream_t s,
+                      const SplitIn &sp = SplitIn(), int *ovf_h13 = nullptr);
 int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, const float *sinb,
                        const float *gq, const float *gk, h16_t *qr, h16_t *kr, float *rq, float *rk,
-                       int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s);
+                       int T, int S, int NH, int NKV, int HD, float eps, hipStream_t s,
+                       const SplitIn &sp = SplitIn(), int *ovf_qkv = nullptr);
 int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qkv, long ld,
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk,
                        float dg_scale, int T, int S, int NH, int NKV, int HD, int *ovf, float *part,
-                       hipStream_t s);
+                       hipStream_t s, bool defer_colsum = false);
 
 // ---- attention (k_attn.hip): causal, GQA kv head = q head / (NH/NKV) ----
 struct AttnArgs {
@@ -126,6 +141,9 @@ struct AttnArgs {
   h16_t *dv; long lddv;          // [T, NKV*HD] 16-bit
   float *part;                   // nullable: [2][T, NH*HD] fp32 per-query-head dK/dV partials
                                  // (GQA only: one block per query head, then a head-order sum)
+  SplitIn dsp;                   // split-K partials of dout (its GEMM's reduction, done by the
+                                 // delta kernel, which writes dout); dsp.n = 0: dout is written
+  int *ovf_dout;                 // overflow flag of dout's 16-bit rounding (with dsp)
   int *ovf;
   int B, S, NH, NKV, HD;
   float scale;
