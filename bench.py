@@ -14,7 +14,7 @@ measured MFMA issue ceiling of ne_k_mfma_ceiling), the same step at batch 8 x se
 (`at_scale`), decode tokens/s at batch 1 and 32.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-decode]
-                  [--no-scale] [--no-graphs] [--calib-copy]
+                  [--no-scale] [--no-graphs] [--no-overlap] [--calib-copy]
 """
 import argparse
 import json
@@ -82,10 +82,11 @@ def batches(w, n, seed0=1000):
             for i in range(n)]
 
 
-def run_train(w, steps, warmup, graphs=True):
+def run_train(w, steps, warmup, graphs=True, overlap=True):
     alpha = 1.0 / math.sqrt(2.0 * w["n_layers"])
     m = ne.Model(**w, res_alpha=alpha, dtype=ne.NE_FP16)
     m.use_graphs(graphs)
+    m.overlap_weight_grads(overlap)
     init_weights(m, w)
     toks = batches(w, steps + warmup)
     lr = 3e-4
@@ -238,6 +239,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a captured HIP graph "
                          "(for tracers that do not follow graph launches)")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="run the weight-gradient GEMMs in order on the step's stream instead of on a "
+                         "second stream beside the activation-gradient chain")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run three plain 1 GiB device copies (a known-size kernel that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
@@ -252,7 +256,7 @@ def main():
     if a.calib_copy:
         calib_copy()
     ceil = mfma_ceiling()
-    r = run_train(w, a.steps, a.warmup, graphs=not a.no_graphs)
+    r = run_train(w, a.steps, a.warmup, graphs=not a.no_graphs, overlap=not a.no_overlap)
     summ = train_summary(w, r, ceil["mfma_32x32x16_tflops"])
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
@@ -293,7 +297,7 @@ def main():
     }
     if not a.no_scale and a.workload == "qwen3-0.6b-s256-b1":
         ws = WORKLOADS["qwen3-0.6b-s2048-b8"]
-        rs = run_train(ws, 3, 1, graphs=not a.no_graphs)
+        rs = run_train(ws, 3, 1, graphs=not a.no_graphs, overlap=not a.no_overlap)
         out["at_scale"] = {"workload": "qwen3-0.6b-s2048-b8", "tokens_per_step": ws["batch"] * ws["seq"],
                            **train_summary(ws, rs, ceil["mfma_32x32x16_tflops"])}
     if not a.no_decode and a.workload.startswith("qwen3"):

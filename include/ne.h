@@ -103,11 +103,22 @@ int ne_get_tensor(ne_ctx *ctx, int kind, int tensor_id, float *host, size_t n);
  * embed_backward. */
 int ne_train_step(ne_ctx *ctx, const int32_t *tokens, float loss_scale, float *loss_out);
 /* Replay the step, and each position of ne_decode, from captured HIP graphs (default on;
- * the step's graph is off while per-kernel profiling is enabled).  The step's graph is
+ * the step's graph is used only while ne_overlap_weight_grads is off and per-kernel
+ * profiling is disabled: the two-stream step runs faster from eager launches).  The step's graph is
  * captured on first use per (fresh accumulation, loss_scale, internal gradient scale), the
  * decode graphs per (batch size, greedy or sampling); they replace the reference's
  * per-kernel ANE dispatch (TD/io.h:190-229).  Off: every kernel is launched eagerly. */
 int ne_use_graphs(ne_ctx *ctx, int on);
+/* Run the step's weight-gradient GEMMs (and the embedding gradient of the classifier) on a
+ * second HIP stream beside the chain of activation gradients, handed over once per layer
+ * (default on; off: one stream, in order, replayed from a graph if ne_use_graphs is on).
+ * Results are identical either way: every kernel writes its own outputs and the second
+ * stream is joined before the gain-gradient sums and the embedding scatter.
+ * Mirrors the reference's dW scheduling: its cblas weight-gradient sgemms are queued on a
+ * concurrent dispatch queue beside the ANE backward evals (TD/train.m:377-378, 521, 554,
+ * 588, 628) and awaited once before the update (TD/train.m:756).  The switch has no
+ * counterpart there: it is for timing, and for checking that the two orders agree. */
+int ne_overlap_weight_grads(ne_ctx *ctx, int on);
 
 /* Scale grads by grad_scale, global L2 norm, clip to `clip` (if > 0), AdamW with
  * bias-corrected moments (t = ++adam_t), weight decay wd on matrices and the embedding

@@ -116,7 +116,8 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
     d[col] = o1;
     d[g.N + col] = o3;
   } else if constexpr (EPI == EPI_CE_BWD) {
-    float p = col < g.n_valid ? __expf(v - g.lse[row]) : 0.f;  // padding columns: no gradient
+    const float e = __expf(v - g.lse[row]);
+    float p = col < g.n_valid ? e : 0.f;  // padding columns: no gradient (a select, not a branch)
     if (col == g.targets[row]) p -= 1.f;
     const h16_t o = HT::h(p * g.scale);
     bad |= HT::bad(o);
@@ -216,11 +217,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         // reduce over the 32 lanes sharing this row (lanes with equal lane>>5)
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        // a row with no valid column in this tile has mx = -inf and sum 0
+        const float mxs = mx > -INFINITY ? mx : 0.f;
         float s = 0.f;
-        if (mx > -INFINITY) {
 #pragma unroll
-          for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] - mx);
-        }
+        for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] - mxs);
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         if ((lane & 31) == 0) {

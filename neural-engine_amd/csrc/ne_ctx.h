@@ -49,6 +49,10 @@ struct ne_ctx {
   int32_t skipped = 0;    // optimizer steps skipped after a 16-bit overflow
   int good_steps = 0;     // consecutive non-overflowing optimizer steps
   hipStream_t st = nullptr;
+  // weight-gradient GEMMs run on st2 beside the dX chain on st: forked after the GEMM that
+  // produces each dY, joined once before the end of the backward
+  hipStream_t st2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   long n_params = 0, n_decay = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
   h16_t *Pb = nullptr;
@@ -60,6 +64,9 @@ struct ne_ctx {
   float *xL, *rf;
   h16_t *xf;
   float *dx, *dx2, *dtmp, *dq, *dk, *delta, *attn_part;
+  // per layer (the weight-gradient GEMMs on st2 read them while st moves on): dbf [2L][T, D]
+  // (alpha * dx into the FFN of layer l at 2l, into its attention at 2l + 1), dh13 [L][T, 2H],
+  // dqkv [L][T, QKV]
   h16_t *dbf, *dh13, *dattn, *dqkv, *dlogits;
   float *ce_part, *ce_tgt, *ce_lse, *ce_rows, *loss;
   int32_t *tok_in, *tok_tgt, *tok_nxt, *tok_first;  // [T] each, one staging copy
@@ -71,8 +78,9 @@ struct ne_ctx {
                           // of this accumulation window was not finite
   int32_t last_ovf_sites = 0;  // bit mask of the sites that flagged the last skipped step
   bool grads_fresh = true;     // G holds no accumulation yet: the next step overwrites it
-  float *ws = nullptr;         // split-K workspace
-  long ws_elems = 0;
+  float *ws = nullptr;         // split-K workspace (st)
+  float *ws2 = nullptr;        // split-K workspace of the weight-gradient GEMMs (st2)
+  long ws_elems = 0;           // capacity of each, floats
   float *gpart = nullptr;      // per-block gain-gradient partials: one slab per norm site
   long rms_slab = 0, qk_slab = 0;  // floats per RMSNorm / QK-norm site
   ColsumJob *cs_jobs = nullptr;    // device table: every site's ordered partial sum, one launch
@@ -84,6 +92,7 @@ struct ne_ctx {
   struct GraphEntry { bool fresh; float loss_scale; float gs; hipGraphExec_t exec; };
   std::vector<GraphEntry> graphs;
   bool use_graphs = true;
+  bool overlap_wgrad = true;  // weight-gradient GEMMs on st2 (ne_overlap_weight_grads)
   float *h_scalar = nullptr; // pinned [4]
   int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};

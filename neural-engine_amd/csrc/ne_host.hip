@@ -112,6 +112,54 @@ int gemm(ne_ctx *c, int fam, int site, int layout, int epi, int M, int N, int K,
   return gemm_launch(c->dt, layout, epi, g, c->st);
 }
 
+// Weight-gradient GEMM C[M,N] (fp32, = or +=) of the step's backward; on st2 when the step
+// forks (see Fork), else in order on st.
+// Its split-K partials (if any) go to ws2 either way, so they never meet the dX partials
+// that a consumer has yet to read from ws.
+int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X,
+            long ldx, float *C, float u) {
+  ProfScope ps(c, fam);
+  GemmArgs g = {};
+  g.M = M; g.N = N; g.K = K;
+  g.A = dY; g.lda = ldy; g.B = X; g.ldb = ldx; g.C = C; g.ldc = N;
+  g.alpha = u;
+  g.ws = c->ws2;
+  g.ws_elems = c->ws_elems;
+  return gemm_launch(c->dt, GEMM_TN, epi, g, side ? c->st2 : c->st);
+}
+
+// Weight-gradient GEMMs of the backward.  With `on`, they are queued and handed to st2 in
+// batches: flush() makes st2 wait for everything enqueued on st so far (inside a stream
+// capture, a graph edge) and enqueues the batch there; join() makes st wait for st2.
+// Without, each runs at once, in order, on st (per-kernel-family event timing records on st).
+struct WgradQueue {
+  struct Job { int fam, epi, M, N, K; const h16_t *dY; long ldy; const h16_t *X; long ldx; float *C; float u; };
+  ne_ctx *c;
+  bool on;
+  std::vector<Job> jobs;
+  int add(int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X, long ldx, float *C,
+          float u) {
+    if (!on) return gemm_dw(c, false, fam, epi, M, N, K, dY, ldy, X, ldx, C, u);
+    jobs.push_back({fam, epi, M, N, K, dY, ldy, X, ldx, C, u});
+    return 0;
+  }
+  int flush() {
+    if (!on || jobs.empty()) return 0;
+    NE_HIP(hipEventRecord(c->ev_fork, c->st));
+    NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
+    for (const Job &j : jobs) NE_CHECK(gemm_dw(c, true, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u));
+    jobs.clear();
+    return 0;
+  }
+  int join() {
+    if (!on) return 0;
+    NE_CHECK(flush());
+    NE_HIP(hipEventRecord(c->ev_join, c->st2));
+    NE_HIP(hipStreamWaitEvent(c->st, c->ev_join, 0));
+    return 0;
+  }
+};
+
 // GEMM whose split-K reduction, when it splits, is left to the kernel that consumes C:
 // *sp then describes the partials in c->ws (C unwritten), else has n = 0 (C written).  C must
 // be [M, N] row-major with ldc = N; R (EPI_RESID) is the residual added after the sum.
@@ -256,7 +304,9 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->dx, T * D); pl.add(&c->dx2, T * D); pl.add(&c->dtmp, T * D);
   pl.add(&c->dq, T * Q); pl.add(&c->dk, T * KV); pl.add(&c->delta, T * NH);
   pl.add(&c->attn_part, c->NH != c->NKV ? 2 * T * Q : 1);
-  pl.add(&c->dbf, T * D); pl.add(&c->dh13, T * 2 * H); pl.add(&c->dattn, T * Q); pl.add(&c->dqkv, T * QKV);
+  const size_t L = c->L;
+  pl.add(&c->dbf, 2 * L * T * D); pl.add(&c->dh13, L * T * 2 * H); pl.add(&c->dattn, T * Q);
+  pl.add(&c->dqkv, L * T * QKV);
   pl.add(&c->dlogits, T * (size_t)c->V);
   pl.add(&c->ce_part, T * (size_t)(c->V / 64) * 2);
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
@@ -266,6 +316,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
   c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
+  pl.add(&c->ws2, (size_t)c->ws_elems);
   // gain-gradient partials of every norm site (2L+1 RMSNorms, L QK-norm pairs), summed by one
   // ordered launch at the end of the backward
   c->rms_slab = rmsnorm_bwd_part_elems(c->T, c->D);
@@ -276,6 +327,9 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
 
   int rc = 0;
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking), "stream"))) goto fail;
+  if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st2, hipStreamNonBlocking), "stream"))) goto fail;
+  if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event"))) goto fail;
+  if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
   pl.assign((char *)c->arena);
   c->tok_tgt = c->tok_in + T;
@@ -341,7 +395,10 @@ fail:
 extern "C" void ne_destroy(ne_ctx *c) {
   if (!c) return;
   if (c->st) hipStreamSynchronize(c->st);
+  if (c->st2) hipStreamSynchronize(c->st2);
   for (auto &e : c->graphs) hipGraphExecDestroy(e.exec);
+  if (c->ev_fork) hipEventDestroy(c->ev_fork);
+  if (c->ev_join) hipEventDestroy(c->ev_join);
   for (int i = 0; i < 2; i++)
     if (c->tok_ev[i]) hipEventDestroy(c->tok_ev[i]);
   decode_free(c);
@@ -357,6 +414,7 @@ extern "C" void ne_destroy(ne_ctx *c) {
   if (c->h_tok) hipHostFree(c->h_tok);
   if (c->h_scalar) hipHostFree(c->h_scalar);
   if (c->h_ovf) hipHostFree(c->h_ovf);
+  if (c->st2) hipStreamDestroy(c->st2);
   if (c->st) hipStreamDestroy(c->st);
   delete c;
 }
@@ -423,7 +481,7 @@ extern "C" int ne_set_state(ne_ctx *c, const ne_train_state *st) {
 
 // Enqueue one forward+backward on c->st with token ids already in c->tok_in/tok_tgt.
 // Free of host synchronisation and memsets, so it can be captured into a HIP graph.
-static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
+static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two) {
   const int T = c->T, S = c->S, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, V = c->V;
   const float alpha = c->c.res_alpha, eps = c->c.norm_eps;
   const h16_t *Pb = c->Pb;
@@ -511,45 +569,53 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
   }
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------
-  // The dX GEMMs feeding an RMSNorm backward leave their split-K partials to it (sp_d); the
-  // weight-gradient GEMM beside each runs first, since both split into the one workspace.
+  // The dX GEMMs feeding an RMSNorm backward leave their split-K partials to it (sp_d).  The
+  // weight-gradient GEMMs run on st2, forked after the kernel producing their dY: what they
+  // read (dlogits, the saved activations, the per-layer dbf / dh13 / dqkv) is not written
+  // again in this step, so st never waits for them until the join before the gain sums.
+  WgradQueue wq{c, two, {}};
+  const size_t TD = (size_t)T * D;
   SplitIn sp_d;
   if (compact) {
     // compact embedding gradient, then added to its rows (TD/cpu_ops.h:425-431); the rows
     // outside the compact vocabulary get only the input-embedding gradient
-    NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_F32, Vc, D, T, c->dlogits, Vc, c->xf, D, c->gcE, D, nullptr, 0, u));
+    NE_CHECK(wq.add(NE_PROF_CE, EPI_F32, Vc, D, T, c->dlogits, Vc, c->xf, D, c->gcE, u));
+    NE_CHECK(wq.flush());
     ProfScope ps(c, NE_PROF_CE);
-    if (fresh) NE_CHECK(launch_fill_f32(G + c->off_E, 0.f, (long)V * D, c->st));
-    NE_CHECK(launch_scatter_add_rows(G + c->off_E, c->gcE, c->cids, c->cv, D, c->st));
+    hipStream_t sd = wq.on ? c->st2 : c->st;
+    if (fresh) NE_CHECK(launch_fill_f32(G + c->off_E, 0.f, (long)V * D, sd));
+    NE_CHECK(launch_scatter_add_rows(G + c->off_E, c->gcE, c->cids, c->cv, D, sd));
   } else {
-    NE_CHECK(gemm(c, NE_PROF_CE, -1, GEMM_TN, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, D, nullptr, 0, u));
+    NE_CHECK(wq.add(NE_PROF_CE, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, u));
+    NE_CHECK(wq.flush());
   }
   NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, Vc, c->dlogits, Vc, Ecls, D, c->dtmp, &sp_d));
   {
     ProfScope ps(c, NE_PROF_NORM);
-    NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx, c->dbf, alpha,
-                                G + c->off_gfinal, u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true));
+    NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx,
+                                c->dbf + 2 * (size_t)(c->L - 1) * TD, alpha, G + c->off_gfinal, u, T, D,
+                                ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
-    // FFN: dbf = alpha * dx
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DH13, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, c->dbf, D, Pb + o.w2, H, c->dh13, 2 * H,
-                  a.h13, 2 * H));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, H, T, c->dbf, D, a.gate, H, G + o.w2, H, nullptr, 0, u));
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, 2 * H, D, T, c->dh13, 2 * H, a.x2n, D, G + o.w13, D,
-                  nullptr, 0, u));
-    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, c->dh13, 2 * H, Pb + o.w13, D, c->dtmp,
+    h16_t *dbf_ffn = c->dbf + 2 * (size_t)l * TD, *dbf_att = dbf_ffn + TD;
+    h16_t *dh13 = c->dh13 + (size_t)l * T * 2 * H, *dqkv = c->dqkv + (size_t)l * T * QKV;
+    // FFN: dbf_ffn = alpha * dx
+    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DH13, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, dbf_ffn, D, Pb + o.w2, H, dh13,
+                  2 * H, a.h13, 2 * H));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, H, T, dbf_ffn, D, a.gate, H, G + o.w2, u));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, 2 * H, D, T, dh13, 2 * H, a.x2n, D, G + o.w13, u));
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, dh13, 2 * H, Pb + o.w13, D, c->dtmp,
                         &sp_d));
     {
       ProfScope ps(c, NE_PROF_NORM);
-      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, c->dbf, alpha, G + o.g_ffn, u,
-                                  T, D, ovf + OVF_NORM_BWD, norm_part(c, 1 + 2 * l), c->st, sp_d, true));
+      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, dbf_att, alpha, G + o.g_ffn,
+                                  u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 1 + 2 * l), c->st, sp_d, true));
     }
-    // attention: dbf = alpha * dx2
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, D, Q, T, c->dbf, D, a.attn, Q, G + o.wo, Q, nullptr, 0, u));
+    // attention: dbf_att = alpha * dx2
     SplitIn sp_o;
-    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_H16, T, Q, D, c->dbf, D, Pb + o.wo, Q, c->dattn, &sp_o,
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_H16, T, Q, D, dbf_att, D, Pb + o.wo, Q, c->dattn, &sp_o,
                         nullptr, 1.f, ovf + OVF_DATTN));
     {
       ProfScope ps(c, NE_PROF_ATTN_BWD);
@@ -558,28 +624,29 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
       at.q = a.qr; at.ldq = Q; at.k = a.kr; at.ldk = KV; at.v = a.qkv + Q + KV; at.ldv = QKV;
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
-      at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = c->dqkv + Q + KV; at.lddv = QKV;
+      at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = dqkv + Q + KV; at.lddv = QKV;
       at.part = c->NH != c->NKV ? c->attn_part : nullptr;
       at.ovf = ovf + OVF_DV;
       NE_CHECK(launch_attn_bwd(dt, at, c->st));
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
-                                  c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, c->dqkv,
+                                  c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, dqkv,
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
                                   c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->c.qk_norm ? qk_part(c, l) : nullptr,
                                   c->st, true));
     }
-    NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, -1, GEMM_TN, EPI_DW, QKV, D, T, c->dqkv, QKV, a.xn, D, G + o.wqkv, D, nullptr,
-                  0, u));
-    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, c->dqkv, QKV, Pb + o.wqkv, D, c->dtmp,
-                        &sp_d));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));
+    NE_CHECK(wq.flush());  // one hand-over per layer
+    NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, dqkv, QKV, Pb + o.wqkv, D, c->dtmp, &sp_d));
     {
       ProfScope ps(c, NE_PROF_NORM);
       // the bottom layer needs no 16-bit copy (the embedding scatter reads the fp32 dx)
-      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx, l > 0 ? c->dbf : nullptr,
-                                  alpha, G + o.g_att, u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st,
-                                  sp_d, true));
+      NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx,
+                                  l > 0 ? c->dbf + 2 * (size_t)(l - 1) * TD : nullptr, alpha, G + o.g_att, u, T, D,
+                                  ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st, sp_d, true));
     }
   }
+  NE_CHECK(wq.join());
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_colsum_batch(c->cs_jobs, c->cs_njobs, std::max(c->D, c->HD), c->st));
@@ -592,7 +659,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh) {
 }
 
 // Graph cache: one captured step per (fresh, loss scale, internal gradient scale).
-static int train_step_graph(ne_ctx *c, float loss_scale, bool fresh) {
+static int train_step_graph(ne_ctx *c, float loss_scale, bool fresh, bool two) {
   for (auto &e : c->graphs)
     if (e.fresh == fresh && e.loss_scale == loss_scale && e.gs == c->gs) {
       NE_HIP(hipGraphLaunch(e.exec, c->st));
@@ -600,7 +667,7 @@ static int train_step_graph(ne_ctx *c, float loss_scale, bool fresh) {
     }
   hipGraph_t graph = nullptr;
   NE_HIP(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
-  const int rc = train_step_enqueue(c, loss_scale, fresh);
+  const int rc = train_step_enqueue(c, loss_scale, fresh, two);
   const hipError_t ec = hipStreamEndCapture(c->st, &graph);
   if (rc) {
     if (graph) (void)hipGraphDestroy(graph);
@@ -652,8 +719,13 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   c->grads_fresh = false;
   // event timing of kernels inside the step needs eager launches; optimizer families don't
   const int step_fams = c->prof.mask & ~((1 << NE_PROF_ADAM) | (1 << NE_PROF_GNORM));
-  if (c->use_graphs && !(c->prof.on && step_fams)) NE_CHECK(train_step_graph(c, loss_scale, fresh));
-  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh));
+  const bool profiled = c->prof.on && step_fams;
+  // per-family event timing needs every kernel of the step on st.  The two-stream step is
+  // launched eagerly: replaying it from a graph measured slower than in order on one stream
+  // (the branches' hand-overs cost more in a graph than between eager launches).
+  const bool two = c->overlap_wgrad && !profiled;
+  if (c->use_graphs && !profiled && !two) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
+  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two));
   if (loss_out) {
     NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
@@ -665,6 +737,17 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
 extern "C" int ne_use_graphs(ne_ctx *c, int on) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   c->use_graphs = on != 0;
+  return 0;
+}
+
+extern "C" int ne_overlap_weight_grads(ne_ctx *c, int on) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  if (c->overlap_wgrad == (on != 0)) return 0;
+  NE_HIP(hipStreamSynchronize(c->st));
+  // the captured steps bake the stream layout in
+  for (auto &e : c->graphs) (void)hipGraphExecDestroy(e.exec);
+  c->graphs.clear();
+  c->overlap_wgrad = on != 0;
   return 0;
 }
 

@@ -26,7 +26,7 @@ OVF_SITES = ("norm_fwd", "qkv", "h13", "swiglu", "dlogits", "norm_bwd", "dh13", 
 # every symbol include/ne.h declares
 EXPORTS = (
     "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
-    "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_optimizer_step",
+    "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_overlap_weight_grads", "ne_optimizer_step",
     "ne_zero_grads",
     "ne_grad_scale_info", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
@@ -107,6 +107,7 @@ def lib():
         "ne_get_tensor": (I, [P, I, I, P, C.c_size_t]),
         "ne_train_step": (I, [P, P, F, P]),
         "ne_use_graphs": (I, [P, I]),
+        "ne_overlap_weight_grads": (I, [P, I]),
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
         "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
@@ -245,6 +246,9 @@ class Model:
 
     def use_graphs(self, on=True):
         check(lib().ne_use_graphs(self._h, int(on)), "use_graphs")
+
+    def overlap_weight_grads(self, on=True):
+        check(lib().ne_overlap_weight_grads(self._h, int(on)), "overlap_weight_grads")
 
     def set_vocab_map(self, ids):
         """Vocabulary compaction: classifier + softmax over these embedding rows (None: all)."""

@@ -193,6 +193,7 @@ def test_graph_replay_matches_eager_launches():
     for graphs in (True, False):
         m = ne.Model.from_oracle(cfg, batch=2)
         m.use_graphs(graphs)
+        m.overlap_weight_grads(False)  # the two-stream step is never captured
         m.set_params(P)
         losses = [m.train_step(t, 256.0) for t in toks] + [m.train_step(toks[0], 256.0)]
         out.append((losses, m.get_all(shapes(cfg), ne.NE_GRAD)))
@@ -235,19 +236,26 @@ def test_decode_sampling_mfma_path():
     m.close()
 
 
-def test_step_identical_across_launch_modes():
+@pytest.mark.parametrize("compact", [False, True])
+def test_step_identical_across_launch_modes(compact):
     """The step gives bit-identical losses and gradients over two accumulating micro-steps
-    whether its kernels are launched eagerly, replayed from a HIP graph, or launched with
-    per-kernel profiling events between them."""
+    whether its kernels are launched eagerly with the weight-gradient GEMMs on a second
+    stream (two_streams, the default), in order on one stream with per-kernel profiling
+    events between them (profiled), or in order replayed from a HIP graph (graph)."""
     cfg = om.tiny(**CASES["qwen3"], n_layers=2, dim=1024, hidden=4096, vocab=4096, seq=256)
     P = om.init_params(cfg, seed=0, std=0.02)
     toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2)]
+    ids = np.unique(np.concatenate([t.ravel() for t in toks])).astype(np.int32)
     out = []
-    for mode in ("profiled", "eager", "graph"):
+    for mode in ("profiled", "two_streams", "graph"):
+        print(f"\n[compact={compact}] mode {mode}", flush=True)
         m = ne.Model.from_oracle(cfg, batch=2)
         m.use_graphs(mode == "graph")
+        m.overlap_weight_grads(mode == "two_streams")
         if mode == "profiled":
             m.prof_enable()
+        if compact:
+            m.set_vocab_map(ids)
         m.set_params(P)
         losses = [m.train_step(t, 256.0) for t in toks]
         out.append((losses, m.get_all(shapes(cfg), ne.NE_GRAD)))
