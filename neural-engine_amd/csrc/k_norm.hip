@@ -31,16 +31,22 @@ __global__ void embed_bwd_kernel(float *__restrict__ gE, const int32_t *__restri
 // Deterministic form of embed_bwd_kernel: the rows of one token id are chained in token
 // order (nxt[t]: next row with the same id, -1 at the end; first[t]: t is the id's first
 // row), and the wave of the first row sums the chain in that order and adds it to gE once.
-// No atomics, so the result does not depend on scheduling.
+// No atomics, so the result does not depend on scheduling.  With dsq, slot t receives the
+// change of the sum of squares of the gE row the wave of row t updated (0 for the other rows),
+// so a sum of squares of gE taken before this kernel can be brought up to date.
 constexpr int EMB_MAXV = 8;  // float4 per lane: D <= 2048
 __global__ __launch_bounds__(256) void embed_bwd_chain_kernel(float *__restrict__ gE, const int32_t *__restrict__ tok,
                                                               const int32_t *__restrict__ nxt,
                                                               const int32_t *__restrict__ first,
                                                               const float *__restrict__ dx, float scale, int T,
-                                                              int D) {
+                                                              int D, double *__restrict__ dsq) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= T || !first[row]) return;
+  if (row >= T) return;
+  if (!first[row]) {
+    if (dsq && lane == 0) dsq[row] = 0.0;
+    return;
+  }
   const int D4 = D / 4;
   float4 acc[EMB_MAXV];
 #pragma unroll
@@ -57,14 +63,21 @@ __global__ __launch_bounds__(256) void embed_bwd_chain_kernel(float *__restrict_
     }
   }
   float4 *dst = (float4 *)(gE + (long)tok[row] * D);
+  double d = 0.0;
 #pragma unroll
   for (int j = 0; j < EMB_MAXV; j++) {
     const int i = lane + 64 * j;
     if (i < D4) {
       float4 g = dst[i];
+      const float o = g.x * g.x + g.y * g.y + g.z * g.z + g.w * g.w;
       g.x += scale * acc[j].x; g.y += scale * acc[j].y; g.z += scale * acc[j].z; g.w += scale * acc[j].w;
       dst[i] = g;
+      d += (double)(g.x * g.x + g.y * g.y + g.z * g.z + g.w * g.w) - (double)o;
     }
+  }
+  if (dsq) {
+    d = wave_sum_d(d);
+    if (lane == 0) dsq[row] = d;
   }
 }
 
@@ -540,9 +553,10 @@ int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale
 }
 
 int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, const int32_t *first,
-                           const float *dx, float scale, int T, int D, hipStream_t s) {
+                           const float *dx, float scale, int T, int D, hipStream_t s, double *dsq) {
   if (D % 4 || D > 4 * 64 * EMB_MAXV) return ne_fail(NE_ERR_ARG, "embed_bwd: D must be a multiple of 4, <= 2048");
-  hipLaunchKernelGGL(embed_bwd_chain_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, nxt, first, dx, scale, T, D);
+  hipLaunchKernelGGL(embed_bwd_chain_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gE, tok, nxt, first, dx, scale, T, D,
+                     dsq);
   return ne_hip_status(hipGetLastError(), "embed_bwd_chain");
 }
 

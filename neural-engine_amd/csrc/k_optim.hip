@@ -36,7 +36,8 @@ __global__ void clip_finalize_kernel(const double *__restrict__ partials, int np
   for (int i = threadIdx.x; i < nparts; i += 64) s += partials[i];
   s = wave_sum_d(s);
   if (threadIdx.x == 0) {
-    const float norm = (float)(sqrt(s) * (double)grad_scale);
+    // the partials may include signed row changes (embedding scatter): never below 0
+    const float norm = (float)(sqrt(fmax(s, 0.0)) * (double)grad_scale);
     float f = grad_scale;
     if (clip > 0.f && norm > clip) f *= clip / norm;
     gscale[0] = f;

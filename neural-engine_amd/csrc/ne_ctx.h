@@ -72,7 +72,11 @@ struct ne_ctx {
   int32_t *tok_in, *tok_tgt, *tok_nxt, *tok_first;  // [T] each, one staging copy
   std::vector<int32_t> tok_last;                     // host scratch [V] for the id chains
   float *cosb, *sinb;
+  // sum-of-squares partials of the gradient, in a fixed reduction order: gn_slots() slots.
+  // The step fills them as each part of G becomes final (see gn_layer etc. in ne_host.hip);
+  // gn_ready: they describe G as it is now (else the optimizer sums G itself)
   double *gn_part;
+  bool gn_ready = false;
   float *gscale, *gnorm;
   int *ovf;               // device flags [32], one per conversion site (OVF_*): a 16-bit value
                           // of this accumulation window was not finite

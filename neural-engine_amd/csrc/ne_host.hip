@@ -132,22 +132,37 @@ int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h
 // batches: flush() makes st2 wait for everything enqueued on st so far (inside a stream
 // capture, a graph edge) and enqueues the batch there; join() makes st wait for st2.
 // Without, each runs at once, in order, on st (per-kernel-family event timing records on st).
+// Also queued: the sum of squares of a finished part of G into its partial slots (sumsq()).
 struct WgradQueue {
-  struct Job { int fam, epi, M, N, K; const h16_t *dY; long ldy; const h16_t *X; long ldx; float *C; float u; };
+  struct Job {
+    int fam, epi, M, N, K;
+    const h16_t *dY; long ldy; const h16_t *X; long ldx; float *C; float u;
+    long n; int nparts; double *part;  // M == 0: sum of squares of C[0, n) into part[0, nparts)
+  };
   ne_ctx *c;
   bool on;
   std::vector<Job> jobs;
+  int run(const Job &j, bool side) {
+    if (j.M == 0) return launch_sumsq(j.C, j.n, j.part, j.nparts, side ? c->st2 : c->st);
+    return gemm_dw(c, side, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u);
+  }
+  int push(const Job &j) {
+    if (!on) return run(j, false);
+    jobs.push_back(j);
+    return 0;
+  }
   int add(int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X, long ldx, float *C,
           float u) {
-    if (!on) return gemm_dw(c, false, fam, epi, M, N, K, dY, ldy, X, ldx, C, u);
-    jobs.push_back({fam, epi, M, N, K, dY, ldy, X, ldx, C, u});
-    return 0;
+    return push({fam, epi, M, N, K, dY, ldy, X, ldx, C, u, 0, 0, nullptr});
+  }
+  int sumsq(const float *g, long n, long slot, int nparts) {
+    return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, n, nparts, c->gn_part + slot});
   }
   int flush() {
     if (!on || jobs.empty()) return 0;
     NE_HIP(hipEventRecord(c->ev_fork, c->st));
     NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
-    for (const Job &j : jobs) NE_CHECK(gemm_dw(c, true, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u));
+    for (const Job &j : jobs) NE_CHECK(run(j, true));
     jobs.clear();
     return 0;
   }
@@ -192,6 +207,17 @@ int gemm_split(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, con
 // 2 + 2l: its attention norm) and of layer l's QK-norm pair.
 float *norm_part(ne_ctx *c, int site) { return c->gpart + (long)site * c->rms_slab; }
 float *qk_part(ne_ctx *c, int l) { return c->gpart + (long)(2 * c->L + 1) * c->rms_slab + (long)l * c->qk_slab; }
+
+// Sum-of-squares partials of G, reduced in slot order by the optimizer: layer l's matrix
+// gradients (contiguous from lo[l].wqkv), the embedding, the gains, then one slot per token
+// row for the change the embedding scatter makes to the row it updates.
+constexpr int GN_LAYER = 128, GN_EMBED = 512, GN_GAINS = 16, GN_FULL = 1024;
+long gn_layer(const ne_ctx *c, int l) { (void)c; return (long)l * GN_LAYER; }
+long gn_embed(const ne_ctx *c) { return (long)c->L * GN_LAYER; }
+long gn_gains(const ne_ctx *c) { return gn_embed(c) + GN_EMBED; }
+long gn_rows(const ne_ctx *c) { return gn_gains(c) + GN_GAINS; }
+long gn_slots(const ne_ctx *c) { return gn_rows(c) + c->T; }
+long layer_params(const ne_ctx *c) { return (long)(c->QKV + c->Q + 3L * c->H) * c->D; }
 
 int validate(const ne_config *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null config");
@@ -312,7 +338,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
   pl.add(&c->tok_in, 4 * T);  // inputs, targets, id chains: filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
-  pl.add(&c->gn_part, 1024); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
+  pl.add(&c->gn_part, (size_t)std::max<long>(gn_slots(c), GN_FULL)); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
   c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
@@ -444,6 +470,7 @@ extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, siz
     NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
     c->grads_fresh = false;
   }
+  if (kind == NE_GRAD) c->gn_ready = false;  // the step's sum-of-squares partials no longer hold
   NE_HIP(hipMemcpyAsync(base + c->t_off[id], host, n * 4, hipMemcpyHostToDevice, c->st));
   if (kind == NE_PARAM) NE_CHECK(launch_f32_to_h16(c->dt, c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
@@ -580,15 +607,18 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two)
     // compact embedding gradient, then added to its rows (TD/cpu_ops.h:425-431); the rows
     // outside the compact vocabulary get only the input-embedding gradient
     NE_CHECK(wq.add(NE_PROF_CE, EPI_F32, Vc, D, T, c->dlogits, Vc, c->xf, D, c->gcE, u));
-    NE_CHECK(wq.flush());
+    NE_CHECK(wq.flush());  // the fill and scatter below follow it on the same stream
     ProfScope ps(c, NE_PROF_CE);
     hipStream_t sd = wq.on ? c->st2 : c->st;
     if (fresh) NE_CHECK(launch_fill_f32(G + c->off_E, 0.f, (long)V * D, sd));
     NE_CHECK(launch_scatter_add_rows(G + c->off_E, c->gcE, c->cids, c->cv, D, sd));
   } else {
     NE_CHECK(wq.add(NE_PROF_CE, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, u));
-    NE_CHECK(wq.flush());
   }
+  // the embedding gradient as it stands before the input-embedding scatter (which reports
+  // its change per row)
+  NE_CHECK(wq.sumsq(G + c->off_E, (long)V * D, gn_embed(c), GN_EMBED));
+  NE_CHECK(wq.flush());
   NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, Vc, c->dlogits, Vc, Ecls, D, c->dtmp, &sp_d));
   {
     ProfScope ps(c, NE_PROF_NORM);
@@ -636,6 +666,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two)
     }
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));
+    NE_CHECK(wq.sumsq(G + o.wqkv, layer_params(c), gn_layer(c, l), GN_LAYER));
     NE_CHECK(wq.flush());  // one hand-over per layer
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, dqkv, QKV, Pb + o.wqkv, D, c->dtmp, &sp_d));
     {
@@ -650,10 +681,12 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two)
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_colsum_batch(c->cs_jobs, c->cs_njobs, std::max(c->D, c->HD), c->st));
+    NE_CHECK(launch_sumsq(G + c->n_decay, c->n_params - c->n_decay, c->gn_part + gn_gains(c), GN_GAINS, c->st));
   }
   {
     ProfScope ps(c, NE_PROF_EMBED);
-    NE_CHECK(launch_embed_bwd_chain(G + c->off_E, c->tok_in, c->tok_nxt, c->tok_first, c->dx, u, T, D, c->st));
+    NE_CHECK(launch_embed_bwd_chain(G + c->off_E, c->tok_in, c->tok_nxt, c->tok_first, c->dx, u, T, D, c->st,
+                                    c->gn_part + gn_rows(c)));
   }
   return 0;
 }
@@ -724,8 +757,10 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // launched eagerly: replaying it from a graph measured slower than in order on one stream
   // (the branches' hand-overs cost more in a graph than between eager launches).
   const bool two = c->overlap_wgrad && !profiled;
+  c->gn_ready = false;
   if (c->use_graphs && !profiled && !two) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
   else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two));
+  c->gn_ready = true;  // the step refreshed every sum-of-squares partial of G
   if (loss_out) {
     NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
@@ -815,8 +850,15 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   }
   {
     ProfScope ps(c, NE_PROF_GNORM);
-    NE_CHECK(launch_sumsq(c->G, c->n_params, c->gn_part, 1024, c->st));
-    NE_CHECK(launch_clip_finalize(c->gn_part, 1024, grad_scale, clip, c->gscale, c->gnorm, c->st));
+    // the last micro-step left the partials of G as it is now; otherwise (G written through
+    // ne_set_tensor, or no micro-step since the last update) sum it here
+    if (c->gn_ready && !c->grads_fresh) {
+      NE_CHECK(launch_clip_finalize(c->gn_part, (int)gn_slots(c), grad_scale, clip, c->gscale, c->gnorm, c->st));
+    } else {
+      if (c->grads_fresh) NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
+      NE_CHECK(launch_sumsq(c->G, c->n_params, c->gn_part, GN_FULL, c->st));
+      NE_CHECK(launch_clip_finalize(c->gn_part, GN_FULL, grad_scale, clip, c->gscale, c->gnorm, c->st));
+    }
   }
   c->state.adam_t += 1;
   const int t = c->state.adam_t;
@@ -827,8 +869,6 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   a.bc1 = 1.f - powf(b1, (float)t);
   a.bc2 = 1.f - powf(b2, (float)t);
   a.gscale = c->gscale; a.zero_grad = 0;
-  const bool fresh = c->grads_fresh;  // no micro-step since the last update: all-zero grads
-  if (fresh) NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
   {
     ProfScope ps(c, NE_PROF_ADAM);
     NE_CHECK(launch_adam(c->dt, a, c->st));

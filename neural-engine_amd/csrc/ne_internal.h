@@ -87,8 +87,10 @@ int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D,
 int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D,
                      hipStream_t s);
 // Deterministic scatter over per-id row chains (nxt / first arrays built on the host).
+// dsq (nullable, [T] doubles): per row, the change of the sum of squares of the gE row it
+// updated (0 for rows that are not the first of their id).
 int launch_embed_bwd_chain(float *gE, const int32_t *tok, const int32_t *nxt, const int32_t *first,
-                           const float *dx, float scale, int T, int D, hipStream_t s);
+                           const float *dx, float scale, int T, int D, hipStream_t s, double *dsq = nullptr);
 // With sp.n > 0, x is formed from split-K partials (SplitIn) and written to x before use.
 int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *r, int T, int D,
                        float eps, int *ovf, hipStream_t s, const SplitIn &sp = SplitIn());

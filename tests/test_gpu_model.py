@@ -107,6 +107,46 @@ def test_optimizer_step_matches_oracle(clip):
     m.close()
 
 
+@pytest.mark.parametrize("compact", [False, True])
+@pytest.mark.parametrize("overlap", [False, True])
+def test_grad_norm_from_step_partials(compact, overlap):
+    """The optimizer's gradient norm comes from sum-of-squares partials the step leaves as each
+    part of G becomes final (per layer, the embedding before the input-embedding scatter plus
+    the change the scatter makes to each row, the gains).  Over two accumulating micro-steps
+    (repeated token ids, so the scatter updates rows that already hold gradient) it equals the
+    float64 norm of the gradients read back; after a direct gradient write the optimizer sums
+    G itself."""
+    cfg = om.tiny(**CASES["qwen3"])
+    P = om.init_params(cfg, seed=0, std=0.02)
+    toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2)]
+    sh = shapes(cfg)
+    m = ne.Model.from_oracle(cfg, batch=2)
+    m.overlap_weight_grads(overlap)
+    if compact:
+        m.set_vocab_map(np.unique(np.concatenate([t.ravel() for t in toks])).astype(np.int32))
+    m.set_params(P)
+
+    def norm64(G):
+        return float(np.sqrt(sum(np.sum(g.astype(np.float64) ** 2) for g in G.values())))
+
+    for t in toks:
+        m.train_step(t, 256.0)
+    want = norm64(m.get_all(sh, ne.NE_GRAD)) / 256
+    gn = m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=0.0)
+    print(f"\n[compact={compact} overlap={overlap}] norm {gn:.7f} float64 {want:.7f}", flush=True)
+    assert abs(gn - want) <= 1e-6 * want, (gn, want)
+    m.train_step(toks[1], 256.0)
+    G = m.get_all(sh, ne.NE_GRAD)
+    G["layers.1.Wq"] = G["layers.1.Wq"] * 3.0
+    m.set("layers.1.Wq", G["layers.1.Wq"], ne.NE_GRAD)
+    want = norm64(G) / 256
+    gn = m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=0.0)
+    assert abs(gn - want) <= 1e-6 * want, (gn, want)
+    # no micro-step since the update: all-zero gradients
+    assert m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=0.0) == 0.0
+    m.close()
+
+
 def _held_params(cfg, dtype, seed=0, std=0.02):
     """Weights rounded to the context's 16-bit format, so the decode's weight shadow and the
     fp32 oracle see identical values."""
