@@ -53,6 +53,11 @@ struct ne_ctx {
   // produces each dY, joined once before the end of the backward
   hipStream_t st2 = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  // The optimizer's update also runs on st2, in chunks (0: embedding + gains, 1 + l: layer l)
+  // each marked by ev_adam[k]; the next step's forward waits for chunk k just before it reads
+  // what the chunk writes.  adam_pending: an update was enqueued that st has not waited for.
+  std::vector<hipEvent_t> ev_adam;
+  bool adam_pending = false;
   long n_params = 0, n_decay = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
   h16_t *Pb = nullptr;

@@ -64,28 +64,42 @@ struct Plan {
   }
 };
 
-void prof_begin(ne_ctx *c, int fam, hipEvent_t *e0) {
+void prof_begin(ne_ctx *c, int fam, hipEvent_t *e0, hipStream_t s) {
   if (!c->prof.on || !(c->prof.mask & (1 << fam))) return;
   *e0 = c->prof.get();
-  hipEventRecord(*e0, c->st);
+  hipEventRecord(*e0, s);
 }
-void prof_end(ne_ctx *c, int fam, hipEvent_t e0) {
+void prof_end(ne_ctx *c, int fam, hipEvent_t e0, hipStream_t s) {
   if (!c->prof.on || !(c->prof.mask & (1 << fam))) return;
   hipEvent_t e1 = c->prof.get();
-  hipEventRecord(e1, c->st);
+  hipEventRecord(e1, s);
   c->prof.pending.push_back({fam, e0, e1});
 }
 
+// Event pair around the work of one kernel family enqueued on s (default: the step stream).
 struct ProfScope {
   ne_ctx *c;
   int fam;
+  hipStream_t s;
   hipEvent_t e0 = nullptr;
-  ProfScope(ne_ctx *c_, int f) : c(c_), fam(f) { prof_begin(c, fam, &e0); }
-  ~ProfScope() { prof_end(c, fam, e0); }
+  ProfScope(ne_ctx *c_, int f, hipStream_t s_ = nullptr) : c(c_), fam(f), s(s_ ? s_ : c_->st) {
+    prof_begin(c, fam, &e0, s);
+  }
+  ~ProfScope() { prof_end(c, fam, e0, s); }
 };
+
+// Make st wait for an optimizer update still running on st2 (every entry point that reads
+// or writes parameters, moments or gradients, other than the next training step).
+int adam_join(ne_ctx *c) {
+  if (!c->adam_pending) return 0;
+  NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[c->L], 0));
+  c->adam_pending = false;
+  return 0;
+}
 
 int prof_collect(ne_ctx *c) {
   if (c->prof.pending.empty()) return 0;
+  NE_CHECK(adam_join(c));
   NE_HIP(hipStreamSynchronize(c->st));
   for (auto &r : c->prof.pending) {
     float ms = 0.f;
@@ -356,6 +370,9 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st2, hipStreamNonBlocking), "stream"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event"))) goto fail;
+  c->ev_adam.assign(c->L + 1, nullptr);
+  for (auto &e : c->ev_adam)
+    if ((rc = ne_hip_status(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
   pl.assign((char *)c->arena);
   c->tok_tgt = c->tok_in + T;
@@ -425,6 +442,8 @@ extern "C" void ne_destroy(ne_ctx *c) {
   for (auto &e : c->graphs) hipGraphExecDestroy(e.exec);
   if (c->ev_fork) hipEventDestroy(c->ev_fork);
   if (c->ev_join) hipEventDestroy(c->ev_join);
+  for (auto e : c->ev_adam)
+    if (e) hipEventDestroy(e);
   for (int i = 0; i < 2; i++)
     if (c->tok_ev[i]) hipEventDestroy(c->tok_ev[i]);
   decode_free(c);
@@ -447,6 +466,7 @@ extern "C" void ne_destroy(ne_ctx *c) {
 
 extern "C" int ne_sync(ne_ctx *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(adam_join(c));
   NE_HIP(hipStreamSynchronize(c->st));
   return 0;
 }
@@ -462,6 +482,7 @@ extern "C" int64_t ne_tensor_numel(const ne_ctx *c, int id) {
 
 extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, size_t n) {
   if (!c || !host) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_CHECK(adam_join(c));
   if (id < 0 || id >= (int)c->t_off.size()) return ne_fail(NE_ERR_ARG, "bad tensor id %d", id);
   if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
   float *base = kind_base(c, kind);
@@ -479,6 +500,7 @@ extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, siz
 
 extern "C" int ne_get_tensor(ne_ctx *c, int kind, int id, float *host, size_t n) {
   if (!c || !host) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_CHECK(adam_join(c));
   if (id < 0 || id >= (int)c->t_off.size()) return ne_fail(NE_ERR_ARG, "bad tensor id %d", id);
   if ((long)n != c->t_numel[id]) return ne_fail(NE_ERR_ARG, "tensor %d has %ld elements, got %zu", id, c->t_numel[id], n);
   float *base = kind_base(c, kind);
@@ -508,7 +530,7 @@ extern "C" int ne_set_state(ne_ctx *c, const ne_train_state *st) {
 
 // Enqueue one forward+backward on c->st with token ids already in c->tok_in/tok_tgt.
 // Free of host synchronisation and memsets, so it can be captured into a HIP graph.
-static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two) {
+static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two, bool adam_ov = false) {
   const int T = c->T, S = c->S, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, V = c->V;
   const float alpha = c->c.res_alpha, eps = c->c.norm_eps;
   const h16_t *Pb = c->Pb;
@@ -529,6 +551,14 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two)
   // gradients instead of accumulating (no zeroing pass, no read of G); only the gains,
   // which accumulate through atomics, are cleared.
   const int EPI_DW = fresh ? EPI_F32 : EPI_F32_ACC;
+  // The optimizer update of the previous step may still run on st2 (adam_ov): chunk 0 (the
+  // embedding and the gains, read and written below first), then chunk 1 + l before layer l.
+  // The last wait comes before the backward, the first writer of G.
+  auto wait_update = [&](int k) -> int {
+    if (adam_ov) NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[k], 0));
+    return 0;
+  };
+  NE_CHECK(wait_update(0));
   if (fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
 
   // ---------------- forward ----------------
@@ -543,6 +573,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two)
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
     float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
+    NE_CHECK(wait_update(1 + l));
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_fwd(dt, a.x_in, P + o.g_att, a.xn, a.r1, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
@@ -757,9 +788,13 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // launched eagerly: replaying it from a graph measured slower than in order on one stream
   // (the branches' hand-overs cost more in a graph than between eager launches).
   const bool two = c->overlap_wgrad && !profiled;
+  // an update still running on st2: the two-stream step waits for it chunk by chunk
+  const bool adam_ov = c->adam_pending && two;
+  if (!adam_ov) NE_CHECK(adam_join(c));
   c->gn_ready = false;
   if (c->use_graphs && !profiled && !two) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
-  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two));
+  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two, adam_ov));
+  c->adam_pending = false;  // the forward waited for the last chunk before the backward
   c->gn_ready = true;  // the step refreshed every sum-of-squares partial of G
   if (loss_out) {
     NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
@@ -778,6 +813,7 @@ extern "C" int ne_use_graphs(ne_ctx *c, int on) {
 extern "C" int ne_overlap_weight_grads(ne_ctx *c, int on) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
   if (c->overlap_wgrad == (on != 0)) return 0;
+  NE_CHECK(adam_join(c));
   NE_HIP(hipStreamSynchronize(c->st));
   // the captured steps bake the stream layout in
   for (auto &e : c->graphs) (void)hipGraphExecDestroy(e.exec);
@@ -788,6 +824,7 @@ extern "C" int ne_overlap_weight_grads(ne_ctx *c, int on) {
 
 extern "C" int ne_set_vocab_map(ne_ctx *c, const int32_t *ids, int cv) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(adam_join(c));
   if (cv < 0 || cv > c->V || (cv > 0 && !ids)) return ne_fail(NE_ERR_ARG, "vocab map: %d ids of %d", cv, c->V);
   if (!c->grads_fresh) return ne_fail(NE_ERR_STATE, "vocab map: change it between accumulation windows");
   std::vector<int32_t> f2c(cv ? c->V : 0, -1);
@@ -822,6 +859,7 @@ extern "C" int ne_set_vocab_map(ne_ctx *c, const int32_t *ids, int cv) {
 
 extern "C" int ne_zero_grads(ne_ctx *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(adam_join(c));
   NE_HIP(hipMemsetAsync(c->ovf, 0, OVF_COUNT * sizeof(int), c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   c->grads_fresh = true;
@@ -831,6 +869,7 @@ extern "C" int ne_zero_grads(ne_ctx *c) {
 extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float eps, float wd, float grad_scale,
                                  float clip, float *gnorm_out) {
   if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  NE_CHECK(adam_join(c));
   // overflow check of the accumulation window (dynamic gradient scaling)
   NE_HIP(hipMemcpyAsync(c->h_ovf, c->ovf, OVF_COUNT * sizeof(int), hipMemcpyDeviceToHost, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
@@ -869,7 +908,27 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   a.bc1 = 1.f - powf(b1, (float)t);
   a.bc2 = 1.f - powf(b2, (float)t);
   a.gscale = c->gscale; a.zero_grad = 0;
-  {
+  if (c->overlap_wgrad) {
+    // on st2 in chunks, so that the next step's forward can start on the embedding and layer
+    // 0 while the later layers are still being updated (ne_train_step waits per chunk)
+    NE_HIP(hipEventRecord(c->ev_fork, c->st));
+    NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
+    ProfScope ps(c, NE_PROF_ADAM, c->st2);
+    auto chunk = [&](long off, long n, long n_decay, hipEvent_t done) -> int {
+      AdamArgs ch = a;
+      ch.p = c->P + off; ch.g = c->G + off; ch.m = c->M + off; ch.v = c->Vm + off; ch.pb = c->Pb + off;
+      ch.n = n; ch.n_decay = n_decay;
+      NE_CHECK(launch_adam(c->dt, ch, c->st2));
+      NE_HIP(hipEventRecord(done, c->st2));
+      return 0;
+    };
+    NE_CHECK(chunk(c->off_E, c->n_params - c->off_E, c->n_decay - c->off_E, c->ev_adam[0]));
+    for (int l = 0; l < c->L; l++) {
+      const long n = layer_params(c);
+      NE_CHECK(chunk(c->lo[l].wqkv, n, n, c->ev_adam[1 + l]));
+    }
+    c->adam_pending = true;
+  } else {
     ProfScope ps(c, NE_PROF_ADAM);
     NE_CHECK(launch_adam(c->dt, a, c->st));
   }
@@ -984,6 +1043,7 @@ int io_body(ne_ctx *c, FILE *f, bool rd, bool qkn) {
 
 extern "C" int ne_load_ckpt_v4(ne_ctx *c, const char *path, ne_train_state *st) {
   if (!c || !path) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_CHECK(adam_join(c));
   NE_HIP(hipStreamSynchronize(c->st));
   FILE *f = fopen(path, "rb");
   if (!f) return ne_fail(NE_ERR_IO, "cannot open %s", path);
@@ -1017,6 +1077,7 @@ extern "C" int ne_load_ckpt_v4(ne_ctx *c, const char *path, ne_train_state *st) 
 
 extern "C" int ne_save_ckpt_v4(ne_ctx *c, const char *path, const ne_train_state *st) {
   if (!c || !path) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_CHECK(adam_join(c));
   NE_HIP(hipStreamSynchronize(c->st));
   const ne_train_state &s = st ? *st : c->state;
   CkptHdr h = {};
@@ -1038,5 +1099,6 @@ extern "C" int ne_save_ckpt_v4(ne_ctx *c, const char *path, const ne_train_state
 extern "C" int ne_decode(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float temperature, float top_p,
                          const double *uniforms, int32_t *out_tokens) {
   if (!c || !prompt || !out_tokens) return ne_fail(NE_ERR_ARG, "null argument");
+  NE_CHECK(adam_join(c));
   return decode_run(c, prompt, B, P, n_new, temperature, top_p, uniforms, out_tokens);
 }

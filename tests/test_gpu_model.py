@@ -279,9 +279,11 @@ def test_decode_sampling_mfma_path():
 @pytest.mark.parametrize("compact", [False, True])
 def test_step_identical_across_launch_modes(compact):
     """The step gives bit-identical losses and gradients over two accumulating micro-steps
-    whether its kernels are launched eagerly with the weight-gradient GEMMs on a second
-    stream (two_streams, the default), in order on one stream with per-kernel profiling
-    events between them (profiled), or in order replayed from a HIP graph (graph)."""
+    whether its kernels are launched eagerly with the weight-gradient GEMMs and the optimizer
+    update on a second stream (two_streams, the default: the update overlaps the next step's
+    forward), in order on one stream with per-kernel profiling events between them
+    (profiled), or in order replayed from a HIP graph (graph); the same holds for the
+    weights after two updates and the gradients of the steps that follow them."""
     cfg = om.tiny(**CASES["qwen3"], n_layers=2, dim=1024, hidden=4096, vocab=4096, seq=256)
     P = om.init_params(cfg, seed=0, std=0.02)
     toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2)]
@@ -298,13 +300,21 @@ def test_step_identical_across_launch_modes(compact):
             m.set_vocab_map(ids)
         m.set_params(P)
         losses = [m.train_step(t, 256.0) for t in toks]
-        out.append((losses, m.get_all(shapes(cfg), ne.NE_GRAD)))
+        g_acc = m.get_all(shapes(cfg), ne.NE_GRAD)
+        # an update, then a step whose forward overlaps it (two_streams), then another update
+        gn = [m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=1.0)]
+        losses.append(m.train_step(toks[0], 256.0))
+        gn.append(m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=1.0))
+        losses.append(m.train_step(toks[1], 256.0))
+        out.append((losses, gn, g_acc, m.get_all(shapes(cfg), ne.NE_GRAD), m.get_all(shapes(cfg))))
         m.close()
-    (l0, g0) = out[0]
-    for li, gi in out[1:]:
+    (l0, n0, *t0) = out[0]
+    for li, ni, *ti in out[1:]:
         assert li == l0
-        for n in g0:
-            np.testing.assert_array_equal(gi[n], g0[n], err_msg=n)
+        assert ni == n0
+        for a, b in zip(ti, t0):
+            for n in b:
+                np.testing.assert_array_equal(a[n], b[n], err_msg=n)
 
 
 def _compact_case(vocab=1024, seed=5):
