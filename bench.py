@@ -261,7 +261,10 @@ def main():
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
-    adam_ms = r["adam"][0] / max(r["adam"][1], 1)
+    # one AdamW pass per step: 29 launches (embedding + gains, then one per layer) on the second
+    # stream, each between its own event pair; the pass time is the sum of their durations
+    adam_launches = max(r["adam"][1], 1) / a.steps
+    adam_ms = r["adam"][0] / a.steps
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
     out = {
         "metric": "Qwen3-0.6B train tokens/s + step ms on 1 MI355X; MFMA util %; decode tok/s",
@@ -279,13 +282,16 @@ def main():
         "config": {"workload": a.workload, "global_batch": w["batch"], "seq_len": w["seq"],
                    "tokens_per_step": w["batch"] * w["seq"], "params": npar, "parallelism": "single GPU",
                    "precision": "fp32 master weights + AdamW state, fp16 activations/operands, fp32 accumulate"},
-        "roofline": {"bound": "hbm", "kernel": "adam_kernel (fused AdamW over all parameters)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "adam_kernel (fused AdamW; one pass over all parameters per step, in "
+                               f"{adam_launches:.0f} launches: embedding + gains, then one per layer)",
                      "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
                      "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
                      "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated "
                                        "(profiles/adam_hbm_counters_qwen3-0.6b.md)",
-                     "bytes_per_launch": adam_bytes, "avg_launch_ms": adam_ms},
+                     "bytes_per_pass": adam_bytes, "pass_ms": adam_ms, "launches_per_pass": adam_launches,
+                     "bytes_per_launch": adam_bytes / adam_launches, "avg_launch_ms": adam_ms / adam_launches},
         "dominant_family": dom,
         "kernel_ms_per_step": fam_ms,
         "mfma_util": summ["mfma_util"],

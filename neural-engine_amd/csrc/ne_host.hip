@@ -913,12 +913,14 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
     // 0 while the later layers are still being updated (ne_train_step waits per chunk)
     NE_HIP(hipEventRecord(c->ev_fork, c->st));
     NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
-    ProfScope ps(c, NE_PROF_ADAM, c->st2);
     auto chunk = [&](long off, long n, long n_decay, hipEvent_t done) -> int {
       AdamArgs ch = a;
       ch.p = c->P + off; ch.g = c->G + off; ch.m = c->M + off; ch.v = c->Vm + off; ch.pb = c->Pb + off;
       ch.n = n; ch.n_decay = n_decay;
-      NE_CHECK(launch_adam(c->dt, ch, c->st2));
+      {
+        ProfScope ps(c, NE_PROF_ADAM, c->st2);  // per launch: the family time is the sum of durations
+        NE_CHECK(launch_adam(c->dt, ch, c->st2));
+      }
       NE_HIP(hipEventRecord(done, c->st2));
       return 0;
     };
