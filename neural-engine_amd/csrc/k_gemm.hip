@@ -91,6 +91,34 @@ struct Stage {
 
 __device__ __forceinline__ float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Barrier that orders LDS only: waits for this wave's LDS operations, not for the global
+// loads still in flight (they stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Instruction order of one K step, for the scheduler: G groups, each [MFMA, fragment reads,
+// global load, MFMA, LDS store], the counts spread evenly (NMF MFMAs, NDR fragment reads, NGL
+// global loads, NDW LDS stores per step), so the memory instructions issue between the MFMAs
+// instead of in bursts that leave the matrix pipe idle.
+template <int NMF, int NDR, int NGL, int NDW, int G, int I = 0>
+__device__ __forceinline__ void sched_kstep() {
+  if constexpr (I < G) {
+    constexpr int m0 = I * NMF / G, m1 = (I + 1) * NMF / G, mh = (m0 + m1) / 2;
+    constexpr int r = (I + 1) * NDR / G - I * NDR / G;
+    constexpr int l = (I + 1) * NGL / G - I * NGL / G;
+    constexpr int w = (I + 1) * NDW / G - I * NDW / G;
+    if constexpr (mh > m0) __builtin_amdgcn_sched_group_barrier(0x008, mh - m0, 0);  // MFMA
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);          // LDS read
+    if constexpr (l > 0) __builtin_amdgcn_sched_group_barrier(0x020, l, 0);          // global load
+    if constexpr (m1 > mh) __builtin_amdgcn_sched_group_barrier(0x008, m1 - mh, 0);  // MFMA
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);          // LDS write
+    sched_kstep<NMF, NDR, NGL, NDW, G, I + 1>();
+  }
+}
+
 
 // Final store of one output element v (alpha already applied) for every non-CE epilogue.
 template <typename HT, int EPI>
@@ -132,8 +160,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
   static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
-  // 256x256 tiles: 144 KB of the 160 KB LDS of a gfx950 CU (one work-group per CU)
-  __shared__ __attribute__((aligned(16))) h16_t lds[2][(BM + BN) * PITCH];
+  // 256x256 tiles: 144 KB of the 160 KB LDS of a gfx950 CU (one work-group per CU).  Two
+  // named buffers (not one array), so the compiler sees that the stores into one and the
+  // fragment reads from the other do not alias and can interleave them.
+  __shared__ __attribute__((aligned(16))) h16_t lds0[(BM + BN) * PITCH];
+  __shared__ __attribute__((aligned(16))) h16_t lds1[(BM + BN) * PITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -146,8 +177,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int kt0 = (int)((long)nkt * blockIdx.z / g.split);
   const int kt1 = (int)((long)nkt * (blockIdx.z + 1) / g.split);
 
-  Stage<NTHREADS, BM, BK, AKC> sa;
-  Stage<NTHREADS, BN, BK, BKC> sb;
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; i++)
@@ -156,20 +185,19 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  sa.load(A, g.lda, m0, kt0 * BK, tid);
-  sb.load(B, g.ldb, n0, kt0 * BK, tid);
-  sa.template store<PITCH>(lds[0], tid);
-  sb.template store<PITCH>(lds[0] + BM * PITCH, tid);
-  __syncthreads();
-
-  for (int kt = kt0; kt < kt1; kt++) {
-    const int cur = (kt - kt0) & 1;
-    if (kt + 1 < kt1) {
-      sa.load(A, g.lda, m0, (kt + 1) * BK, tid);
-      sb.load(B, g.ldb, n0, (kt + 1) * BK, tid);
-    }
-    const h16_t *As = lds[cur];
-    const h16_t *Bs = lds[cur] + BM * PITCH;
+  // Software pipeline: while a K step's MFMAs run from one LDS buffer, the next stage (held in
+  // registers since the previous step) is written into the other, and the stage after that is
+  // loaded from global memory into the second register set: global loads are issued two steps
+  // ahead of their use, and the LDS-only barrier lets them cross the step boundary.
+  typedef Stage<NTHREADS, BM, BK, AKC> SA;
+  typedef Stage<NTHREADS, BN, BK, BKC> SB;
+  SA sa0, sa1;
+  SB sb0, sb1;
+  constexpr int NMF = FM * FN * (BK / 16), NDR = (FM + FN) * (BK / 16);
+  constexpr int NGL = (AKC ? SA::PER : SA::PER * 4) + (BKC ? SB::PER : SB::PER * 4);
+  constexpr int NDW = (AKC ? SA::PER : SA::PER * 8) + (BKC ? SB::PER : SB::PER * 8);
+  auto compute = [&](const h16_t *L) {
+    const h16_t *As = L, *Bs = L + BM * PITCH;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
       typename HT::v8 a[FM], b[FN];
@@ -184,12 +212,39 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = HT::mfma32(a[i], b[j], acc[i][j]);
     }
-    if (kt + 1 < kt1) {
-      sa.template store<PITCH>(lds[cur ^ 1], tid);
-      sb.template store<PITCH>(lds[cur ^ 1] + BM * PITCH, tid);
-    }
-    __syncthreads();
+  };
+  auto load = [&](SA &a, SB &b, int kt) {
+    a.load(A, g.lda, m0, kt * BK, tid);
+    b.load(B, g.ldb, n0, kt * BK, tid);
+  };
+  auto store = [&](h16_t *L, SA &a, SB &b) {
+    a.template store<PITCH>(L, tid);
+    b.template store<PITCH>(L + BM * PITCH, tid);
+  };
+  auto sched = [&]() { sched_kstep<NMF, NDR, NGL, NDW, NGL>(); };
+
+  const int n = kt1 - kt0;  // K steps of this split (>= 1)
+  // Stage j of the split is loaded from K step kt0 + min(j, n - 1): the loads past the end
+  // repeat the last step (valid memory, never computed), so the loop body has no branch and
+  // one register allocation covers every split length.
+  auto kstep = [&](int j) { return kt0 + min(j, n - 1); };
+  load(sa0, sb0, kt0);
+  store(lds0, sa0, sb0);
+  load(sa0, sb0, kstep(1));
+  lds_barrier();
+  for (int i = 0; i + 1 < n; i += 2) {  // steps i (lds0) and i + 1 (lds1)
+    load(sa1, sb1, kstep(i + 2));
+    compute(lds0);
+    store(lds1, sa0, sb0);
+    sched();
+    lds_barrier();
+    load(sa0, sb0, kstep(i + 3));
+    compute(lds1);
+    store(lds0, sa1, sb1);
+    sched();
+    lds_barrier();
   }
+  if (n & 1) compute(lds0);  // the last step of an odd count is in lds0
 
   // ---- epilogue: lane owns column (lane & 31) and rows 8*(e/4) + 4*(lane/32) + e%4 ----
   const float alpha = g.alpha;
