@@ -3,12 +3,12 @@
 // C[M,N] = epi(alpha * sum_k A[m,k] B[k,n]).  Operands are 16-bit (fp16 or bf16) with fp32
 // accumulation on v_mfma_f32_32x32x16_{f16,bf16}.  Each operand may be K-contiguous
 // (activation rows, weight rows [N,K]) or M/N-contiguous (the dY^T and X of a
-// weight-gradient GEMM); both are staged into LDS K-contiguous so every MFMA operand is
-// one 16-byte LDS read.  M/N-contiguous tiles are transposed in registers in 4x8 blocks on
-// the way into LDS, with a thread mapping that keeps those 8-byte LDS writes free of bank
-// conflicts.  Double-buffered LDS, one barrier per K step.  Block tiles: 256x256 or 256x128
-// with 8 waves (64x128 / 64x64 each) for large shapes, 128x128 or 64x64 with 4 waves
-// (64x64 / 32x32) otherwise.
+// weight-gradient GEMM, the weights of a dX GEMM); either is staged into LDS as it lies in
+// memory (16-byte loads and stores), and an MFMA operand is one 16-byte LDS read
+// (K-contiguous) or two gfx950 transpose reads (M/N-contiguous).  Double-buffered LDS, one
+// LDS-only barrier per K step, global loads two steps ahead, memory instructions interleaved
+// with the MFMAs.  Block tiles: 256x256 or 256x128 with 8 waves (64x128 / 64x64 each) for
+// large shapes, 128x128 or 64x64 with 4 waves (64x64 / 32x32) otherwise.
 //
 // Small-M shapes (a 256-token step) leave too few output tiles to fill 256 CUs, so the
 // launcher splits K over grid.z: each split writes its fp32 partial tile to a workspace
@@ -25,66 +25,75 @@
 
 namespace {
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// gfx950 LDS transpose read: lane i of each 16-lane group receives tile[row0 + j][col0 + i],
+// j = 0..3 (row pitch P); row0 / col0 may differ between the 4 groups of the wave.
+template <int P>
+__device__ __forceinline__ u16x4 tr4(const h16_t *tile, int row0, int col0) {
+  const int m = threadIdx.x & 15;
+  const h16_t *p = tile + (row0 + (m >> 2)) * P + col0 + 4 * (m & 3);
+  return __builtin_bit_cast(u16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p));
+}
+
+// One operand's K-step tile: R rows (M or N) by BK columns (K), staged into LDS as it lies
+// in memory, 16 bytes per global load and per LDS store.
+//  KC (K-contiguous, element (r, k) at p[r*ld + k]): LDS [R][BK + 8]; an MFMA operand (8
+//    consecutive k of one row) is one 16-byte LDS read.
+//  MN-contiguous (element at p[k*ld + r]): LDS [BK][R + 32]; the operand is two transpose
+//    reads (ds_read_b64_tr_b16) of 4 k rows each.  The 64-byte row pad puts the 4 rows a
+//    16-lane group reads on distinct banks.
 template <int NT, int R, int BK, bool KC>
 struct Stage {
-  // KC: element (r, k) at p[r*ld + k]; otherwise at p[k*ld + r].
-  static constexpr int NCH = KC ? R * BK / 8 : (R / 8) * (BK / 4);
+  static constexpr int PITCH = KC ? BK + 8 : R + 32;
+  static constexpr int ELEMS = KC ? R * PITCH : BK * PITCH;
+  static constexpr int NCH = R * BK / 8;  // 16-byte chunks
   static constexpr int PER = (NCH + NT - 1) / NT;
-  static constexpr int NV = KC ? PER : PER * 4;
-  static_assert(KC || (R / 8) % 4 == 0, "MN-contiguous tiles need R % 32 == 0");
-  u16x8 v[NV];
+  static constexpr int FRAG_READS = KC ? 1 : 2;  // LDS reads per MFMA operand
+  u16x8 v[PER];
 
-  // MN-contiguous chunk c -> (k block of 4, 8-wide r chunk): 4 consecutive threads take
-  // consecutive r chunks (64-byte row segments in HBM), the next bits walk the k blocks, so
-  // the 8-byte LDS writes of a wave land on distinct banks.
-  __device__ __forceinline__ static void mn_idx(int c, int &kb, int &rc) {
-    const int lo = c % 4, kk = (c / 4) % (BK / 4), hi = c / (4 * (BK / 4));
-    kb = kk;
-    rc = hi * 4 + lo;
+  // chunk c -> (row of the LDS tile, 8-element column block); consecutive threads take
+  // consecutive 16-byte pieces of one memory row
+  __device__ __forceinline__ static void idx(int c, int &row, int &col8) {
+    constexpr int CPR = KC ? BK / 8 : R / 8;  // chunks per memory row
+    row = c / CPR;
+    col8 = c % CPR;
   }
 
   __device__ __forceinline__ void load(const h16_t *p, long ld, int r0, int k0, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      int c = tid + i * NT;
+      const int c = tid + i * NT;
       if (NCH % NT == 0 || c < NCH) {
-        if (KC) {
-          int r = c / (BK / 8), k8 = c % (BK / 8);
-          v[i] = *(const u16x8 *)(p + (long)(r0 + r) * ld + k0 + k8 * 8);
-        } else {
-          int kb, rc;
-          mn_idx(c, kb, rc);
-#pragma unroll
-          for (int j = 0; j < 4; j++)
-            v[i * 4 + j] = *(const u16x8 *)(p + (long)(k0 + kb * 4 + j) * ld + r0 + rc * 8);
-        }
+        int row, col8;
+        idx(c, row, col8);
+        v[i] = KC ? *(const u16x8 *)(p + (long)(r0 + row) * ld + k0 + col8 * 8)
+                  : *(const u16x8 *)(p + (long)(k0 + row) * ld + r0 + col8 * 8);
       }
     }
   }
 
-  template <int PITCH>
   __device__ __forceinline__ void store(h16_t *lds, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      int c = tid + i * NT;
+      const int c = tid + i * NT;
       if (NCH % NT == 0 || c < NCH) {
-        if (KC) {
-          int r = c / (BK / 8), k8 = c % (BK / 8);
-          *(u16x8 *)(lds + r * PITCH + k8 * 8) = v[i];
-        } else {
-          int kb, rc;
-          mn_idx(c, kb, rc);
-#pragma unroll
-          for (int e = 0; e < 8; e++) {
-            u16x4 t;
-            t[0] = v[i * 4 + 0][e];
-            t[1] = v[i * 4 + 1][e];
-            t[2] = v[i * 4 + 2][e];
-            t[3] = v[i * 4 + 3][e];
-            *(u16x4 *)(lds + (rc * 8 + e) * PITCH + kb * 4) = t;
-          }
-        }
+        int row, col8;
+        idx(c, row, col8);
+        *(u16x8 *)(lds + row * PITCH + col8 * 8) = v[i];
       }
+    }
+  }
+
+  // MFMA 32x32x16 operand of rows rb + (lane & 31), k = 16 kk + 8 (lane >> 5) + 0..7
+  __device__ __forceinline__ static u16x8 frag(const h16_t *lds, int rb, int kk, int lane) {
+    if constexpr (KC) {
+      return *(const u16x8 *)(lds + (rb + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8);
+    } else {
+      const int g = lane >> 4;
+      const int col = rb + 16 * (g & 1), k = kk * 16 + 8 * (g >> 1);
+      const u16x4 lo = tr4<PITCH>(lds, k, col), hi = tr4<PITCH>(lds, k + 4, col);
+      return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
 };
@@ -156,15 +165,16 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int NTHREADS = WM * WN * 64;
-  constexpr int PITCH = BK + 8;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
   static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
   // 256x256 tiles: 144 KB of the 160 KB LDS of a gfx950 CU (one work-group per CU).  Two
   // named buffers (not one array), so the compiler sees that the stores into one and the
   // fragment reads from the other do not alias and can interleave them.
-  __shared__ __attribute__((aligned(16))) h16_t lds0[(BM + BN) * PITCH];
-  __shared__ __attribute__((aligned(16))) h16_t lds1[(BM + BN) * PITCH];
+  typedef Stage<NTHREADS, BM, BK, AKC> SA;
+  typedef Stage<NTHREADS, BN, BK, BKC> SB;
+  __shared__ __attribute__((aligned(16))) h16_t lds0[SA::ELEMS + SB::ELEMS];
+  __shared__ __attribute__((aligned(16))) h16_t lds1[SA::ELEMS + SB::ELEMS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -189,24 +199,19 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // registers since the previous step) is written into the other, and the stage after that is
   // loaded from global memory into the second register set: global loads are issued two steps
   // ahead of their use, and the LDS-only barrier lets them cross the step boundary.
-  typedef Stage<NTHREADS, BM, BK, AKC> SA;
-  typedef Stage<NTHREADS, BN, BK, BKC> SB;
   SA sa0, sa1;
   SB sb0, sb1;
-  constexpr int NMF = FM * FN * (BK / 16), NDR = (FM + FN) * (BK / 16);
-  constexpr int NGL = (AKC ? SA::PER : SA::PER * 4) + (BKC ? SB::PER : SB::PER * 4);
-  constexpr int NDW = (AKC ? SA::PER : SA::PER * 8) + (BKC ? SB::PER : SB::PER * 8);
+  constexpr int NMF = FM * FN * (BK / 16), NDR = (FM * SA::FRAG_READS + FN * SB::FRAG_READS) * (BK / 16);
+  constexpr int NGL = SA::PER + SB::PER, NDW = SA::PER + SB::PER;
   auto compute = [&](const h16_t *L) {
-    const h16_t *As = L, *Bs = L + BM * PITCH;
+    const h16_t *As = L, *Bs = L + SA::ELEMS;
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
       typename HT::v8 a[FM], b[FN];
 #pragma unroll
-      for (int i = 0; i < FM; i++)
-        a[i] = HT::op(*(const u16x8 *)(As + (wm * TM + i * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+      for (int i = 0; i < FM; i++) a[i] = HT::op(SA::frag(As, wm * TM + i * 32, kk, lane));
 #pragma unroll
-      for (int j = 0; j < FN; j++)
-        b[j] = HT::op(*(const u16x8 *)(Bs + (wn * TN + j * 32 + (lane & 31)) * PITCH + kk * 16 + (lane >> 5) * 8));
+      for (int j = 0; j < FN; j++) b[j] = HT::op(SB::frag(Bs, wn * TN + j * 32, kk, lane));
 #pragma unroll
       for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -218,8 +223,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     b.load(B, g.ldb, n0, kt * BK, tid);
   };
   auto store = [&](h16_t *L, SA &a, SB &b) {
-    a.template store<PITCH>(L, tid);
-    b.template store<PITCH>(L + BM * PITCH, tid);
+    a.store(L, tid);
+    b.store(L + SA::ELEMS, tid);
   };
   auto sched = [&]() { sched_kstep<NMF, NDR, NGL, NDW, NGL>(); };
 
