@@ -279,22 +279,22 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
 }
 
 // dK / dV of NW*16*RG keys (RG groups of 16 per wave) of one kv head.  SPLIT: the block
-// handles one query head (blockIdx.y) and writes fp32 per-query-head partials to a.part
+// handles one query head (block row by) and writes fp32 per-query-head partials to a.part
 // (reduced by gqa_reduce_kernel); otherwise it loops over the query heads of its kv head
-// (blockIdx.y) and writes dK (fp32) and dV (16-bit) directly.  Query tiles of 64 from the
+// (block row by) and writes dK (fp32) and dV (16-bit) directly.  Query tiles of 64 from the
 // block's diagonal on.
+// Block (bx, by, bz) of the dK / dV grid; lds: [buffer][Q tile, dO tile].
 template <typename HT, int HD, int NW, int RG, bool SPLIT>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__device__ __forceinline__ void dkdv_block(const AttnArgs &a, int bx, int by, int bz, h16_t (*lds)[2 * BLK * (HD + 16)],
+                                           float (*lse_s)[BLK], float (*dl_s)[BLK]) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
   constexpr int ROWS = NW * 16 * RG;  // keys per block
-  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][Q tile, dO tile]
-  __shared__ float lse_s[2][BLK], dl_s[2][BLK];
   const int nqb = a.S / BLK;
-  const int k0 = blockIdx.x * ROWS;  // smallest keys have the most query tiles: launched first
+  const int k0 = bx * ROWS;  // smallest keys have the most query tiles: launched first
   const int qb_first = k0 / BLK;
   const int ratio = a.NH / a.NKV;
-  const int kvh = SPLIT ? blockIdx.y / ratio : blockIdx.y, b = blockIdx.z;
-  const int h_begin = SPLIT ? blockIdx.y : kvh * ratio, h_end = SPLIT ? blockIdx.y + 1 : (kvh + 1) * ratio;
+  const int kvh = SPLIT ? by / ratio : by, b = bz;
+  const int h_begin = SPLIT ? by : kvh * ratio, h_end = SPLIT ? by + 1 : (kvh + 1) * ratio;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const long tb = (long)b * a.S;
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkdv_kernel(AttnArgs a) {
   for (int r = 0; r < RG; r++) {
     const long tk = tb + ki[r];
     if (SPLIT) {
-      const int h = blockIdx.y;
+      const int h = by;
       float *pk = a.part, *pv = a.part + (long)a.B * a.S * a.NH * HD;
 #pragma unroll
       for (int d = 0; d < ND; d++) {
@@ -464,14 +464,15 @@ __global__ void gqa_reduce_kernel(AttnArgs a) {
 }
 
 // NW waves per block, RG groups of 16 queries per wave; key tiles of 64 up to the diagonal.
+// Block (bx, by, bz) of a dQ grid nbx blocks wide; lds: [buffer][K tile, V tile].
 template <typename HT, int HD, int NW, int RG>
-__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(AttnArgs a) {
+__device__ __forceinline__ void dq_block(const AttnArgs &a, int bx, int by, int bz, int nbx,
+                                         h16_t (*lds)[2 * BLK * (HD + 16)]) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
   constexpr int ROWS = NW * 16 * RG;  // queries per block
-  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * ROWS;  // longest rows first
+  const int q0 = (nbx - 1 - bx) * ROWS;  // longest rows first
   const int kb_last = (q0 + ROWS - 1) / BLK;
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = by, b = bz;
   const int kvh = h / (a.NH / a.NKV);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -613,37 +614,41 @@ int fwd_t(const AttnArgs &a, hipStream_t s) {
   return fwd_shape<HT, 64>(a, s);
 }
 
+// dK / dV and dQ in one launch: blocks x < nkv are dK / dV key blocks (grid.y rows >= nky
+// idle: without the per-query-head split there is one block row per KV head), the rest dQ
+// query blocks.  The two kinds depend only on delta (computed before), so they run side by
+// side: at short sequences each alone leaves half the CUs idle.
+template <typename HT, int HD, int NW, int RG, bool SPLIT>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_kernel(AttnArgs a, int nkv, int nky) {
+  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * BLK * (HD + 16)];
+  __shared__ float lse_s[2][BLK], dl_s[2][BLK];
+  if ((int)blockIdx.x < nkv) {
+    if ((int)blockIdx.y < nky)
+      dkdv_block<HT, HD, NW, RG, SPLIT>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds, lse_s, dl_s);
+  } else {
+    dq_block<HT, HD, NW, RG>(a, blockIdx.x - nkv, blockIdx.y, blockIdx.z, gridDim.x - nkv, lds);
+  }
+}
+
 template <typename HT, int HD, int NW, int RG>
-int dkdv_hd(const AttnArgs &a, hipStream_t s) {
-  const int nblk = a.S / (16 * NW * RG);
+int bwd_hd(const AttnArgs &a, hipStream_t s) {
+  const int nblk = a.S / (16 * NW * RG);  // key blocks of dK / dV = query blocks of dQ
+  const dim3 grid(2 * nblk, a.NH, a.B);
   if (a.part && a.NH != a.NKV) {
-    dim3 gkv(nblk, a.NH, a.B);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, RG, true>), gkv, dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_kernel<HT, HD, NW, RG, true>), grid, dim3(NW * 64), 0, s, a, nblk, a.NH);
     NE_HIP(hipGetLastError());
     const long n4 = (long)a.B * a.S * a.NKV * HD / 4;
     hipLaunchKernelGGL(gqa_reduce_kernel<HT>, dim3((int)std::min<long>((n4 + 255) / 256, 4096)), dim3(256), 0, s, a);
   } else {
-    dim3 gkv(nblk, a.NKV, a.B);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<HT, HD, NW, RG, false>), gkv, dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_kernel<HT, HD, NW, RG, false>), grid, dim3(NW * 64), 0, s, a, nblk, a.NKV);
   }
-  return ne_hip_status(hipGetLastError(), "attn_bwd dkdv");
-}
-
-template <typename HT, int HD, int NW, int RG>
-int dq_hd(const AttnArgs &a, hipStream_t s) {
-  dim3 gq(a.S / (16 * NW * RG), a.NH, a.B);
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<HT, HD, NW, RG>), gq, dim3(NW * 64), 0, s, a);
-  return ne_hip_status(hipGetLastError(), "attn_bwd dq");
+  return ne_hip_status(hipGetLastError(), "attn_bwd");
 }
 
 template <typename HT, int HD>
 int bwd_shape(const AttnArgs &a, hipStream_t s) {
-  if (pick_shape(a) != SHAPE_2x1) {
-    NE_CHECK((dkdv_hd<HT, HD, 4, 1>(a, s)));
-    return dq_hd<HT, HD, 4, 1>(a, s);
-  }
-  NE_CHECK((dkdv_hd<HT, HD, 2, 1>(a, s)));
-  return dq_hd<HT, HD, 2, 1>(a, s);
+  if (pick_shape(a) != SHAPE_2x1) return bwd_hd<HT, HD, 4, 1>(a, s);
+  return bwd_hd<HT, HD, 2, 1>(a, s);
 }
 
 template <typename HT>
