@@ -64,6 +64,14 @@ struct H16F {
              : [&] { using HT = H16B; return __VA_ARGS__; }())
 
 // Raise a device overflow flag (non-finite 16-bit result) once per thread.
+// Barrier that orders LDS only: waits for this wave's LDS operations, not for the global
+// loads still in flight (they stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void flag_overflow(int *ovf, bool bad) {
   if (ovf && bad) *ovf = 1;
 }

@@ -8,7 +8,8 @@
 // recomputes P per tile.  GQA: kv head = q head / (NH/NKV).
 //
 // Tiles of 64 keys (or queries) are staged row-major in LDS (16-byte copies, double
-// buffered through registers, one barrier per tile).  A wave owns 16 or 32 rows (one or two
+// buffered through registers, one barrier per tile; the forward loads its K/V tiles two
+// steps ahead and waits only on LDS at the barrier).  A wave owns 16 or 32 rows (one or two
 // groups of 16 sharing every LDS operand read).  Operands that are needed transposed
 // (V^T for P.V, Q^T and dO^T for dK/dV, K^T for dQ) are read from the same row-major tiles
 // with gfx950's LDS transpose read (ds_read_b64_tr_b16): the 16 lanes of a group each give
@@ -104,10 +105,13 @@ struct TileCopy {
 // NW waves per block, RG groups of 16 queries per wave (the K/V fragments read from LDS
 // serve every group: RG = 2 halves LDS traffic per MFMA); key tiles of 64.
 template <typename HT, int HD, int NW, int RG>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd_kernel(AttnArgs a) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
   constexpr int ROWS = NW * 16 * RG;  // queries per block
-  __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * TILE];  // [buffer][K tile, V tile]
+  // [K tile, V tile] per buffer; two named buffers so the compiler sees that the stores into
+  // one and the reads from the other do not alias
+  __shared__ __attribute__((aligned(16))) h16_t lds0[2 * TILE];
+  __shared__ __attribute__((aligned(16))) h16_t lds1[2 * TILE];
   const int q0 = (gridDim.x - 1 - blockIdx.x) * ROWS;  // longest rows first
   const int kb_last = (q0 + ROWS - 1) / BLK;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -132,20 +136,24 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   }
   const float sl2 = a.scale * LOG2E;
 
-  TileCopy<HD, NT, 2> cp;
-  cp.load(0, a.k, a.ldk, tb, kvh * HD);
-  cp.load(1, a.v, a.ldv, tb, kvh * HD);
-  cp.template store<RP>(0, lds[0]);
-  cp.template store<RP>(1, lds[0] + TILE);
-  __syncthreads();
-  for (int kb = 0; kb <= kb_last; kb++) {
-    const int cur = kb & 1;
-    if (kb < kb_last) {
-      cp.load(0, a.k, a.ldk, tb + (kb + 1) * BLK, kvh * HD);
-      cp.load(1, a.v, a.ldv, tb + (kb + 1) * BLK, kvh * HD);
-    }
+  // K/V tiles are loaded two steps ahead into alternating register sets; each step writes the
+  // next tile (loaded during the previous step) into the other LDS buffer right after its
+  // QK^T MFMAs, and the LDS-only barrier lets the loads in flight cross the step boundary.
+  // Loads past the last tile repeat it (valid memory, never used), so the loop has no tail.
+  typedef TileCopy<HD, NT, 2> TC;
+  TC cp0, cp1;
+  auto tload = [&](TC &cp, int kb) {
+    const int kc = min(kb, kb_last);
+    cp.load(0, a.k, a.ldk, tb + kc * BLK, kvh * HD);
+    cp.load(1, a.v, a.ldv, tb + kc * BLK, kvh * HD);
+  };
+  auto tstore = [&](TC &cp, h16_t *L) {
+    cp.template store<RP>(0, L);
+    cp.template store<RP>(1, L + TILE);
+  };
+  auto step = [&](int kb, const h16_t *L, TC &nxt, h16_t *Ln) {
     if (kb * BLK <= qw + 16 * RG - 1) {  // tiles wholly above this wave's queries add nothing
-      const h16_t *Ks = lds[cur], *Vs = lds[cur] + TILE;
+      const h16_t *Ks = L, *Vs = L + TILE;
       f32x4 s[RG][4];
 #pragma unroll
       for (int nb = 0; nb < 4; nb++)
@@ -160,6 +168,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int r = 0; r < RG; r++) s[r][nb] = HT::mfma16(kfrag, qf[r][kk], s[r][nb]);
         }
+      tstore(nxt, Ln);  // the next tile, while the softmax and P.V run
       // s[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r]); keys above a query are
       // masked on the tiles that cross this wave's diagonal only
       const bool diag = kb * BLK + BLK - 1 > qw;
@@ -211,13 +220,24 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int r = 0; r < RG; r++) acc[r][d] = HT::mfma16(vfrag, pb[r][c], acc[r][d]);
         }
+    } else {
+      tstore(nxt, Ln);
     }
-    if (kb < kb_last) {
-      cp.template store<RP>(0, lds[cur ^ 1]);
-      cp.template store<RP>(1, lds[cur ^ 1] + TILE);
-    }
-    __syncthreads();
+  };
+  tload(cp0, 0);
+  tstore(cp0, lds0);
+  tload(cp0, 1);
+  lds_barrier();
+  const int nkb = kb_last + 1;
+  for (int kb = 0; kb + 1 < nkb; kb += 2) {
+    tload(cp1, kb + 2);
+    step(kb, lds0, cp0, lds1);
+    lds_barrier();
+    tload(cp0, kb + 3);
+    step(kb + 1, lds1, cp1, lds0);
+    lds_barrier();
   }
+  if (nkb & 1) step(nkb - 1, lds0, cp1, lds1);  // stores an unused tile into the idle buffer
 #pragma unroll
   for (int r = 0; r < RG; r++) {
     const long tq = tb + qi[r];

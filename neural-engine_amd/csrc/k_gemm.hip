@@ -100,14 +100,6 @@ struct Stage {
 
 __device__ __forceinline__ float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// Barrier that orders LDS only: waits for this wave's LDS operations, not for the global
-// loads still in flight (they stay in flight across it).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Instruction order of one K step, for the scheduler: G groups, each [MFMA, fragment reads,
 // global load, MFMA, LDS store], the counts spread evenly (NMF MFMAs, NDR fragment reads, NGL
 // global loads, NDW LDS stores per step), so the memory instructions issue between the MFMAs
