@@ -400,68 +400,90 @@ __global__ void swiglu_fwd_kernel(h16_t *__restrict__ h13, h16_t *__restrict__ g
   flag_overflow(ovf_h13, bad13);
 }
 
-// Per (token, head, pair): optional per-head RMSNorm with gain g[HD], then interleaved
-// RoPE on pair (2i, 2i+1) at position t % S with fp32 tables cos/sin [S, HD/2].
-// Head slots 0..NH-1 are q heads (qkv columns h*HD), NH..NH+NKV-1 are k heads
+// Per (token, head): optional per-head RMSNorm with gain g[HD], then interleaved RoPE on the
+// pairs (2i, 2i+1) at position t % S with fp32 tables cos/sin [S, HD/2].  One block per token;
+// each head slot is HD/8 consecutive lanes owning 8 elements (4 pairs) each, so every access
+// is 16 bytes.  Head slots 0..NH-1 are q heads (qkv columns h*HD), NH..NH+NKV-1 are k heads
 // (columns NH*HD + (h-NH)*HD).  Replaces the RoPE of gen_sdpa_fwd_dynamic
 // (TD/mil_dynamic.h:133-169).
 // With split-K partials of the QKV GEMM (sp.n > 0, qkv row pitch ld = q|k|v width) the
-// threads also cover the v heads: each pair is summed in split order, scaled, rounded to 16
-// bits and written to qkv (the GEMM's own output, read by attention and the backward), and
-// the q/k pairs continue from the rounded values.
-template <typename HT, bool QKN>
-__global__ void qk_prep_fwd_kernel(h16_t *__restrict__ qkv, long ld, const float *__restrict__ cosb,
-                                   const float *__restrict__ sinb, const float *__restrict__ gq,
-                                   const float *__restrict__ gk, h16_t *__restrict__ qr,
-                                   h16_t *__restrict__ kr, float *__restrict__ rq, float *__restrict__ rk,
-                                   int T, int S, int NH, int NKV, int HD, float eps, SplitIn sp, int *ovf_qkv) {
-  const int half = HD / 2;
+// threads also cover the v heads: each element is summed in split order, scaled, rounded to
+// 16 bits and written to qkv (the GEMM's own output, read by attention and the backward), and
+// the q/k elements continue from the rounded values.
+template <typename HT, bool QKN, int HD>
+__global__ __launch_bounds__(256) void qk_prep_fwd_kernel(h16_t *__restrict__ qkv, long ld,
+                                                          const float *__restrict__ cosb,
+                                                          const float *__restrict__ sinb,
+                                                          const float *__restrict__ gq,
+                                                          const float *__restrict__ gk, h16_t *__restrict__ qr,
+                                                          h16_t *__restrict__ kr, float *__restrict__ rq,
+                                                          float *__restrict__ rk, int S, int NH, int NKV,
+                                                          float eps, SplitIn sp, int *ovf_qkv) {
+  constexpr int TPH = HD / 8, HALF = HD / 2;  // lanes per head slot (a divisor of 64)
+  const long t = blockIdx.x;
   const int slots = sp.n > 0 ? NH + 2 * NKV : NH + NKV;
-  const long gid = blockIdx.x * (long)blockDim.x + threadIdx.x;
-  const long total = (long)T * slots * half;
-  if (gid >= total) return;  // total is a multiple of 64: whole waves exit together
-  const int i = gid % half;
-  const long th = gid / half;
-  const int h = th % slots;
-  const long t = th / slots;
-  const bool isq = h < NH, isv = h >= NH + NKV;
-  const int hh = isq ? h : isv ? h - NH - NKV : h - NH;
-  const long col = (isq ? 0 : isv ? (long)(NH + NKV) * HD : (long)NH * HD) + (long)hh * HD + 2 * i;
-  uint32_t pr;
-  if (sp.n > 0) {
-    const float *p = sp.part + t * ld + col;
-    float s0 = p[0], s1 = p[1];
-    for (int z = 1; z < sp.n; z++) {
-      s0 += p[z * sp.slice];
-      s1 += p[z * sp.slice + 1];
+  const int pos = (int)(t % S);
+  bool bad = false;
+  // whole head slots are active or idle together, so the shuffles below stay within a slot
+  for (int w = threadIdx.x; w < slots * TPH; w += 256) {
+    const int h = w / TPH, j = w % TPH;
+    const bool isq = h < NH, isv = h >= NH + NKV;
+    const int hh = isq ? h : isv ? h - NH - NKV : h - NH;
+    const long col = (isq ? 0 : isv ? (long)(NH + NKV) * HD : (long)NH * HD) + (long)hh * HD + 8 * j;
+    u16x8 pr;
+    if (sp.n > 0) {
+      const float *p = sp.part + t * ld + col;
+      float4 s0 = *(const float4 *)p, s1 = *(const float4 *)(p + 4);
+      for (int z = 1; z < sp.n; z++) {
+        const float4 a0 = *(const float4 *)(p + z * sp.slice), a1 = *(const float4 *)(p + z * sp.slice + 4);
+        s0.x += a0.x; s0.y += a0.y; s0.z += a0.z; s0.w += a0.w;
+        s1.x += a1.x; s1.y += a1.y; s1.z += a1.z; s1.w += a1.w;
+      }
+      const float v[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        pr[e] = HT::h(v[e] * sp.alpha);
+        bad |= HT::bad(pr[e]);
+      }
+      *(u16x8 *)(qkv + t * ld + col) = pr;
+      if (isv) continue;  // uniform per head slot
+    } else {
+      pr = *(const u16x8 *)(qkv + t * ld + col);
     }
-    const h16_t o0 = HT::h(s0 * sp.alpha), o1 = HT::h(s1 * sp.alpha);
-    flag_overflow(ovf_qkv, HT::bad(o0) | HT::bad(o1));
-    pr = (uint32_t)o0 | ((uint32_t)o1 << 16);
-    *(uint32_t *)(qkv + t * ld + col) = pr;
-    if (isv) return;  // uniform per wave (a head slot spans whole waves)
-  } else {
-    pr = *(const uint32_t *)(qkv + t * ld + col);
-  }
-  float x0 = HT::f((h16_t)(pr & 0xFFFF)), x1 = HT::f((h16_t)(pr >> 16));
-  if (QKN) {
-    float ss = x0 * x0 + x1 * x1;
-    for (int o = 1; o < half; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    const float r = 1.0f / sqrtf(ss / (float)HD + eps);
-    const float *gg = isq ? gq : gk;
-    x0 = x0 * r * gg[2 * i];
-    x1 = x1 * r * gg[2 * i + 1];
-    if (i == 0) {
-      if (isq) rq[t * NH + hh] = r;
-      else rk[t * NKV + hh] = r;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = HT::f(pr[e]);
+    if (QKN) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+#pragma unroll
+      for (int o = 1; o < TPH; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      const float r = 1.0f / sqrtf(ss / (float)HD + eps);
+      const float *gg = (isq ? gq : gk) + 8 * j;
+      const float4 g0 = *(const float4 *)gg, g1 = *(const float4 *)(gg + 4);
+      const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) x[e] = x[e] * r * gv[e];
+      if (j == 0) {
+        if (isq) rq[t * NH + hh] = r;
+        else rk[t * NKV + hh] = r;
+      }
     }
+    const float4 c4 = *(const float4 *)(cosb + (long)pos * HALF + 4 * j);
+    const float4 s4 = *(const float4 *)(sinb + (long)pos * HALF + 4 * j);
+    const float cv[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+    u16x8 o;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float x0 = x[2 * q], x1 = x[2 * q + 1];
+      o[2 * q] = HT::h(x0 * cv[q] - x1 * sv[q]);
+      o[2 * q + 1] = HT::h(x0 * sv[q] + x1 * cv[q]);
+    }
+    if (isq) *(u16x8 *)(qr + t * (long)NH * HD + (long)hh * HD + 8 * j) = o;
+    else *(u16x8 *)(kr + t * (long)NKV * HD + (long)hh * HD + 8 * j) = o;
   }
-  const int pos = t % S;
-  const float c = cosb[pos * half + i], s = sinb[pos * half + i];
-  const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
-  const uint32_t out = (uint32_t)HT::h(y0) | ((uint32_t)HT::h(y1) << 16);
-  if (isq) *(uint32_t *)(qr + t * (long)NH * HD + (long)hh * HD + 2 * i) = out;
-  else *(uint32_t *)(kr + t * (long)NKV * HD + (long)hh * HD + 2 * i) = out;
+  flag_overflow(ovf_qkv, bad);
 }
 
 // Backward of qk_prep: inverse rotation (TD/cpu_ops.h:510-537), then the exact
@@ -633,12 +655,20 @@ int launch_qk_prep_fwd(int dt, const h16_t *qkv, long ld, const float *cosb, con
                        const SplitIn &sp, int *ovf_qkv) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
   if (sp.n > 0 && ld != (long)(NH + 2 * NKV) * HD) return ne_fail(NE_ERR_ARG, "qk_prep: split input needs a dense qkv");
-  const long total = (long)T * (sp.n > 0 ? NH + 2 * NKV : NH + NKV) * (HD / 2);
-  const int blocks = (int)((total + 255) / 256);
+  if (ld % 8 || ((uintptr_t)qkv & 15)) return ne_fail(NE_ERR_ARG, "qk_prep: qkv rows must be 16-byte aligned (ld %% 8 == 0)");
   h16_t *q = (h16_t *)qkv;
   return DISPATCH_H16(dt, [&] {
-    if (gq) hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, true>), dim3(blocks), dim3(256), 0, s, q, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps, sp, ovf_qkv);
-    else hipLaunchKernelGGL((qk_prep_fwd_kernel<HT, false>), dim3(blocks), dim3(256), 0, s, q, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, T, S, NH, NKV, HD, eps, sp, ovf_qkv);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(T), dim3(256), 0, s, q, ld, cosb, sinb, gq, gk, qr, kr, rq, rk, S, NH, NKV, eps,
+                         sp, ovf_qkv);
+    };
+    if (HD == 128) {
+      if (gq) go(qk_prep_fwd_kernel<HT, true, 128>);
+      else go(qk_prep_fwd_kernel<HT, false, 128>);
+    } else {
+      if (gq) go(qk_prep_fwd_kernel<HT, true, 64>);
+      else go(qk_prep_fwd_kernel<HT, false, 64>);
+    }
     return ne_hip_status(hipGetLastError(), "qk_prep_fwd");
   }());
 }
