@@ -171,7 +171,22 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  // Grouped tile order: the blocks of a group of GM M-tiles take those M tiles in turn for
+  // each N tile.  Work-groups go to the 8 XCDs round-robin, so with GM = 8 an XCD keeps one A
+  // tile in its L2 across the whole group while each B tile is fetched from HBM about once per
+  // group (the other XCDs hit the memory-side cache) instead of once per M tile.
+  constexpr int GM = 8;
+  int mt, nt;
+  {
+    const int num_m = gridDim.y, num_n = gridDim.x;
+    const int pid = blockIdx.y * num_n + blockIdx.x;
+    const int grp = pid / (GM * num_n), first_m = grp * GM;
+    const int gsz = min(num_m - first_m, GM);
+    const int r = pid - grp * GM * num_n;
+    mt = first_m + r % gsz;
+    nt = r / gsz;
+  }
+  const int n0 = nt * BN, m0 = mt * BM;
   const h16_t *A = (const h16_t *)g.A;
   const h16_t *B = (const h16_t *)g.B;
   // K steps of this split: [kt0, kt1)
@@ -291,7 +306,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int w = 0; w < WN; w++)
         if (red_m[w][r] > -INFINITY) s += red_s[w][r] * __expf(red_m[w][r] - mx);
-      float *p = g.part + ((long)(m0 + r) * g.n_tiles + blockIdx.x) * 2;
+      float *p = g.part + ((long)(m0 + r) * g.n_tiles + nt) * 2;
       p[0] = mx;
       p[1] = s;
     }
