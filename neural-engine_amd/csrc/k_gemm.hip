@@ -329,6 +329,60 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     return;
   }
 
+  if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // Through LDS, so that the gate reads and the dh1 | dh3 writes are 16-byte row pieces
+    // (in the MFMA layout each lane would touch one 2-byte element per row): pass i stages row
+    // block i of every wave row (WM * 32 rows x BN fp32, the first half of the rows in lds0, the
+    // second in lds1), then each thread takes 8 consecutive columns of a row.
+    constexpr int SR = WM * 32, HR = SR / 2, SP = BN + 8;  // rows per pass, per buffer; pitch
+    constexpr int CPR8 = BN / 8, NCHK = SR * CPR8 / NTHREADS;
+    static_assert(HR * SP * 4 <= (SA::ELEMS + SB::ELEMS) * 2, "SwiGLU epilogue: staging must fit an LDS buffer");
+    static_assert(SR * CPR8 % NTHREADS == 0, "SwiGLU epilogue: whole chunks per thread");
+    float *st0 = (float *)lds0, *st1 = (float *)lds1;
+    const h16_t *hb = (const h16_t *)g.R;
+    h16_t *db = (h16_t *)g.C;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      lds_barrier();  // the buffers' previous readers (last K step, previous pass) are done
+      float *stw = wm < WM / 2 ? st0 : st1;
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int col = wn * TN + j * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int rr = (wm % (WM / 2)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          stw[rr * SP + col] = acc[i][j][e] * alpha;
+        }
+      }
+      lds_barrier();
+#pragma unroll
+      for (int c = 0; c < NCHK; c++) {
+        const int chunk = tid + c * NTHREADS, row = chunk / CPR8, c8 = chunk % CPR8;
+        const float *str = (row < HR ? st0 : st1) + (row % HR) * SP + c8 * 8;
+        const float4 v0 = *(const float4 *)str, v1 = *(const float4 *)(str + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const long grow = m0 + (row / 32) * TM + i * 32 + row % 32;
+        const int gcol = n0 + c8 * 8;
+        const u16x8 h1v = *(const u16x8 *)(hb + grow * g.ldr + gcol);
+        const u16x8 h3v = *(const u16x8 *)(hb + grow * g.ldr + g.N + gcol);
+        u16x8 o1, o3;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float h1 = HT::f(h1v[e]), h3 = HT::f(h3v[e]);
+          const float sg = fast_sigmoid(h1);
+          o1[e] = HT::h(v[e] * h3 * sg * (1.f + h1 * (1.f - sg)));
+          o3[e] = HT::h(v[e] * h1 * sg);
+          bad |= HT::bad(o1[e]) | HT::bad(o3[e]);
+        }
+        *(u16x8 *)(db + grow * g.ldc + gcol) = o1;
+        *(u16x8 *)(db + grow * g.ldc + g.N + gcol) = o3;
+      }
+    }
+    flag_overflow(g.ovf, bad);
+    return;
+  }
+
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
@@ -455,6 +509,8 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
   if ((g.lda % 8) || (g.ldb % 8) || (((uintptr_t)g.A | (uintptr_t)g.B) & 15))
     return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
+  if (epi == EPI_SWIGLU_BWD && ((g.ldr % 8) || (g.ldc % 8) || (((uintptr_t)g.R | (uintptr_t)g.C) & 15)))
+    return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU backward epilogue needs 16-byte aligned h13 / dh13 rows");
   const int tile = gemm_tile(g.M, g.N, g.K);
   // split K while there are too few work-groups for the 256 CUs (one per CU for the 8-wave
   // tiles, two for the others), keeping >= 4 K steps per split
