@@ -273,8 +273,10 @@ def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
 # --------------------------------------------------------------- cross-entropy (LM head)
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768)])
+@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768), (256, 128, 65664)])
 def test_fused_ce_fwd_bwd(fmt, T, D, V):
+    """(256, 128, 65664): a vocabulary 256.5 tiles of 256 wide.  The guard row after dlogits
+    must stay zero (no store past the last column)."""
     dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(V)
     x = rnd(rng.standard_normal((T, D)).astype(np.float32))
@@ -292,13 +294,15 @@ def test_fused_ce_fwd_bwd(fmt, T, D, V):
     loss_r = np.mean(-np.log(p_t + 1e-10))
     np.testing.assert_allclose(host(lse), lse_r, rtol=1e-5)
     assert abs(host(loss)[0] - loss_r) < 1e-4 * abs(loss_r)
-    dl = zeros((T, V), tdt)
+    dlg = zeros((T + 1, V), tdt)  # + a guard row
     scale = 1024.0
-    call(L.ne_k_ce_bwd, dt, ptr(xd), ptr(Ed), ptr(td), ptr(lse), T, D, V, scale, ptr(dl), None)
+    call(L.ne_k_ce_bwd, dt, ptr(xd), ptr(Ed), ptr(td), ptr(lse), T, D, V, scale, ptr(dlg), None)
     ref = np.exp(logits - lse_r[:, None])
     ref[np.arange(T), tgt] -= 1
     ref *= scale
-    assert rel_l2(host(dl), ref) < u
+    got = host(dlg)
+    assert rel_l2(got[:T], ref) < u
+    assert np.abs(got[T]).max() == 0
 
 
 # ------------------------------------------------------------------------ optimizer

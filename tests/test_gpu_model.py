@@ -56,6 +56,23 @@ def test_train_step_matches_oracle(case):
     m.close()
 
 
+def test_step_with_ragged_vocab_tiles():
+    """A vocabulary that is not a multiple of 256 (65,664 = 256.5 tiles) with 256 tokens: the
+    classifier / CE GEMMs and the embedding-gradient GEMM take tiles that divide it.  A store
+    past the last embedding row would land in the gain gradients that follow it in G, which
+    the comparison with the oracle covers."""
+    cfg = om.tiny(**CASES["qwen3"], vocab=65664)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = om.tokens_for_step(cfg, 4, cfg.seq, seed=1)
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    Go = om.backward(cfg, P, cache)
+    m, loss, G = run_step(cfg, P, tok)
+    m.close()
+    assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
+    for n in P:
+        assert rel_l2(G[n], Go[n]) <= GRAD_RL2, (n, rel_l2(G[n], Go[n]))
+
+
 def test_grads_accumulate_and_zero():
     cfg = om.tiny()
     P = om.init_params(cfg, seed=0, std=0.02)
