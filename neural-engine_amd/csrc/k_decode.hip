@@ -65,8 +65,10 @@ enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2 };
 // (PRO_RMSNORM, generate.py:81-84) or silu(h1) * h3 with in = [h1 | h3] rows of 2K
 // (PRO_SWIGLU).  resid may alias out (each element is read, then written, by one lane).
 // AMX: also write the block's (max, first row) of each sequence to amv/ami [b][blockIdx.x].
-// The wave's weights (KC chunks of 512 per row, K <= 512*KC) are loaded before the input
-// prologue, so HBM latency overlaps the prologue.
+// Every global load (input rows, gains, residual, then the wave's weights: KC chunks of 512
+// per row, K <= 512*KC) is issued before the first wait, so the block pays one HBM latency,
+// not one per load: with loads behind branches or in a load-store loop each waited for the
+// one before, which doubled the time of a batch-1 GEMV.
 // GATE (W1|W3 rows [2*gate_n, K]): the wave's rows are j..j+RPW/2-1 of W1 and the same j of
 // W3 (rows gate_n + j), and it writes gate[b, j] = silu(h1) * h3 (generate.py:190) instead of h1, h3.
 template <typename HT, int NB, int RPW, int KC, int PRO, bool AMX, bool GATE>
@@ -82,36 +84,45 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
   constexpr int HALF = GATE ? RPW / 2 : RPW;
   const long row0 = ((long)blockIdx.x * 4 + w) * HALF;
   auto wrow = [&](int r) -> long { return GATE && r >= HALF ? gate_n + row0 + (r - HALF) : row0 + r; };
+  // Every global load of the block is issued before the first wait: the input rows (16 bytes
+  // per lane, XI per row), the gains, the residual and then the weights.  Addresses past the
+  // end of a row are clamped into it (no branches around loads, so none waits for another);
+  // the values they bring are not used.
+  constexpr int XI = (KC + 1) / 2;  // 1024 * XI >= 512 * KC >= K
+  float4 xa[NB][XI], xb[PRO == PRO_SWIGLU ? NB : 1][XI], gv[XI];
+#pragma unroll
+  for (int i = 0; i < XI; i++) {
+    const int k = (i * 256 + tid) * 4, kc = k < K ? k : K - 4;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const float *src = in + (long)(b < B ? b : B - 1) * ldi;
+      xa[b][i] = *(const float4 *)(src + kc);
+      if (PRO == PRO_SWIGLU) xb[b][i] = *(const float4 *)(src + K + kc);
+    }
+    if (PRO == PRO_RMSNORM) gv[i] = *(const float4 *)(g + kc);
+  }
+  // residual of this lane's output (written by the same lane below; resid may alias out)
+  const int rl = lane < RPW * NB ? lane / NB : 0, bl = lane < RPW * NB ? lane % NB : 0;
+  const float res_v = !GATE && resid && lane < RPW * NB && bl < B ? resid[(long)bl * ldo + row0 + rl] : 0.f;
   u16x8 wv[RPW][KC];
 #pragma unroll
   for (int c = 0; c < KC; c++) {
-    const int k = c * 512 + lane * 8;
+    const int k = c * 512 + lane * 8, kc = k < K ? k : K - 8;
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
-      if (k < K) wv[r][c] = __builtin_nontemporal_load((const u16x8 *)(W + wrow(r) * K + k));
+    for (int r = 0; r < RPW; r++) wv[r][c] = __builtin_nontemporal_load((const u16x8 *)(W + wrow(r) * K + kc));
   }
-  for (int b = 0; b < NB; b++) {
-    const float *src = in + (long)b * ldi;
-    for (int k = tid; k < K; k += 256) {
-      float v = 0.f;
-      if (b < B) {
-        if (PRO == PRO_SWIGLU) {
-          const float h1 = src[k], h3 = src[K + k];
-          v = h1 * (1.f / (1.f + expf(-h1))) * h3;
-        } else {
-          v = src[k];
-        }
-      }
-      xs[b * K + k] = v;
-    }
-  }
+  float rms[NB];
   if (PRO == PRO_RMSNORM) {
-    __syncthreads();
     float ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       ss[b] = 0.f;
-      for (int k = tid; k < K; k += 256) ss[b] += xs[b * K + k] * xs[b * K + k];
+#pragma unroll
+      for (int i = 0; i < XI; i++)
+        if ((i * 256 + tid) * 4 < K) {
+          const float4 v = xa[b][i];
+          ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
       ss[b] = wave_sum(ss[b]);
     }
     if (lane == 0)
@@ -119,9 +130,30 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
       for (int b = 0; b < NB; b++) red[w][b] = ss[b];
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-      const float rms = sqrtf((red[0][b] + red[1][b] + red[2][b] + red[3][b]) / (float)K + eps);
-      for (int k = tid; k < K; k += 256) xs[b * K + k] = xs[b * K + k] / rms * g[k];
+    for (int b = 0; b < NB; b++) rms[b] = sqrtf((red[0][b] + red[1][b] + red[2][b] + red[3][b]) / (float)K + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < XI; i++) {
+    const int k = (i * 256 + tid) * 4;
+    if (k < K) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        float4 v = xa[b][i];
+        if (PRO == PRO_SWIGLU) {
+          const float4 h3 = xb[b][i];
+          v.x = v.x * (1.f / (1.f + expf(-v.x))) * h3.x;
+          v.y = v.y * (1.f / (1.f + expf(-v.y))) * h3.y;
+          v.z = v.z * (1.f / (1.f + expf(-v.z))) * h3.z;
+          v.w = v.w * (1.f / (1.f + expf(-v.w))) * h3.w;
+        } else if (PRO == PRO_RMSNORM) {
+          v.x = v.x / rms[b] * gv[i].x;
+          v.y = v.y / rms[b] * gv[i].y;
+          v.z = v.z / rms[b] * gv[i].z;
+          v.w = v.w / rms[b] * gv[i].w;
+        }
+        if (b >= B) v = make_float4(0.f, 0.f, 0.f, 0.f);
+        *(float4 *)(xs + b * K + k) = v;
+      }
     }
   }
   __syncthreads();
@@ -177,7 +209,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
     if (b < B) {
       const long n = row0 + r;
       float o = alpha * v;
-      if (resid) o += resid[(long)b * ldo + n];
+      if (resid) o += res_v;
       out[(long)b * ldo + n] = o;
       if (AMX) bmv[b][w * RPW + r] = o;
     }
@@ -688,6 +720,8 @@ int gemv_small(ne_ctx *c, int B, int pro, bool amx, const h16_t *W, int N, int K
   Dec *d = (Dec *)c->dec;
   if (N % 4 || K % 8 || K > 3072)
     return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%4, K%%8, K <= 3072)", N, K);
+  if ((((uintptr_t)in | (uintptr_t)(g ? g : in)) & 15) || ldi % 4)
+    return ne_fail(NE_ERR_ARG, "decode gemv: input rows and gains must be 16-byte aligned");
   const float eps = c->c.norm_eps;
   return DISPATCH_H16(c->dt, [&] {
     if (pro == PRO_RMSNORM && gate)
