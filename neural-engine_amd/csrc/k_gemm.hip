@@ -171,18 +171,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  // Grouped tile order: the blocks of a group of GM M-tiles take those M tiles in turn for
-  // each N tile.  Work-groups go to the 8 XCDs round-robin, so with GM = 8 an XCD keeps one A
-  // tile in its L2 across the whole group while each B tile is fetched from HBM about once per
-  // group (the other XCDs hit the memory-side cache) instead of once per M tile.
-  constexpr int GM = 8;
+  // Tile order.  Work-groups go to the NX = 8 XCDs round-robin (work-group w to XCD w % 8),
+  // and each XCD has its own L2.  The tiles are laid out in grouped order (groups of GM M
+  // tiles, the M tiles of a group in turn for each N tile, so consecutive tiles share a B
+  // tile and a group's A tiles recur), and XCD x takes one contiguous stretch of that
+  // sequence: the M tiles that share a B tile run on the same XCD and find it in its L2, as
+  // do the recurring A tiles.  (Handing consecutive tiles to different XCDs made every XCD
+  // fetch each B tile: 4x the weight bytes for a 256-token forward GEMM.)
+  constexpr int GM = 8, NX = 8;
   int mt, nt;
   {
     const int num_m = gridDim.y, num_n = gridDim.x;
+    const int T = num_m * num_n;
     const int pid = blockIdx.y * num_n + blockIdx.x;
-    const int grp = pid / (GM * num_n), first_m = grp * GM;
+    const int x = pid % NX, q = T / NX, rem = T % NX;
+    const int u = x * q + min(x, rem) + pid / NX;  // a bijection of [0, T)
+    const int grp = u / (GM * num_n), first_m = grp * GM;
     const int gsz = min(num_m - first_m, GM);
-    const int r = pid - grp * GM * num_n;
+    const int r = u - grp * GM * num_n;
     mt = first_m + r % gsz;
     nt = r / gsz;
   }
@@ -426,11 +432,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
 
 namespace {
 
-template <typename HT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int EPI>
+template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 int launch_t(GemmArgs g, hipStream_t s) {
   g.n_tiles = g.N / BN;
   dim3 grid(g.N / BN, g.M / BM, g.split);
-  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, 64, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
   NE_HIP(hipGetLastError());
   if (g.split > 1 && !g.defer_reduce) {
     if constexpr (EPI != EPI_CE_FWD) {
@@ -452,10 +458,10 @@ constexpr int tile_bn(int t) { return t == TILE_256 ? 256 : t == TILE_64 ? 64 : 
 
 template <typename HT, bool AKC, bool BKC, int EPI>
 int launch_e(GemmArgs g, int tile, hipStream_t s) {
-  if (tile == TILE_256) return launch_t<HT, 256, 256, 4, 2, AKC, BKC, EPI>(g, s);
-  if (tile == TILE_256x128) return launch_t<HT, 256, 128, 4, 2, AKC, BKC, EPI>(g, s);
-  if (tile == TILE_128) return launch_t<HT, 128, 128, 2, 2, AKC, BKC, EPI>(g, s);
-  return launch_t<HT, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
+  if (tile == TILE_256) return launch_t<HT, 256, 256, 64, 4, 2, AKC, BKC, EPI>(g, s);
+  if (tile == TILE_256x128) return launch_t<HT, 256, 128, 64, 4, 2, AKC, BKC, EPI>(g, s);
+  if (tile == TILE_128) return launch_t<HT, 128, 128, 64, 2, 2, AKC, BKC, EPI>(g, s);
+  return launch_t<HT, 64, 64, 64, 2, 2, AKC, BKC, EPI>(g, s);
 }
 
 template <typename HT, bool AKC, bool BKC>
