@@ -39,9 +39,10 @@ struct Dec {
   int Bp;                 // MFMA path: batch padded to 16 or 32
   int ctx;                // max positions
   float *kc, *vc;         // [L][Bmax][NKV][ctx][HD]
-  float *x, *xn, *qkv, *att, *h13, *logits;  // [Bp, *]
+  float *x, *xn, *qkv, *att, *logits;  // [Bp, *]
   float *ws;              // MFMA split-K partials
   long ws_elems;
+  float *gate;            // [Bp, H] SwiGLU gate (batch 5..32)
   float *amv;             // argmax partials [Bmax][nblk]
   int32_t *ami;
   int lm_nblk;
@@ -233,22 +234,26 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Partial (or, with one split, final) products of 16 weight rows (blockIdx.x) over the K
-// range of split blockIdx.y, for NT tiles of 16 sequences.  x rows [Bp, K] fp32, or with
-// SWIGLU rows [Bp, 2K] of [h1 | h3] and x = silu(h1) * h3 formed on the fly.  Each wave
-// loads up to 8 weight chunks ahead of their use.
-template <typename HT, int NT, bool SWIGLU>
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(const h16_t *__restrict__ W, long ldw,
-                                                        const float *__restrict__ x, int K, int ksplit,
+// Products of 16 weight rows (blockIdx.x) with x rows [Bp, K] (fp32, row stride ldx) over the
+// K range of split blockIdx.y, for NT tiles of 16 sequences; the 4 waves split that range.
+// With a workspace ws, split z's products go to slice z of ws [ksplit][Bp, N] (one split's
+// slice is laid out as the output rows); without (one split), out = alpha * products + resid.
+// GATE (one split; W = [W1; W3], gate_n rows each): the block's rows are j0..j0+7 of W1 and
+// the same of W3 (j0 = 8 * blockIdx.x), and it writes out[b, j] = silu(h1) * h3
+// (generate.py:190).  WV waves per block split the K range; each loads up to 8 weight chunks
+// ahead of their use.
+template <typename HT, int NT, bool GATE, int WV = 4>
+__global__ __launch_bounds__(WV * 64) void gemv_mfma_kernel(const h16_t *__restrict__ W, long ldw,
+                                                        const float *__restrict__ x, long ldx, int K, int ksplit,
                                                         float *out, long ldo, const float *resid, float alpha,
-                                                        float *ws, int N, int B) {
-  __shared__ f32x4 red[4][NT][64];
+                                                        float *ws, int N, int B, long gate_n) {
+  __shared__ f32x4 red[WV][NT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const long row = (long)blockIdx.x * 16 + r;
-  const int kc = K / ksplit, ks = kc / 4;
+  const long row = GATE ? (r < 8 ? (long)blockIdx.x * 8 + r : gate_n + (long)blockIdx.x * 8 + r - 8)
+                        : (long)blockIdx.x * 16 + r;
+  const int kc = K / ksplit, ks = kc / WV;
   const int kbeg = blockIdx.y * kc + w * ks, kend = kbeg + ks;
-  const long ldx = SWIGLU ? 2L * K : K;
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -265,19 +270,8 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const h16_t *__restrict_
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           const float *xr = x + (long)(t * 16 + r) * ldx + k0 + g * 8;
-          float xv[8];
-          if (SWIGLU) {
-            const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 4);
-            const float4 b0 = *(const float4 *)(xr + K), b1 = *(const float4 *)(xr + K + 4);
-            const float h1[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            const float h3[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) xv[j] = h1[j] * (1.f / (1.f + expf(-h1[j]))) * h3[j];
-          } else {
-            const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 4);
-            xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
-            xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
-          }
+          const float4 a0 = *(const float4 *)xr, a1 = *(const float4 *)(xr + 4);
+          const float xv[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
           for (int j = 0; j < 8; j++) acc[t] = mfma_f32(HT::f(wv[i][j]), xv[j], acc[t]);
         }
@@ -290,11 +284,25 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const h16_t *__restrict_
   if (w == 0) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      const f32x4 s = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
+      f32x4 s = red[0][t][lane];
+#pragma unroll
+      for (int v = 1; v < WV; v++) s += red[v][t][lane];
       // s[i] = sum for sequence t*16 + r, weight row blockIdx.x*16 + 4g + i
       const int b = t * 16 + r;
       const long n = (long)blockIdx.x * 16 + g * 4;
-      if (ksplit > 1) {
+      if (GATE) {
+        // lanes g = 0, 1 hold h1 of gate outputs j0 + 4g + i; lanes g + 2 hold their h3
+        f32x4 h3;
+#pragma unroll
+        for (int i = 0; i < 4; i++) h3[i] = __shfl(s[i], (lane + 32) & 63, 64);
+        if (g < 2 && b < B) {
+          float4 o;
+          float *op = &o.x;
+#pragma unroll
+          for (int i = 0; i < 4; i++) op[i] = s[i] * (1.f / (1.f + expf(-s[i]))) * h3[i];
+          *(float4 *)(out + b * ldo + (long)blockIdx.x * 8 + g * 4) = o;
+        }
+      } else if (ws) {
         *(f32x4 *)(ws + ((long)blockIdx.y * NT * 16 + b) * N + n) = s;
       } else if (b < B) {
         float4 o = make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
@@ -308,17 +316,66 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const h16_t *__restrict_
   }
 }
 
-// Ordered sum of the split-K partials (split 0 first), alpha, residual.
-__global__ void gemv_reduce_kernel(const float *__restrict__ ws, int ksplit, int Bp, int N, float *out, long ldo,
-                                   const float *resid, float alpha, int B) {
-  const long i = blockIdx.x * 256L + threadIdx.x;
-  if (i >= (long)B * N) return;
-  const int b = (int)(i / N), n = (int)(i % N);
-  float s = 0.f;
-  for (int z = 0; z < ksplit; z++) s += ws[((long)z * Bp + b) * N + n];
-  float o = alpha * s;
-  if (resid) o += resid[(long)b * ldo + n];
-  out[(long)b * ldo + n] = o;
+// One block per sequence b: out[b, :] = alpha * (ordered sum of the split-K partials, split 0
+// first) + resid[b, :], and (gn != null) xn[b, :] = out[b, :] / rms * gn, the RMSNorm of the
+// new row (generate.py:81-84, rms = sqrt(mean(out^2) + eps)) that the next GEMV reads.
+// KS > 0 (the split count, rows of at most 1024): every partial and residual load of a thread
+// is issued before the first add.
+template <int KS>
+__global__ __launch_bounds__(256) void gemv_reduce_rows_kernel(const float *__restrict__ ws, int ksplit, int Bp, int N,
+                                                               float *out, long ldo, const float *resid, float alpha,
+                                                               const float *gn, float *xn, float eps) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float ss = 0.f;
+  float rv[4];  // KS path: the thread's residual inputs, then its outputs
+  if constexpr (KS > 0) {
+    float v[4 * (KS > 0 ? KS : 1)];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int n = min(tid + 256 * e, N - 1);  // rows shorter than 1024: clamped, unused
+#pragma unroll
+      for (int z = 0; z < KS; z++) v[e * KS + z] = ws[((long)z * Bp + b) * N + n];
+      rv[e] = resid ? resid[(long)b * ldo + n] : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int n = tid + 256 * e;
+      if (n < N) {
+        float s = 0.f;
+#pragma unroll
+        for (int z = 0; z < KS; z++) s += v[e * KS + z];
+        float o = alpha * s;
+        if (resid) o += rv[e];
+        out[(long)b * ldo + n] = o;
+        ss += o * o;
+        rv[e] = o;
+      }
+    }
+  } else {
+    for (int n = tid; n < N; n += 256) {
+      float s = 0.f;
+      for (int z = 0; z < ksplit; z++) s += ws[((long)z * Bp + b) * N + n];
+      float o = alpha * s;
+      if (resid) o += resid[(long)b * ldo + n];
+      out[(long)b * ldo + n] = o;
+      ss += o * o;
+    }
+  }
+  if (!gn) return;
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)N + eps);
+  if constexpr (KS > 0) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int n = tid + 256 * e;
+      if (n < N) xn[(long)b * N + n] = rv[e] / rms * gn[n];
+    }
+  } else {  // read back what this thread wrote
+    for (int n = tid; n < N; n += 256) xn[(long)b * N + n] = out[(long)b * ldo + n] / rms * gn[n];
+  }
 }
 
 // ------------------------------------------------------------- elementwise / attention ----
@@ -327,29 +384,26 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ ws, int ksplit, int
 // embedding row.  One block per sequence.
 template <typename HT>
 __global__ void dec_token_kernel(const int32_t *__restrict__ prompt, int ctx, const DecState *__restrict__ st,
-                                 int32_t *tok, const h16_t *__restrict__ E, float *x, int D, int B) {
+                                 int32_t *tok, const h16_t *__restrict__ E, float *x, int D, int B,
+                                 const float *__restrict__ gn, float *xn, float eps) {
+  __shared__ float red[4];
   const int b = blockIdx.x;
   const int pos = st->pos;
   const int t = pos < st->P ? prompt[(long)b * ctx + pos] : tok[b];
-  for (int i = threadIdx.x; i < D; i += blockDim.x) x[(long)b * D + i] = b < B ? HT::f(E[(long)t * D + i]) : 0.f;
-  __syncthreads();
-  if (threadIdx.x == 0) tok[b] = t;
-}
-
-// generate.py:81-84: (x / rms) * w, rms = sqrt(mean(x^2) + eps); one block per sequence
-__global__ void dec_rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ g, float *y, int D,
-                                   float eps) {
-  __shared__ float red[4];
-  const int b = blockIdx.x;
-  const float *xr = x + (long)b * D;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < D; i += 256) ss += xr[i] * xr[i];
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const float v = b < B ? HT::f(E[(long)t * D + i]) : 0.f;
+    x[(long)b * D + i] = v;
+    ss += v * v;
+  }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  const float tot = red[0] + red[1] + red[2] + red[3];
-  const float rms = sqrtf(tot / (float)D + eps);
-  for (int i = threadIdx.x; i < D; i += 256) y[(long)b * D + i] = xr[i] / rms * g[i];
+  if (threadIdx.x == 0) tok[b] = t;
+  if (gn) {  // the RMSNorm of the row (generate.py:81-84), read by the batch-5..32 QKV GEMV
+    const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += blockDim.x) xn[(long)b * D + i] = x[(long)b * D + i] / rms * gn[i];
+  }
 }
 
 template <int HD, int RATIO>
@@ -357,7 +411,8 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
                                                        const float *__restrict__ gq, const float *__restrict__ gk,
                                                        const float *__restrict__ cosb, const float *__restrict__ sinb,
                                                        float *kc, float *vc, float *att, int NH, int NKV, int ctx,
-                                                       const DecState *__restrict__ st, float eps, double scale) {
+                                                       const DecState *__restrict__ st, float eps, double scale,
+                                                       const float *__restrict__ qws, int qnz, int Bp) {
   extern __shared__ float sc[];  // [RATIO][ctx]
   constexpr int C4 = HD / 4, NG = 256 / C4, HALF = HD / 2;
   __shared__ float4 qs[RATIO][C4];
@@ -369,21 +424,29 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   float *K = kc + ((long)b * NKV + kvh) * ctx * HD;
   float *V = vc + ((long)b * NKV + kvh) * ctx * HD;
   const float *row = qkv + (long)b * QKV;
+  // element col of this sequence's q|k|v row: the row itself, or (qnz > 1) the ordered sum of
+  // the QKV GEMV's split-K partial slices [qnz][Bp, QKV]
+  auto qval = [&](int col) -> float {
+    if (qnz <= 1) return row[col];
+    float s = 0.f;
+    for (int z = 0; z < qnz; z++) s += qws[((long)z * Bp + b) * QKV + col];
+    return s;
+  };
   // slots 0..RATIO-1: q heads kvh*RATIO + slot; RATIO: k head kvh; RATIO+1: v head kvh
   for (int i = tid; i < (RATIO + 2) * HALF; i += 256) {
     const int slot = i / HALF, p = i % HALF;
     float *q2 = (float *)qs, *k2 = (float *)kn, *v2 = (float *)vn;
     if (slot == RATIO + 1) {
-      const float *src = row + (NH + NKV) * HD + kvh * HD;
-      const float y0 = src[2 * p], y1 = src[2 * p + 1];
+      const int c0 = (NH + NKV) * HD + kvh * HD;
+      const float y0 = qval(c0 + 2 * p), y1 = qval(c0 + 2 * p + 1);
       v2[2 * p] = y0; v2[2 * p + 1] = y1;
       V[(long)pos * HD + 2 * p] = y0;
       V[(long)pos * HD + 2 * p + 1] = y1;
       continue;
     }
     const bool isq = slot < RATIO;
-    const float *src = isq ? row + (kvh * RATIO + slot) * HD : row + NH * HD + kvh * HD;
-    float x0 = src[2 * p], x1 = src[2 * p + 1];
+    const int c0 = isq ? (kvh * RATIO + slot) * HD : NH * HD + kvh * HD;
+    float x0 = qval(c0 + 2 * p), x1 = qval(c0 + 2 * p + 1);
     const float *gg = isq ? gq : gk;
     if (gg) {  // uniform per block: every lane of the slot's (half-)wave takes part
       float ss = x0 * x0 + x1 * x1;
@@ -736,42 +799,67 @@ int gemv_small(ne_ctx *c, int B, int pro, bool amx, const h16_t *W, int N, int K
   }());
 }
 
-template <typename HT, int NT, bool SW>
-void launch_mfma(dim3 grid, hipStream_t st, const h16_t *W, int K, const float *x, int ks, float *out, long ldo,
-                 const float *resid, float alpha, float *ws, int N, int B) {
-  hipLaunchKernelGGL((gemv_mfma_kernel<HT, NT, SW>), grid, dim3(256), 0, st, W, (long)K, x, K, ks, out, ldo, resid,
-                     alpha, ws, N, B);
-}
-
-// Batch 5..32: out = alpha * W . x + resid with x [Bp, K] fp32 (swiglu: x = gate of h13 rows
-// [Bp, 2K]).  Requires N % 16, K % 128.
-int gemv_big(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, float *out, long ldo,
-             const float *resid, float alpha, bool swiglu = false) {
+// Batch 5..32: the products of W [N, K] with x rows [Bp, K] (row stride ldx).  wsp
+// (nullable): a workspace of cap floats for the split-K partials.
+//  * nz_out != null: the partials stay in wsp for the consumer (*nz_out slices of [Bp, N]);
+//  * else, with wsp: out = alpha * (their ordered sum) + resid, one block per sequence, and
+//    with gn also xn = RMSNorm(out) * gn (the next GEMV's input);
+//  * without wsp: one split, out = alpha * products (+ resid) directly;
+//  * gate: W = [W1; W3] (2N rows), out [Bp, N] = silu(W1.x) * (W3.x), one split.
+// Requires N % 16 (gate: N % 8), K % 128.
+int gemv_big(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, long ldx, float *wsp, long cap,
+             float *out, long ldo, const float *resid, float alpha, int *nz_out, const float *gn = nullptr,
+             float *xn = nullptr, bool gate = false) {
   Dec *d = (Dec *)c->dec;
-  if (N % 16 || K % 128) return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%16, K%%128)", N, K);
+  if ((gate ? N % 8 : N % 16) || K % 128)
+    return ne_fail(NE_ERR_ARG, "decode gemv: N=%d K=%d (need N%%16 (gate: %%8), K%%128)", N, K);
+  if (gate && wsp) return ne_fail(NE_ERR_ARG, "decode gemv: the gate form has one split");
   int ks = 1;
-  while ((N / 16) * ks < 512 && K % (128 * ks * 2) == 0 && (long)ks * 2 * d->Bp * N <= d->ws_elems) ks *= 2;
-  const dim3 grid(N / 16, ks);
+  if (wsp)
+    while ((N / 16) * ks < 512 && K % (128 * ks * 2) == 0 && (long)ks * 2 * d->Bp * N <= cap) ks *= 2;
+  if (wsp && (long)ks * d->Bp * N > cap) return ne_fail(NE_ERR_ARG, "decode gemv: workspace too small");
+  const dim3 grid(gate ? N / 8 : N / 16, ks);
+  // the gate form has one split: 8 waves per block shorten each wave's K range instead
+  // (K % 256 then; else 4 waves)
+  const bool wide = gate && K % 256 == 0;
   NE_CHECK(DISPATCH_H16(c->dt, [&] {
+    auto go = [&](auto kernel, int threads) {
+      hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, c->st, W, (long)K, x, ldx, K, ks, out, ldo, resid, alpha,
+                         wsp, N, B, (long)N);
+    };
     if (d->Bp == 16) {
-      if (swiglu) launch_mfma<HT, 1, true>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
-      else launch_mfma<HT, 1, false>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+      if (wide) go(gemv_mfma_kernel<HT, 1, true, 8>, 512);
+      else if (gate) go(gemv_mfma_kernel<HT, 1, true>, 256);
+      else go(gemv_mfma_kernel<HT, 1, false>, 256);
     } else {
-      if (swiglu) launch_mfma<HT, 2, true>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
-      else launch_mfma<HT, 2, false>(grid, c->st, W, K, x, ks, out, ldo, resid, alpha, d->ws, N, B);
+      if (wide) go(gemv_mfma_kernel<HT, 2, true, 8>, 512);
+      else if (gate) go(gemv_mfma_kernel<HT, 2, true>, 256);
+      else go(gemv_mfma_kernel<HT, 2, false>, 256);
     }
     return ne_hip_status(hipGetLastError(), "decode gemv");
   }()));
-  if (ks > 1) {
-    const long n = (long)B * N;
-    hipLaunchKernelGGL(gemv_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, c->st, d->ws, ks, d->Bp, N, out, ldo,
-                       resid, alpha, B);
+  if (nz_out) {
+    *nz_out = ks;
+    return 0;
+  }
+  if (wsp) {
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(B), dim3(256), 0, c->st, wsp, ks, d->Bp, N, out, ldo, resid, alpha, gn, xn,
+                         c->c.norm_eps);
+    };
+    if (N > 1024) go(gemv_reduce_rows_kernel<0>);
+    else if (ks == 1) go(gemv_reduce_rows_kernel<1>);
+    else if (ks == 2) go(gemv_reduce_rows_kernel<2>);
+    else if (ks == 4) go(gemv_reduce_rows_kernel<4>);
+    else if (ks == 8) go(gemv_reduce_rows_kernel<8>);
+    else go(gemv_reduce_rows_kernel<0>);
     NE_HIP(hipGetLastError());
   }
   return 0;
 }
 
-int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc) {
+// qkv: the q|k|v rows [Bp, QKV], or (qnz > 1) qnz split-K partial slices of them.
+int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const float *qkv, int qnz) {
   Dec *d = (Dec *)c->dec;
   const int ratio = c->NH / c->NKV;
   const size_t sh = (size_t)ratio * d->ctx * sizeof(float);
@@ -779,8 +867,8 @@ int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc) {
   const float *gq = c->c.qk_norm ? c->P + o.gq : nullptr, *gk = c->c.qk_norm ? c->P + o.gk : nullptr;
   const dim3 grid(B, c->NKV);
 #define NE_DEC_ATTN(HDV, R)                                                                                     \
-  hipLaunchKernelGGL((dec_attn_kernel<HDV, R>), grid, dim3(256), sh, c->st, d->qkv, c->QKV, gq, gk, d->cosb,   \
-                     d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale)
+  hipLaunchKernelGGL((dec_attn_kernel<HDV, R>), grid, dim3(256), sh, c->st, qkv, c->QKV, gq, gk, d->cosb,      \
+                     d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale, qkv, qnz, d->Bp)
   if (c->HD == 128) {
     if (ratio == 1) NE_DEC_ATTN(128, 1);
     else if (ratio == 2) NE_DEC_ATTN(128, 2);
@@ -804,23 +892,29 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
   const h16_t *Pb = c->Pb;
   const float *Pf = c->P;
   const bool small = B <= VB;
+  // batch 5..32: the kernels that write x (the token lookup, the Wo / W2 split-K reductions)
+  // also write its RMSNorm with the next gain into xn; the QKV GEMV's partials are summed by
+  // the attention kernel
+  const long cap = d->ws_elems;
+  const float *g0 = small ? nullptr : Pf + c->lo[0].g_att;
   if (c->dt == NE_FP16)
     hipLaunchKernelGGL(dec_token_kernel<H16F>, dim3(B), dim3(256), 0, c->st, d->prompt, d->ctx, d->st, d->tok,
-                       Pb + c->off_E, d->x, D, B);
+                       Pb + c->off_E, d->x, D, B, g0, d->xn, eps);
   else
     hipLaunchKernelGGL(dec_token_kernel<H16B>, dim3(B), dim3(256), 0, c->st, d->prompt, d->ctx, d->st, d->tok,
-                       Pb + c->off_E, d->x, D, B);
+                       Pb + c->off_E, d->x, D, B, g0, d->xn, eps);
   NE_HIP(hipGetLastError());
   for (int l = 0; l < c->L; l++) {
     const LayerOff &o = c->lo[l];
     const size_t kvl = (size_t)l * d->Bmax * NKV * d->ctx * HD;
     if (small) {
       NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.wqkv, QKV, D, d->x, D, Pf + o.g_att, d->qkv, QKV, nullptr, 1.f));
+      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->qkv, 1));
     } else {
-      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_att, d->xn, D, eps);
-      NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, d->qkv, QKV, nullptr, 1.f));
+      int qnz = 0;
+      NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, D, d->ws, cap, nullptr, 0, nullptr, 1.f, &qnz));
+      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->ws, qnz));
     }
-    NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl));
     if (small) {
       NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.wo, D, Q, d->att, Q, nullptr, d->x, D, d->x, alpha));
       // W1|W3 with the SwiGLU gate in its epilogue (gate -> xn), then W2 + residual
@@ -828,10 +922,12 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
                           true));
       NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.w2, D, H, d->xn, H, nullptr, d->x, D, d->x, alpha));
     } else {
-      NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, d->x, D, d->x, alpha));
-      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + o.g_ffn, d->xn, D, eps);
-      NE_CHECK(gemv_big(c, B, Pb + o.w13, 2 * H, D, d->xn, d->h13, 2 * H, nullptr, 1.f));
-      NE_CHECK(gemv_big(c, B, Pb + o.w2, D, H, d->h13, d->x, D, d->x, alpha, true));
+      const float *g_next = l + 1 < c->L ? Pf + c->lo[l + 1].g_att : Pf + c->off_gfinal;
+      NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, Q, d->ws, cap, d->x, D, d->x, alpha, nullptr, Pf + o.g_ffn,
+                        d->xn));
+      NE_CHECK(gemv_big(c, B, Pb + o.w13, H, D, d->xn, D, nullptr, 0, d->gate, H, nullptr, 1.f, nullptr, nullptr,
+                        nullptr, true));
+      NE_CHECK(gemv_big(c, B, Pb + o.w2, D, H, d->gate, H, d->ws, cap, d->x, D, d->x, alpha, nullptr, g_next, d->xn));
     }
   }
   if (gen) {
@@ -842,8 +938,7 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
         hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(1024), 0, c->st, d->amv, d->ami, V / (4 * pick_rpw(V)),
                            d->st, d->ctx, d->tok, d->out);
     } else {
-      hipLaunchKernelGGL(dec_rmsnorm_kernel, dim3(B), dim3(256), 0, c->st, d->x, Pf + c->off_gfinal, d->xn, D, eps);
-      NE_CHECK(gemv_big(c, B, Pb + c->off_E, V, D, d->xn, d->logits, V, nullptr, 1.f));
+      NE_CHECK(gemv_big(c, B, Pb + c->off_E, V, D, d->xn, D, nullptr, 0, d->logits, V, nullptr, 1.f, nullptr));
       if (greedy) {
         hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(BIG_ARGMAX, B), dim3(256), 0, c->st, d->logits, V, BIG_ARGMAX,
                            d->amv, d->ami);
@@ -897,8 +992,8 @@ int decode_alloc(ne_ctx *c) {
   const size_t o_kc = take(kv * 4), o_vc = take(kv * 4), o_x = take(Bp * D * 4);
   const size_t o_xn = take(Bp * std::max(D, H) * 4);
   const size_t o_qkv = take(Bp * (Q + 2 * NKV * HD) * 4), o_att = take(Bp * Q * 4);
-  const size_t o_h13 = take(Bp * 2 * H * 4), o_lg = take(Bp * V * 4);
-  const size_t o_ws = take((size_t)d->ws_elems * 4);
+  const size_t o_lg = take(Bp * V * 4);
+  const size_t o_ws = take((size_t)d->ws_elems * 4), o_gate = take(Bp * H * 4);
   const size_t o_amv = take(Bp * (size_t)d->lm_nblk * 4), o_ami = take(Bp * (size_t)d->lm_nblk * 4);
   const size_t o_tok = take(Bp * 4), o_out = take(Bp * ctx * 4), o_pr = take(Bp * ctx * 4), o_u = take(Bp * ctx * 8);
   const size_t o_cos = take(ctx * HD / 2 * 4), o_sin = take(ctx * HD / 2 * 4), o_st = take(sizeof(DecState));
@@ -907,8 +1002,9 @@ int decode_alloc(ne_ctx *c) {
   d->kc = (float *)(base + o_kc); d->vc = (float *)(base + o_vc);
   d->x = (float *)(base + o_x); d->xn = (float *)(base + o_xn);
   d->qkv = (float *)(base + o_qkv); d->att = (float *)(base + o_att);
-  d->h13 = (float *)(base + o_h13); d->logits = (float *)(base + o_lg);
+  d->logits = (float *)(base + o_lg);
   d->ws = (float *)(base + o_ws);
+  d->gate = (float *)(base + o_gate);
   d->amv = (float *)(base + o_amv); d->ami = (int32_t *)(base + o_ami);
   d->tok = (int32_t *)(base + o_tok); d->out = (int32_t *)(base + o_out); d->prompt = (int32_t *)(base + o_pr);
   d->unif = (double *)(base + o_u);
