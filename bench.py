@@ -307,15 +307,27 @@ def main():
         out["at_scale"] = {"workload": "qwen3-0.6b-s2048-b8", "tokens_per_step": ws["batch"] * ws["seq"],
                            **train_summary(ws, rs, ceil["mfma_32x32x16_tflops"])}
     if not a.no_decode and a.workload.startswith("qwen3"):
-        d1, _ = run_decode(w, 1, graphs=not a.no_graphs)
-        d32, _ = run_decode(w, 32, graphs=not a.no_graphs)
+        P, n_new = 32, 200
+        d1, t1 = run_decode(w, 1, n_new, P, graphs=not a.no_graphs)
+        d32, t32 = run_decode(w, 32, n_new, P, graphs=not a.no_graphs)
         gains = w["n_layers"] * (2 * w["dim"] + (2 * w["head_dim"] if w["qk_norm"] else 0)) + w["dim"]
         wbytes = 2 * (npar - gains)                          # bf16 matrices read once per position
-        out["decode"] = {"tokens_per_s_b1": d1, "tokens_per_s_b32": d32, "prompt": 32, "new_tokens": 200,
-                         "weights": "bf16",
-                         "roofline_b1": {"bound": "hbm", "bytes_per_token": wbytes,
-                                         "achieved_GBps": wbytes * d1 / 1e9,
-                                         "frac": wbytes * d1 / PEAK_HBM}}
+        lm = 2 * w["vocab"] * w["dim"]                       # the LM head: generated positions only
+        npos = P - 1 + n_new                                 # positions run one at a time
+
+        def loop_bytes(B):
+            """HBM bytes of one decode call: the weights once per position (all sequences share
+            them), plus each sequence's fp32 K and V cache rows read by attention."""
+            kv_row = 2 * w["n_layers"] * w["kv_heads"] * w["head_dim"] * 4
+            kv = B * kv_row * sum(p + 1 for p in range(npos))
+            return (P - 1) * (wbytes - lm) + n_new * wbytes + kv
+
+        def roof(B, dt):
+            byt = loop_bytes(B)
+            return {"bound": "hbm", "bytes_per_call": byt, "positions": npos, "us_per_position": dt / npos * 1e6,
+                    "achieved_GBps": byt / dt / 1e9, "frac": byt / dt / PEAK_HBM}
+        out["decode"] = {"tokens_per_s_b1": d1, "tokens_per_s_b32": d32, "prompt": P, "new_tokens": n_new,
+                         "weights": "bf16", "roofline_b1": roof(1, t1), "roofline_b32": roof(32, t32)}
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(a.workload, w)
     print(json.dumps(out), flush=True)
