@@ -517,7 +517,17 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
   if (epi == EPI_SWIGLU_BWD && ((g.ldr % 8) || (g.ldc % 8) || (((uintptr_t)g.R | (uintptr_t)g.C) & 15)))
     return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU backward epilogue needs 16-byte aligned h13 / dh13 rows");
-  const int tile = gemm_tile(g.M, g.N, g.K);
+  int tile = gemm_tile(g.M, g.N, g.K);
+  // A long reduction into a small output (the weight gradients of a long step: K = tokens)
+  // takes the 256x256 tile too when split-K can give it a full wave of work-groups: its higher
+  // MFMA rate outweighs writing and summing the fp32 partials (a few % of the GEMM's time).
+  if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD && tile != TILE_256 && g.M % 256 == 0 && g.N % 256 == 0 &&
+      g.K >= 8192) {
+    const long t256 = (long)(g.M / 256) * (g.N / 256);
+    int sp = 1;
+    while (t256 * sp < 256 && sp < 8 && (g.K / 64) / (sp * 2) >= 4 && (long)g.M * g.N * sp * 2 <= g.ws_elems) sp *= 2;
+    if (t256 * sp >= 256) tile = TILE_256;
+  }
   // split K while there are too few work-groups for the 256 CUs (one per CU for the 8-wave
   // tiles, two for the others), keeping >= 4 K steps per split
   g.split = 1;
