@@ -146,8 +146,9 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
     d[g.N + col] = o3;
   } else if constexpr (EPI == EPI_CE_BWD) {
     const float e = __expf(v - g.lse[row]);
-    float p = col < g.n_valid ? e : 0.f;  // padding columns: no gradient (a select, not a branch)
-    if (col == g.targets[row]) p -= 1.f;
+    const int gcol = g.col0 + col;  // column of the full vocabulary
+    float p = gcol < g.n_valid ? e : 0.f;  // padding columns: no gradient (a select, not a branch)
+    if (gcol == g.targets[row]) p -= 1.f;
     const h16_t o = HT::h(p * g.scale);
     bad |= HT::bad(o);
     ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-          const int col = n0 + wn * TN + j * 32 + (lane & 31);
+          const int col = g.col0 + n0 + wn * TN + j * 32 + (lane & 31);  // of the full vocabulary
           // padding columns (>= n_valid) take no part in the softmax
           const float v = col < g.n_valid ? acc[i][j][e] * alpha : -INFINITY;
           acc[i][j][e] = v;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int w = 0; w < WN; w++)
         if (red_m[w][r] > -INFINITY) s += red_s[w][r] * __expf(red_m[w][r] - mx);
-      float *p = g.part + ((long)(m0 + r) * g.n_tiles + nt) * 2;
+      float *p = g.part + ((long)(m0 + r) * g.n_tiles + g.tile0 + nt) * 2;
       p[0] = mx;
       p[1] = s;
     }
@@ -434,7 +435,7 @@ namespace {
 
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 int launch_t(GemmArgs g, hipStream_t s) {
-  g.n_tiles = g.N / BN;
+  g.n_tiles = g.part_ld > 0 ? g.part_ld : g.N / BN;
   dim3 grid(g.N / BN, g.M / BM, g.split);
   hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
   NE_HIP(hipGetLastError());
@@ -504,9 +505,21 @@ int gemm_tile(int M, int N, int K) {
 
 }  // namespace
 
-int gemm_tile_n(int M, int N, int K, int epi) {
-  (void)epi;
-  return tile_bn(gemm_tile(M, N, K));
+// A large output with N (or M) not a multiple of 256 — a vocabulary of 151,936 columns — runs
+// as a part of whole 256-wide tiles (which then takes the 256x256 tile) and a narrow
+// remainder.  Returns the width of that main part, or 0 when the shape is not split: only
+// when the main part has at least four waves of 256x256 work-groups and K >= 1024 (smaller
+// shapes run faster on the narrower tile, which gives twice the work-groups).
+int ragged_main(int M, int N, int K) {
+  const int nm = N / 256 * 256;
+  if (M % 256 || N % 256 == 0 || nm == 0 || K < 1024 || (long)(M / 256) * (nm / 256) < 1024) return 0;
+  return nm;
+}
+
+int gemm_ce_tiles(int M, int N, int K) {
+  const int nm = ragged_main(M, N, K);
+  if (!nm) return N / tile_bn(gemm_tile(M, N, K));
+  return nm / 256 + (N - nm) / tile_bn(gemm_tile(M, N - nm, K));
 }
 
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {
@@ -517,6 +530,36 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
   if (epi == EPI_SWIGLU_BWD && ((g.ldr % 8) || (g.ldc % 8) || (((uintptr_t)g.R | (uintptr_t)g.C) & 15)))
     return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU backward epilogue needs 16-byte aligned h13 / dh13 rows");
+  // ragged shapes: the main part of whole 256-wide tiles, then the rest (see ragged_main)
+  if (epi != EPI_SWIGLU_BWD && !g.defer_reduce) {
+    const size_t ce = epi == EPI_H16 || epi == EPI_CE_BWD ? 2 : 4;  // C element size
+    if (const int nm = ragged_main(g.M, g.N, g.K)) {  // split the columns
+      GemmArgs a = g, b = g;
+      a.N = nm;
+      b.N = g.N - nm;
+      b.B = (const h16_t *)g.B + ((layout & 2) ? (long)nm : (long)nm * g.ldb);
+      if (g.C) b.C = (char *)g.C + nm * ce;
+      if (g.R) b.R = (const float *)g.R + nm;
+      b.col0 = g.col0 + nm;
+      if (epi == EPI_CE_FWD) {
+        a.part_ld = b.part_ld = g.part_ld > 0 ? g.part_ld : gemm_ce_tiles(g.M, g.N, g.K);
+        b.tile0 = g.tile0 + nm / 256;
+      }
+      NE_CHECK(gemm_launch(dt, layout, epi, a, s, split_out));
+      return gemm_launch(dt, layout, epi, b, s, nullptr);
+    }
+    if (epi != EPI_CE_FWD && epi != EPI_CE_BWD)
+      if (const int mm = ragged_main(g.N, g.M, g.K)) {  // split the rows
+        GemmArgs a = g, b = g;
+        a.M = mm;
+        b.M = g.M - mm;
+        b.A = (const h16_t *)g.A + ((layout & 1) ? (long)mm : (long)mm * g.lda);
+        if (g.C) b.C = (char *)g.C + (size_t)mm * g.ldc * ce;
+        if (g.R) b.R = (const float *)g.R + (long)mm * g.ldr;
+        NE_CHECK(gemm_launch(dt, layout, epi, a, s, split_out));
+        return gemm_launch(dt, layout, epi, b, s, nullptr);
+      }
+  }
   int tile = gemm_tile(g.M, g.N, g.K);
   // A long reduction into a small output (the weight gradients of a long step: K = tokens)
   // takes the 256x256 tile too when split-K can give it a full wave of work-groups: its higher

@@ -114,7 +114,7 @@ int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int
   g.targets = targets; g.part = part; g.tgt_logit = tgt_logit;
   g.n_valid = n_valid;
   NE_CHECK(gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s));
-  return launch_ce_reduce(part, V / gemm_tile_n(T, V, D, EPI_CE_FWD), tgt_logit, lse, loss_rows, loss, T, s);
+  return launch_ce_reduce(part, gemm_ce_tiles(T, V, D), tgt_logit, lse, loss_rows, loss, T, s);
 }
 
 int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse, int T, int D,

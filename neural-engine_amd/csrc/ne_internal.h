@@ -62,6 +62,9 @@ struct GemmArgs {
   int split;                 // set by the launcher: K splits (grid.z)
   int defer_reduce;          // with K splits, leave the fp32 partials in ws for the consumer
   int n_valid;               // CE epilogues: columns >= n_valid are outside the softmax (0: N)
+  int col0;                  // CE epilogues: the full output's column of this launch's column 0
+  int tile0;                 // EPI_CE_FWD: the partial slot of this launch's first N tile
+  int part_ld;               // EPI_CE_FWD: partial slots per row (0: N / BN)
 };
 
 // Split-K partials of a GEMM whose reduction is folded into its consumer: element e of the
@@ -78,7 +81,7 @@ struct SplitIn {
 // *split_out (nullable) receives the K splits used; with a.defer_reduce and more than one
 // split, C is not written and the partials stay in a.ws (M*N floats per split).
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
-int gemm_tile_n(int M, int N, int K, int epi);  // BN the launcher uses for this shape
+int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per row it writes
 // Measurement kernel: MFMA chains without memory traffic (shape 0 = 32x32x16, 1 = 16x16x32).
 int launch_mfma_ceiling(int dt, int shape, int blocks, int iters, float *out, hipStream_t s);
 

@@ -73,6 +73,42 @@ def test_gemm_epilogues(fmt, epi):
         assert rel_l2(host(c), R + 0.25 * ref) < 1e-6
 
 
+@pytest.mark.parametrize("layout,epi,M,N", [(0, 0, 2048, 32896), (0, 1, 2048, 32896), (0, 3, 2048, 32896),
+                                            (3, 1, 65664, 1024)])
+def test_gemm_ragged_split(layout, epi, M, N):
+    """A large output whose N (or M) is not a multiple of 256 (128.5 or 256.5 tiles of 256,
+    1024-deep) runs as a part of whole 256-wide tiles and the remaining columns (rows): the
+    seam and the last columns (rows) match the float64 product, and the guard row past the
+    output stays zero."""
+    K = 1024
+    dt, tdt, _, u = FMT["fp16"]
+    rng = np.random.default_rng(M + N + epi)
+    A, B, a, lda, b, ldb = _operands(rng, M, N, K, layout, "fp16")
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    if epi == 0:
+        c = zeros((M + 1, N), tdt)
+        call(L.ne_k_gemm, dt, layout, 0, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 1.0, None)
+        got = host(c)
+        assert rel_l2(got[:M], ref) < u
+        assert rel_l2(got[:, -128:][:M], ref[:, -128:]) < u  # the remainder part
+    elif epi == 1:
+        c = zeros((M + 1, N))
+        call(L.ne_k_gemm, dt, layout, 1, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, None, 0, 0.5, None)
+        got = host(c)
+        err = np.abs(got[:M] - 0.5 * ref).max() / np.abs(ref).max()
+        assert err < 1e-5, err
+        tail = got[M - 128:M] if layout == 3 else got[:M, -128:]
+        tref = 0.5 * (ref[M - 128:] if layout == 3 else ref[:, -128:])
+        assert np.abs(tail - tref).max() / np.abs(ref).max() < 1e-5
+    else:
+        R = rng.standard_normal((M, N)).astype(np.float32)
+        c = zeros((M + 1, N))
+        call(L.ne_k_gemm, dt, layout, 3, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N, ptr(dev(R)), N, 0.25, None)
+        got = host(c)
+        assert rel_l2(got[:M], R + 0.25 * ref) < 1e-6
+    assert np.abs(got[M]).max() == 0
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 def test_gemm_swiglu_backward_epilogue(fmt):
     T, D, H = 128, 256, 320
@@ -273,10 +309,13 @@ def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
 # --------------------------------------------------------------- cross-entropy (LM head)
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768), (256, 128, 65664)])
+@pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768), (256, 128, 65664),
+                                   (2048, 1024, 32896)])
 def test_fused_ce_fwd_bwd(fmt, T, D, V):
-    """(256, 128, 65664): a vocabulary 256.5 tiles of 256 wide.  The guard row after dlogits
-    must stay zero (no store past the last column)."""
+    """(256, 128, 65664): a vocabulary 256.5 tiles of 256 wide.  (2048, 1024, 32896): 128.5
+    tiles, large enough that the classifier GEMMs run as whole 256-wide tiles plus the last 128
+    columns (partial slots and target columns offset in the second launch).  The guard row
+    after dlogits must stay zero (no store past the last column)."""
     dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(V)
     x = rnd(rng.standard_normal((T, D)).astype(np.float32))
