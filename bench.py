@@ -113,7 +113,7 @@ def run_train(w, steps, warmup, graphs=True, overlap=True):
     m.prof_reset()
     m.prof_enable()
     for i in range(2):
-        step(toks[i])
+        step(toks[i % len(toks)])
     fam = {k: v for k, v in m.prof().items() if v[1]}
     m.prof_enable(())
     scale, skipped, sites = m.grad_scale_info()
