@@ -178,8 +178,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   // tile and a group's A tiles recur), and XCD x takes one contiguous stretch of that
   // sequence: the M tiles that share a B tile run on the same XCD and find it in its L2, as
   // do the recurring A tiles.  (Handing consecutive tiles to different XCDs made every XCD
-  // fetch each B tile: 4x the weight bytes for a 256-token forward GEMM.)
-  constexpr int GM = 8, NX = 8;
+  // fetch each B tile: 4x the weight bytes for a 256-token forward GEMM.)  GM = 4: a group's
+  // A tiles (4 x 512 KB at K = 1024) stay in the 4 MB L2 beside the streaming B tiles; 8 did
+  // not fit, and the 16k-token step ran 1.2% slower with it.
+  constexpr int GM = 4, NX = 8;
   int mt, nt;
   {
     const int num_m = gridDim.y, num_n = gridDim.x;
