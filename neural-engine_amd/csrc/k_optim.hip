@@ -29,13 +29,20 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float *__restrict__ g,
   if (threadIdx.x == 0) partials[blockIdx.x] = (double)red[0] + red[1] + red[2] + red[3];
 }
 
-// norm = grad_scale * sqrt(sum partials); factor = grad_scale * (clip / norm if norm > clip)
-__global__ void clip_finalize_kernel(const double *__restrict__ partials, int nparts, float grad_scale,
-                                     float clip, float *__restrict__ gscale, float *__restrict__ gnorm) {
+// norm = grad_scale * sqrt(sum partials); factor = grad_scale * (clip / norm if norm > clip).
+// One block of 256 threads: strided sums, then the 4 wave sums in order (it sits between the
+// backward and the update, so its latency is on the step's critical path).
+__global__ __launch_bounds__(256) void clip_finalize_kernel(const double *__restrict__ partials, int nparts,
+                                                            float grad_scale, float clip, float *__restrict__ gscale,
+                                                            float *__restrict__ gnorm) {
+  __shared__ double red[4];
   double s = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += 64) s += partials[i];
+  for (int i = threadIdx.x; i < nparts; i += 256) s += partials[i];
   s = wave_sum_d(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
   if (threadIdx.x == 0) {
+    s = red[0] + red[1] + red[2] + red[3];
     // the partials may include signed row changes (embedding scatter): never below 0
     const float norm = (float)(sqrt(fmax(s, 0.0)) * (double)grad_scale);
     float f = grad_scale;
@@ -118,7 +125,7 @@ int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream
 
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
                          float *gscale_out, float *gnorm_out, hipStream_t s) {
-  hipLaunchKernelGGL(clip_finalize_kernel, dim3(1), dim3(64), 0, s, partials, nparts, grad_scale, clip,
+  hipLaunchKernelGGL(clip_finalize_kernel, dim3(1), dim3(256), 0, s, partials, nparts, grad_scale, clip,
                      gscale_out, gnorm_out);
   return ne_hip_status(hipGetLastError(), "clip_finalize");
 }
