@@ -573,12 +573,15 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
     while (t256 * sp < 256 && sp < 8 && (g.K / 64) / (sp * 2) >= 4 && (long)g.M * g.N * sp * 2 <= g.ws_elems) sp *= 2;
     if (t256 * sp >= 256) tile = TILE_256;
   }
-  // split K while there are too few work-groups for the 256 CUs (one per CU for the 8-wave
-  // tiles, two for the others), keeping >= 4 K steps per split
+  // split K while too few work-groups would run (8-wave tiles: fewer than one per CU;
+  // 4-wave tiles: fewer than 3/4 of the CUs), keeping >= 4 K steps per split.  Each split
+  // adds an fp32 partial output to write and read back: at 256 tokens the partials of a
+  // layer's GEMMs outweighed its weights at two work-groups per CU (target 512: 8.84 ms per
+  // Qwen3-0.6B step, 256: 8.64, 192: 8.54, 128: 9.25).
   g.split = 1;
   if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD) {
     const long tiles = (long)(g.M / tile_bm(tile)) * (g.N / tile_bn(tile));
-    const long target = tile_bm(tile) == 256 ? 256 : 512;
+    const long target = tile_bm(tile) == 256 ? 256 : 192;
     const int nkt = g.K / 64;
     while (tiles * g.split < target && nkt / (g.split * 2) >= 4 && g.split < 64 &&
            (long)g.M * g.N * g.split * 2 <= g.ws_elems)
