@@ -1,4 +1,4 @@
-"""Full-size parity of the training step against the fp32 numpy oracle on the BASELINE
+"""Full-size parity of the training step against the fp32 numpy oracle on the benchmarked
 shapes: Stories110M (B=1, S=256, 10 steps of fwd+bwd+AdamW on fresh batches) and
 Qwen3-0.6B (B=1, S=256, QK-norm, theta=1e6).  Tolerances: loss rel err <= 1e-3, per-tensor
 gradient rel-L2 <= 1e-2; the AdamW update itself is checked to 1e-5 in
