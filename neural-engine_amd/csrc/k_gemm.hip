@@ -409,18 +409,31 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
 }
 
 // Ordered sum of the split-K partials (split 0 first) followed by the epilogue; four
-// consecutive columns per thread.
-template <typename HT, int EPI>
+// consecutive columns per thread.  The partials are read KS at a time (KS divides the split,
+// a power of two), all KS loads issued before the first add, so a thread waits on HBM once per
+// KS partials rather than once per partial.
+template <typename HT, int EPI, int KS>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
   const long n4 = (long)g.M * g.N / 4;
   const long slice = (long)g.M * g.N;
   bool bad = false;
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
     const long e = i * 4;
-    float4 s = *(const float4 *)(g.ws + e);
-    for (int z = 1; z < g.split; z++) {
-      const float4 p = *(const float4 *)(g.ws + z * slice + e);
-      s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+    float4 p[KS];
+#pragma unroll
+    for (int z = 0; z < KS; z++) p[z] = *(const float4 *)(g.ws + z * slice + e);
+    float4 s = p[0];
+#pragma unroll
+    for (int z = 1; z < KS; z++) {
+      s.x += p[z].x; s.y += p[z].y; s.z += p[z].z; s.w += p[z].w;
+    }
+    for (int z0 = KS; z0 < g.split; z0 += KS) {
+#pragma unroll
+      for (int z = 0; z < KS; z++) p[z] = *(const float4 *)(g.ws + (z0 + z) * slice + e);
+#pragma unroll
+      for (int z = 0; z < KS; z++) {
+        s.x += p[z].x; s.y += p[z].y; s.z += p[z].z; s.w += p[z].w;
+      }
     }
     const int row = (int)(e / g.N), col = (int)(e % g.N);
     store_out<HT, EPI>(g, row, col, s.x * g.alpha, bad);
@@ -445,7 +458,10 @@ int launch_t(GemmArgs g, hipStream_t s) {
     if constexpr (EPI != EPI_CE_FWD) {
       const long n4 = (long)g.M * g.N / 4;
       const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
-      hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI>), dim3(blocks), dim3(256), 0, s, g);
+      if (g.split == 2) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 2>), dim3(blocks), dim3(256), 0, s, g);
+      else if (g.split == 4) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 4>), dim3(blocks), dim3(256), 0, s, g);
+      else if (g.split % 8 == 0) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 8>), dim3(blocks), dim3(256), 0, s, g);
+      else return ne_fail(NE_ERR_ARG, "gemm: split %d is not a power of two", g.split);
       NE_HIP(hipGetLastError());
     }
   }
