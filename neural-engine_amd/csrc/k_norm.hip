@@ -90,7 +90,7 @@ constexpr int RMS_NT = 256, RMS_VPT = 2;
 __device__ __forceinline__ float block_sum_row(float v, float (*red)[RMS_NT / 64], int slot) {
   v = wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[slot][threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();  // waits for the LDS writes only: global loads issued earlier stay in flight
   return red[slot][0] + red[slot][1] + red[slot][2] + red[slot][3];
 }
 
@@ -212,29 +212,41 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
   const int r0 = blockIdx.x * rows_per_block;
   const int r1 = min(T, r0 + rows_per_block);
   bool bad = false;
-  for (int row = r0; row < r1; row++) {
-    const float4 *xr = (const float4 *)(x + (long)row * D);
-    float4 dyv[RMS_VPT], xv[RMS_VPT];
+  // Row loads (dy, x, the residual and r) are issued one row ahead: the next row's loads are in
+  // flight during this row's block reduction and stores.
+  float4 dyv[RMS_VPT], xv[RMS_VPT], rsv[RMS_VPT];
+  float r = 0.f;
+  auto load_row = [&](int row, float4 (&dyo)[RMS_VPT], float4 (&xo)[RMS_VPT], float4 (&rso)[RMS_VPT], float &ro) {
     if (sp.n > 0) {
-      split_row(sp, row, D, dyv);
+      split_row(sp, row, D, dyo);
     } else {
       const float4 *dyr = (const float4 *)(dy + (long)row * D);
 #pragma unroll
       for (int j = 0; j < RMS_VPT; j++)
-        dyv[j] = t + RMS_NT * j < D4 ? dyr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        dyo[j] = t + RMS_NT * j < D4 ? dyr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float dot = 0.f;
+    const float4 *xr = (const float4 *)(x + (long)row * D);
+    const float4 *rsr = resid ? (const float4 *)(resid + (long)row * D) : nullptr;
 #pragma unroll
     for (int j = 0; j < RMS_VPT; j++) {
-      xv[j] = t + RMS_NT * j < D4 ? xr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      xo[j] = t + RMS_NT * j < D4 ? xr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      rso[j] = rsr && t + RMS_NT * j < D4 ? rsr[t + RMS_NT * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    ro = rr[row];
+  };
+  if (r0 < r1) load_row(r0, dyv, xv, rsv, r);
+  for (int row = r0; row < r1; row++) {
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < RMS_VPT; j++)
       dot += dyv[j].x * xv[j].x * gw[j].x + dyv[j].y * xv[j].y * gw[j].y + dyv[j].z * xv[j].z * gw[j].z +
              dyv[j].w * xv[j].w * gw[j].w;
-    }
-    const float r = rr[row];
+    float4 dyn[RMS_VPT], xn[RMS_VPT], rsn[RMS_VPT];
+    float rn = 0.f;
+    if (row + 1 < r1) load_row(row + 1, dyn, xn, rsn, rn);
     dot = block_sum_row(dot, red, row & 1);
     const float c = r * r * r * dot * invD;
     float4 *dxr = (float4 *)(dx + (long)row * D);
-    const float4 *rsr = resid ? (const float4 *)(resid + (long)row * D) : nullptr;
     u16x4 *dbr = dxb ? (u16x4 *)(dxb + (long)row * D) : nullptr;
 #pragma unroll
     for (int j = 0; j < RMS_VPT; j++) {
@@ -246,9 +258,8 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
         o.y = r * w.y * dyv[j].y - xv[j].y * c;
         o.z = r * w.z * dyv[j].z - xv[j].z * c;
         o.w = r * w.w * dyv[j].w - xv[j].w * c;
-        if (rsr) {
-          const float4 q = rsr[i];
-          o.x += q.x; o.y += q.y; o.z += q.z; o.w += q.w;
+        if (resid) {
+          o.x += rsv[j].x; o.y += rsv[j].y; o.z += rsv[j].z; o.w += rsv[j].w;
         }
         dxr[i] = o;
         if (dbr) {
@@ -265,6 +276,15 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
         acc[j].z += dyv[j].z * xv[j].z * r;
         acc[j].w += dyv[j].w * xv[j].w * r;
       }
+    }
+    if (row + 1 < r1) {
+#pragma unroll
+      for (int j = 0; j < RMS_VPT; j++) {
+        dyv[j] = dyn[j];
+        xv[j] = xn[j];
+        rsv[j] = rsn[j];
+      }
+      r = rn;
     }
   }
   flag_overflow(ovf, bad);
