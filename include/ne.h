@@ -138,6 +138,19 @@ int ne_zero_grads(ne_ctx *ctx);
  * counterpart (the ANE path had a fixed loss scale 256, TD/train.m:180). */
 int ne_grad_scale_info(const ne_ctx *ctx, float *scale, int32_t *skipped_steps,
                        int32_t *overflow_sites);
+/* Norms of the gradient the last ne_optimizer_step used, before the clip and after its
+ * grad_scale: out[0] the global norm, out[1] the attention matrices (Wq, Wk, Wv, Wo of every
+ * layer), out[2] the FFN matrices (W1, W2, W3), out[3] the embedding; the gains count only
+ * in out[0].  Valid until the next ne_train_step, ne_zero_grads or gradient write
+ * (NE_ERR_STATE otherwise, and after a skipped step).  Replaces the attn_sq / ffn_sq /
+ * embed_sq sums printed with the global norm (TD/train.m:786-830). */
+int ne_grad_norm_parts(ne_ctx *ctx, float out[4]);
+/* Range of the last ne_train_step's final hidden state x (the last layer's output, before the
+ * final RMSNorm) and of the gradient dy of the loss times loss_scale with respect to the
+ * first layer's input, in the reference's scale (d(mean loss * loss_scale)/dx):
+ * out = {x_min, x_max, dy_min, dy_max}.  Synchronises.  Replaces the vDSP_minv / vDSP_maxv of
+ * the step line (TD/train.m:770-777). */
+int ne_step_stats(ne_ctx *ctx, float out[4]);
 int ne_get_state(const ne_ctx *ctx, ne_train_state *st);
 int ne_set_state(ne_ctx *ctx, const ne_train_state *st);
 

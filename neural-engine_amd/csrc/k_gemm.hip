@@ -73,6 +73,11 @@ struct Stage {
     }
   }
 
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < PER; i++) v[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
   __device__ __forceinline__ void store(h16_t *lds, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -144,18 +149,19 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
     bad |= HT::bad(o1) | HT::bad(o3);
     d[col] = o1;
     d[g.N + col] = o3;
-  } else if constexpr (EPI == EPI_CE_BWD) {
-    const float e = __expf(v - g.lse[row]);
-    const int gcol = g.col0 + col;  // column of the full vocabulary
-    float p = gcol < g.n_valid ? e : 0.f;  // padding columns: no gradient (a select, not a branch)
-    if (gcol == g.targets[row]) p -= 1.f;
-    const h16_t o = HT::h(p * g.scale);
-    bad |= HT::bad(o);
-    ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
   }
 }
 
-template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
+// How a split's K steps are run: the software pipeline takes two steps per iteration.
+//  KM_TAIL: an odd last step is computed after the loop (the default);
+//  KM_EVEN: every split has an even step count (no tail code at all);
+//  KM_PAD:  an odd count runs one extra step whose A stage is zero.
+// The cross-entropy epilogues hold more registers than the others: with the tail, the
+// allocator copied the accumulators around the conditional compute (392 bytes of scratch per
+// lane for EPI_CE_FWD); they take KM_EVEN or KM_PAD.
+enum { KM_TAIL = 0, KM_EVEN = 1, KM_PAD = 2 };
+
+template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI, int KMODE>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int NTHREADS = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -234,9 +240,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         for (int j = 0; j < FN; j++) acc[i][j] = HT::mfma32(a[i], b[j], acc[i][j]);
     }
   };
-  auto load = [&](SA &a, SB &b, int kt) {
+  const int n = kt1 - kt0;  // K steps of this split (>= 1)
+  const int nr = KMODE == KM_PAD ? n + (n & 1) : n;  // steps run
+  // Stage j of the split is loaded from K step kt0 + min(j, n - 1): the loads past the end
+  // repeat the last step (valid memory, never computed), so the loop body has no branch and
+  // one register allocation covers every split length.
+  auto load = [&](SA &a, SB &b, int j) {
+    const int kt = kt0 + min(j, n - 1);
     a.load(A, g.lda, m0, kt * BK, tid);
     b.load(B, g.ldb, n0, kt * BK, tid);
+    if constexpr (KMODE == KM_PAD)
+      if (j >= n) a.zero();  // the padding step adds nothing
   };
   auto store = [&](h16_t *L, SA &a, SB &b) {
     a.store(L, tid);
@@ -244,28 +258,24 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   };
   auto sched = [&]() { sched_kstep<NMF, NDR, NGL, NDW, NGL>(); };
 
-  const int n = kt1 - kt0;  // K steps of this split (>= 1)
-  // Stage j of the split is loaded from K step kt0 + min(j, n - 1): the loads past the end
-  // repeat the last step (valid memory, never computed), so the loop body has no branch and
-  // one register allocation covers every split length.
-  auto kstep = [&](int j) { return kt0 + min(j, n - 1); };
-  load(sa0, sb0, kt0);
+  load(sa0, sb0, 0);
   store(lds0, sa0, sb0);
-  load(sa0, sb0, kstep(1));
+  load(sa0, sb0, 1);
   lds_barrier();
-  for (int i = 0; i + 1 < n; i += 2) {  // steps i (lds0) and i + 1 (lds1)
-    load(sa1, sb1, kstep(i + 2));
+  for (int i = 0; i + 1 < nr; i += 2) {  // steps i (lds0) and i + 1 (lds1)
+    load(sa1, sb1, i + 2);
     compute(lds0);
     store(lds1, sa0, sb0);
     sched();
     lds_barrier();
-    load(sa0, sb0, kstep(i + 3));
+    load(sa0, sb0, i + 3);
     compute(lds1);
     store(lds0, sa1, sb1);
     sched();
     lds_barrier();
   }
-  if (n & 1) compute(lds0);  // the last step of an odd count is in lds0
+  if constexpr (KMODE == KM_TAIL)
+    if (n & 1) compute(lds0);  // the last step of an odd count is in lds0
 
   // ---- epilogue: lane owns column (lane & 31) and rows 8*(e/4) + 4*(lane/32) + e%4 ----
   const float alpha = g.alpha;
@@ -286,7 +296,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
           const int col = g.col0 + n0 + wn * TN + j * 32 + (lane & 31);  // of the full vocabulary
           // padding columns (>= n_valid) take no part in the softmax
           const float v = col < g.n_valid ? acc[i][j][e] * alpha : -INFINITY;
-          acc[i][j][e] = v;
           mx = fmaxf(mx, v);
           if (col == tgt) g.tgt_logit[row] = v;
         }
@@ -297,7 +306,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         const float mxs = mx > -INFINITY ? mx : 0.f;
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < FN; j++) s += __expf(acc[i][j][e] - mxs);
+        for (int j = 0; j < FN; j++) {
+          const int col = g.col0 + n0 + wn * TN + j * 32 + (lane & 31);
+          s += col < g.n_valid ? __expf(acc[i][j][e] * alpha - mxs) : 0.f;
+        }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
         if ((lane & 31) == 0) {
@@ -338,18 +350,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     return;
   }
 
-  if constexpr (EPI == EPI_SWIGLU_BWD) {
-    // Through LDS, so that the gate reads and the dh1 | dh3 writes are 16-byte row pieces
+  if constexpr (EPI == EPI_SWIGLU_BWD || EPI == EPI_CE_BWD) {
+    // Through LDS, so that the 16-bit outputs (and the SwiGLU gate reads) are 16-byte row pieces
     // (in the MFMA layout each lane would touch one 2-byte element per row): pass i stages row
     // block i of every wave row (WM * 32 rows x BN fp32, the first half of the rows in lds0, the
     // second in lds1), then each thread takes 8 consecutive columns of a row.
     constexpr int SR = WM * 32, HR = SR / 2, SP = BN + 8;  // rows per pass, per buffer; pitch
     constexpr int CPR8 = BN / 8, NCHK = SR * CPR8 / NTHREADS;
-    static_assert(HR * SP * 4 <= (SA::ELEMS + SB::ELEMS) * 2, "SwiGLU epilogue: staging must fit an LDS buffer");
-    static_assert(SR * CPR8 % NTHREADS == 0, "SwiGLU epilogue: whole chunks per thread");
+    static_assert(HR * SP * 4 <= (SA::ELEMS + SB::ELEMS) * 2, "staged epilogue: a pass must fit an LDS buffer");
+    static_assert(SR * CPR8 % NTHREADS == 0, "staged epilogue: whole chunks per thread");
     float *st0 = (float *)lds0, *st1 = (float *)lds1;
-    const h16_t *hb = (const h16_t *)g.R;
-    h16_t *db = (h16_t *)g.C;
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < FM; i++) {
@@ -373,19 +383,38 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
         const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         const long grow = m0 + (row / 32) * TM + i * 32 + row % 32;
         const int gcol = n0 + c8 * 8;
-        const u16x8 h1v = *(const u16x8 *)(hb + grow * g.ldr + gcol);
-        const u16x8 h3v = *(const u16x8 *)(hb + grow * g.ldr + g.N + gcol);
-        u16x8 o1, o3;
+        if constexpr (EPI == EPI_SWIGLU_BWD) {
+          const h16_t *hb = (const h16_t *)g.R;
+          h16_t *db = (h16_t *)g.C;
+          const u16x8 h1v = *(const u16x8 *)(hb + grow * g.ldr + gcol);
+          const u16x8 h3v = *(const u16x8 *)(hb + grow * g.ldr + g.N + gcol);
+          u16x8 o1, o3;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float h1 = HT::f(h1v[e]), h3 = HT::f(h3v[e]);
-          const float sg = fast_sigmoid(h1);
-          o1[e] = HT::h(v[e] * h3 * sg * (1.f + h1 * (1.f - sg)));
-          o3[e] = HT::h(v[e] * h1 * sg);
-          bad |= HT::bad(o1[e]) | HT::bad(o3[e]);
+          for (int e = 0; e < 8; e++) {
+            const float h1 = HT::f(h1v[e]), h3 = HT::f(h3v[e]);
+            const float sg = fast_sigmoid(h1);
+            o1[e] = HT::h(v[e] * h3 * sg * (1.f + h1 * (1.f - sg)));
+            o3[e] = HT::h(v[e] * h1 * sg);
+            bad |= HT::bad(o1[e]) | HT::bad(o3[e]);
+          }
+          *(u16x8 *)(db + grow * g.ldc + gcol) = o1;
+          *(u16x8 *)(db + grow * g.ldc + g.N + gcol) = o3;
+        } else {
+          // dlogits = (exp(logit - lse) - onehot(target)) * scale; padding columns (of the
+          // full vocabulary's numbering, >= n_valid) get no gradient
+          const float l = g.lse[grow];
+          const int tc = g.targets[grow] - g.col0 - gcol;  // target's offset in this chunk
+          const int nv = g.n_valid - g.col0 - gcol;        // valid columns in this chunk
+          u16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            float p = e < nv ? __expf(v[e] - l) : 0.f;
+            if (e == tc) p -= 1.f;
+            o[e] = HT::h(p * g.scale);
+            bad |= HT::bad(o[e]);
+          }
+          *(u16x8 *)((h16_t *)g.C + grow * g.ldc + gcol) = o;
         }
-        *(u16x8 *)(db + grow * g.ldc + gcol) = o1;
-        *(u16x8 *)(db + grow * g.ldc + g.N + gcol) = o3;
       }
     }
     flag_overflow(g.ovf, bad);
@@ -452,10 +481,17 @@ template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BK
 int launch_t(GemmArgs g, hipStream_t s) {
   g.n_tiles = g.part_ld > 0 ? g.part_ld : g.N / BN;
   dim3 grid(g.N / BN, g.M / BM, g.split);
-  hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI>), grid, dim3(WM * WN * 64), 0, s, g);
+  if constexpr (EPI == EPI_CE_FWD || EPI == EPI_CE_BWD) {  // never split
+    if ((g.K / BK) % 2 == 0)
+      hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KM_EVEN>), grid, dim3(WM * WN * 64), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KM_PAD>), grid, dim3(WM * WN * 64), 0, s, g);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KM_TAIL>), grid, dim3(WM * WN * 64), 0, s, g);
+  }
   NE_HIP(hipGetLastError());
   if (g.split > 1 && !g.defer_reduce) {
-    if constexpr (EPI != EPI_CE_FWD) {
+    if constexpr (EPI != EPI_CE_FWD && EPI != EPI_CE_BWD) {
       const long n4 = (long)g.M * g.N / 4;
       const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
       if (g.split == 2) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 2>), dim3(blocks), dim3(256), 0, s, g);
@@ -548,6 +584,8 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
   if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
   if (epi == EPI_SWIGLU_BWD && ((g.ldr % 8) || (g.ldc % 8) || (((uintptr_t)g.R | (uintptr_t)g.C) & 15)))
     return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU backward epilogue needs 16-byte aligned h13 / dh13 rows");
+  if (epi == EPI_CE_BWD && ((g.ldc % 8) || ((uintptr_t)g.C & 15)))
+    return ne_fail(NE_ERR_ARG, "gemm: the cross-entropy backward needs 16-byte aligned dlogits rows");
   // ragged shapes: the main part of whole 256-wide tiles, then the rest (see ragged_main)
   if (epi != EPI_SWIGLU_BWD && !g.defer_reduce) {
     const size_t ce = epi == EPI_H16 || epi == EPI_CE_BWD ? 2 : 4;  // C element size

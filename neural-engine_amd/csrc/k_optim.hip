@@ -114,6 +114,30 @@ __global__ void fill_f32_kernel(float *__restrict__ dst, float v, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = v;
 }
 
+__global__ __launch_bounds__(256) void minmax_kernel(const float *__restrict__ a, long n, float *__restrict__ out) {
+  __shared__ float rmn[4], rmx[4];
+  float mn = INFINITY, mx = -INFINITY;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const float v = a[i];
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, o, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    rmn[threadIdx.x >> 6] = mn;
+    rmx[threadIdx.x >> 6] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = fminf(fminf(rmn[0], rmn[1]), fminf(rmn[2], rmn[3]));
+    out[2 * blockIdx.x + 1] = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
+  }
+}
+
 int grid_for(long n) { return (int)std::max<long>(1, std::min<long>((n + 255) / 256, 256L * 32)); }
 
 }  // namespace
@@ -146,6 +170,11 @@ int launch_f32_to_h16(int dt, const float *src, h16_t *dst, long n, hipStream_t 
     hipLaunchKernelGGL(f32_to_h16_kernel<HT>, dim3(grid_for(n)), dim3(256), 0, s, src, dst, n);
     return ne_hip_status(hipGetLastError(), "f32_to_h16");
   }());
+}
+
+int launch_minmax(const float *a, long n, float *out, int nblocks, hipStream_t s) {
+  hipLaunchKernelGGL(minmax_kernel, dim3(nblocks), dim3(256), 0, s, a, n, out);
+  return ne_hip_status(hipGetLastError(), "minmax");
 }
 
 int launch_fill_f32(float *dst, float v, long n, hipStream_t s) {

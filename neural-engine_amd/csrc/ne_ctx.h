@@ -32,6 +32,8 @@ enum {
   OVF_DV, OVF_DQKV, OVF_COUNT
 };
 
+constexpr int NE_STATS_BLOCKS = 256;
+
 struct LayerAct {
   float *x_in, *r1, *x2, *r2, *rq, *rk, *lse;
   h16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
@@ -82,6 +84,13 @@ struct ne_ctx {
   // gn_ready: they describe G as it is now (else the optimizer sums G itself)
   double *gn_part;
   bool gn_ready = false;
+  // the last non-skipped optimizer step summed gn_part over G as it then was, at grad_scale
+  // gn_gsc (ne_grad_norm_parts reads the groups back until the next step or gradient write)
+  bool gn_parts_ok = false;
+  float gn_gsc = 1.f;
+  float *stats_part;      // device [2][2 * NE_STATS_BLOCKS] min/max partials (ne_step_stats)
+  float last_u = 0.f;     // fp32-sink factor of the last step: reference-scale dx = dx * last_u
+  bool stats_ok = false;  // a step has run since the context was created
   float *gscale, *gnorm;
   int *ovf;               // device flags [32], one per conversion site (OVF_*): a 16-bit value
                           // of this accumulation window was not finite

@@ -223,15 +223,32 @@ float *norm_part(ne_ctx *c, int site) { return c->gpart + (long)site * c->rms_sl
 float *qk_part(ne_ctx *c, int l) { return c->gpart + (long)(2 * c->L + 1) * c->rms_slab + (long)l * c->qk_slab; }
 
 // Sum-of-squares partials of G, reduced in slot order by the optimizer: layer l's matrix
-// gradients (contiguous from lo[l].wqkv), the embedding, the gains, then one slot per token
-// row for the change the embedding scatter makes to the row it updates.
-constexpr int GN_LAYER = 128, GN_EMBED = 512, GN_GAINS = 16, GN_FULL = 1024;
+// gradients (its attention block Wqkv, Wo from lo[l].wqkv, then its FFN block W13, W2 from
+// lo[l].w13: GN_LAYER / 2 slots each), the embedding, the gains, then one slot per token row
+// for the change the embedding scatter makes to the row it updates.
+constexpr int GN_LAYER = 128, GN_EMBED = 512, GN_GAINS = 16;
 long gn_layer(const ne_ctx *c, int l) { (void)c; return (long)l * GN_LAYER; }
 long gn_embed(const ne_ctx *c) { return (long)c->L * GN_LAYER; }
 long gn_gains(const ne_ctx *c) { return gn_embed(c) + GN_EMBED; }
 long gn_rows(const ne_ctx *c) { return gn_gains(c) + GN_GAINS; }
 long gn_slots(const ne_ctx *c) { return gn_rows(c) + c->T; }
 long layer_params(const ne_ctx *c) { return (long)(c->QKV + c->Q + 3L * c->H) * c->D; }
+long layer_attn_params(const ne_ctx *c) { return (long)(c->QKV + c->Q) * c->D; }
+
+// Sum of squares of all of G into the slots the step fills (the per-row change slots of the
+// embedding scatter read 0), on st: for an optimizer step that follows a direct gradient
+// write or no micro-step at all.
+int gn_sum_all(ne_ctx *c) {
+  for (int l = 0; l < c->L; l++) {
+    const LayerOff &o = c->lo[l];
+    NE_CHECK(launch_sumsq(c->G + o.wqkv, layer_attn_params(c), c->gn_part + gn_layer(c, l), GN_LAYER / 2, c->st));
+    NE_CHECK(launch_sumsq(c->G + o.w13, layer_params(c) - layer_attn_params(c), c->gn_part + gn_layer(c, l) + GN_LAYER / 2,
+                          GN_LAYER / 2, c->st));
+  }
+  NE_CHECK(launch_sumsq(c->G + c->off_E, (long)c->V * c->D, c->gn_part + gn_embed(c), GN_EMBED, c->st));
+  NE_CHECK(launch_sumsq(c->G + c->n_decay, c->n_params - c->n_decay, c->gn_part + gn_gains(c), GN_GAINS, c->st));
+  return launch_fill_f32((float *)(c->gn_part + gn_rows(c)), 0.f, 2L * c->T, c->st);
+}
 
 int validate(const ne_config *c) {
   if (!c) return ne_fail(NE_ERR_ARG, "null config");
@@ -352,7 +369,8 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
   pl.add(&c->tok_in, 4 * T);  // inputs, targets, id chains: filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
-  pl.add(&c->gn_part, (size_t)std::max<long>(gn_slots(c), GN_FULL)); pl.add(&c->gscale, 4); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
+  pl.add(&c->gn_part, (size_t)gn_slots(c)); pl.add(&c->gscale, 4);
+  pl.add(&c->stats_part, 4 * NE_STATS_BLOCKS); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
   c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
@@ -491,7 +509,7 @@ extern "C" int ne_set_tensor(ne_ctx *c, int kind, int id, const float *host, siz
     NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
     c->grads_fresh = false;
   }
-  if (kind == NE_GRAD) c->gn_ready = false;  // the step's sum-of-squares partials no longer hold
+  if (kind == NE_GRAD) c->gn_ready = c->gn_parts_ok = false;  // the sum-of-squares partials no longer hold
   NE_HIP(hipMemcpyAsync(base + c->t_off[id], host, n * 4, hipMemcpyHostToDevice, c->st));
   if (kind == NE_PARAM) NE_CHECK(launch_f32_to_h16(c->dt, c->P + c->t_off[id], c->Pb + c->t_off[id], n, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
@@ -697,7 +715,9 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     }
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));
-    NE_CHECK(wq.sumsq(G + o.wqkv, layer_params(c), gn_layer(c, l), GN_LAYER));
+    NE_CHECK(wq.sumsq(G + o.wqkv, layer_attn_params(c), gn_layer(c, l), GN_LAYER / 2));
+    NE_CHECK(wq.sumsq(G + o.w13, layer_params(c) - layer_attn_params(c), gn_layer(c, l) + GN_LAYER / 2,
+                      GN_LAYER / 2));
     NE_CHECK(wq.flush());  // one hand-over per layer
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, dqkv, QKV, Pb + o.wqkv, D, c->dtmp, &sp_d));
     {
@@ -791,11 +811,13 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // an update still running on st2: the two-stream step waits for it chunk by chunk
   const bool adam_ov = c->adam_pending && two;
   if (!adam_ov) NE_CHECK(adam_join(c));
-  c->gn_ready = false;
+  c->gn_ready = c->gn_parts_ok = false;
+  c->last_u = loss_scale / (float)T / c->gs;  // the factor train_step_enqueue gives the fp32 sinks
   if (c->use_graphs && !profiled && !two) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
   else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two, adam_ov));
   c->adam_pending = false;  // the forward waited for the last chunk before the backward
   c->gn_ready = true;  // the step refreshed every sum-of-squares partial of G
+  c->stats_ok = true;
   if (loss_out) {
     NE_HIP(hipMemcpyAsync(c->h_scalar, c->loss, 4, hipMemcpyDeviceToHost, c->st));
     NE_HIP(hipStreamSynchronize(c->st));
@@ -863,6 +885,7 @@ extern "C" int ne_zero_grads(ne_ctx *c) {
   NE_HIP(hipMemsetAsync(c->ovf, 0, OVF_COUNT * sizeof(int), c->st));
   NE_HIP(hipStreamSynchronize(c->st));
   c->grads_fresh = true;
+  c->gn_parts_ok = false;
   return 0;
 }
 
@@ -883,6 +906,7 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
     NE_HIP(hipStreamSynchronize(c->st));
     c->gs = c->gs * 0.5f;
     c->skipped += 1;
+    c->gn_parts_ok = false;
     c->good_steps = 0;
     if (gnorm_out) *gnorm_out = NAN;
     return 1;
@@ -895,10 +919,12 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
       NE_CHECK(launch_clip_finalize(c->gn_part, (int)gn_slots(c), grad_scale, clip, c->gscale, c->gnorm, c->st));
     } else {
       if (c->grads_fresh) NE_CHECK(launch_fill_f32(c->G, 0.f, c->n_params, c->st));
-      NE_CHECK(launch_sumsq(c->G, c->n_params, c->gn_part, GN_FULL, c->st));
-      NE_CHECK(launch_clip_finalize(c->gn_part, GN_FULL, grad_scale, clip, c->gscale, c->gnorm, c->st));
+      NE_CHECK(gn_sum_all(c));
+      NE_CHECK(launch_clip_finalize(c->gn_part, (int)gn_slots(c), grad_scale, clip, c->gscale, c->gnorm, c->st));
     }
   }
+  c->gn_parts_ok = true;
+  c->gn_gsc = grad_scale;
   c->state.adam_t += 1;
   const int t = c->state.adam_t;
   AdamArgs a = {};
@@ -954,6 +980,49 @@ extern "C" int ne_grad_scale_info(const ne_ctx *c, float *scale, int32_t *skippe
   if (scale) *scale = c->gs;
   if (skipped) *skipped = c->skipped;
   if (sites) *sites = c->last_ovf_sites;
+  return 0;
+}
+
+extern "C" int ne_grad_norm_parts(ne_ctx *c, float *out) {
+  if (!c || !out) return ne_fail(NE_ERR_ARG, "null argument");
+  if (!c->gn_parts_ok) return ne_fail(NE_ERR_STATE, "grad norm parts: no optimizer update since the gradients last changed");
+  std::vector<double> h(gn_slots(c));
+  NE_HIP(hipMemcpyAsync(h.data(), c->gn_part, h.size() * sizeof(double), hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  double attn = 0, ffn = 0, embed = 0, total = 0;
+  for (int l = 0; l < c->L; l++)
+    for (int k = 0; k < GN_LAYER; k++) (k < GN_LAYER / 2 ? attn : ffn) += h[gn_layer(c, l) + k];
+  for (long k = gn_embed(c); k < gn_gains(c); k++) embed += h[k];
+  for (long k = gn_rows(c); k < gn_slots(c); k++) embed += h[k];
+  for (double v : h) total += v;
+  const double sc = c->gn_gsc;
+  out[0] = (float)(sqrt(fmax(total, 0.0)) * sc);
+  out[1] = (float)(sqrt(fmax(attn, 0.0)) * sc);
+  out[2] = (float)(sqrt(fmax(ffn, 0.0)) * sc);
+  out[3] = (float)(sqrt(fmax(embed, 0.0)) * sc);
+  return 0;
+}
+
+extern "C" int ne_step_stats(ne_ctx *c, float *out) {
+  if (!c || !out) return ne_fail(NE_ERR_ARG, "null argument");
+  if (!c->stats_ok) return ne_fail(NE_ERR_STATE, "step stats: no training step has run");
+  const long n = (long)c->T * c->D;
+  NE_CHECK(launch_minmax(c->xL, n, c->stats_part, NE_STATS_BLOCKS, c->st));
+  NE_CHECK(launch_minmax(c->dx, n, c->stats_part + 2 * NE_STATS_BLOCKS, NE_STATS_BLOCKS, c->st));
+  std::vector<float> h(4 * NE_STATS_BLOCKS);
+  NE_HIP(hipMemcpyAsync(h.data(), c->stats_part, h.size() * sizeof(float), hipMemcpyDeviceToHost, c->st));
+  NE_HIP(hipStreamSynchronize(c->st));
+  float v[4] = {INFINITY, -INFINITY, INFINITY, -INFINITY};
+  for (int k = 0; k < 2; k++)
+    for (int b = 0; b < NE_STATS_BLOCKS; b++) {
+      v[2 * k] = fminf(v[2 * k], h[(size_t)(k * NE_STATS_BLOCKS + b) * 2]);
+      v[2 * k + 1] = fmaxf(v[2 * k + 1], h[(size_t)(k * NE_STATS_BLOCKS + b) * 2 + 1]);
+    }
+  // dx holds the gradient at the internal scale; u > 0 maps it to the reference's scale
+  out[0] = v[0];
+  out[1] = v[1];
+  out[2] = v[2] * c->last_u;
+  out[3] = v[3] * c->last_u;
   return 0;
 }
 

@@ -187,3 +187,6 @@ int launch_clip_finalize(const double *partials, int nparts, float grad_scale, f
 int launch_adam(int dt, const AdamArgs &a, hipStream_t s);
 int launch_f32_to_h16(int dt, const float *src, h16_t *dst, long n, hipStream_t s);
 int launch_fill_f32(float *dst, float v, long n, hipStream_t s);
+// Per-block minimum and maximum of a[0, n): out[2*b] = min, out[2*b + 1] = max over the
+// elements of block b (nblocks blocks, grid-strided; a block with no element writes +inf, -inf).
+int launch_minmax(const float *a, long n, float *out, int nblocks, hipStream_t s);

@@ -1,6 +1,6 @@
 /* Qwen3-0.6B at sequence length 512 (TD/models/qwen3_06b_seq512.h of the reference). */
 #pragma once
-#define MODEL_NAME "Qwen3-0.6B"
+#define MODEL_NAME "Qwen3-0.6B-seq512"
 #define DIM 1024
 #define HIDDEN 3072
 #define HEADS 16

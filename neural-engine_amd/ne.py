@@ -28,7 +28,7 @@ EXPORTS = (
     "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
     "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_overlap_weight_grads", "ne_optimizer_step",
     "ne_zero_grads",
-    "ne_grad_scale_info", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
+    "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
@@ -111,6 +111,8 @@ def lib():
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
         "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+        "ne_grad_norm_parts": (I, [P, P]),
+        "ne_step_stats": (I, [P, P]),
         "ne_get_state": (I, [P, C.POINTER(TrainState)]),
         "ne_set_state": (I, [P, C.POINTER(TrainState)]),
         "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
@@ -243,6 +245,18 @@ class Model:
         check(lib().ne_grad_scale_info(self._h, C.byref(sc), C.byref(sk), C.byref(st)), "grad_scale_info")
         names = [n for i, n in enumerate(OVF_SITES) if st.value >> i & 1]
         return float(sc.value), int(sk.value), names
+
+    def grad_norm_parts(self):
+        """(global, attention, FFN, embedding) gradient norms of the last optimizer step."""
+        out = np.zeros(4, np.float32)
+        check(lib().ne_grad_norm_parts(self._h, _ptr(out)), "grad_norm_parts")
+        return tuple(float(v) for v in out)
+
+    def step_stats(self):
+        """(x_min, x_max, dy_min, dy_max) of the last training step (reference scale)."""
+        out = np.zeros(4, np.float32)
+        check(lib().ne_step_stats(self._h, _ptr(out)), "step_stats")
+        return tuple(float(v) for v in out)
 
     def use_graphs(self, on=True):
         check(lib().ne_use_graphs(self._h, int(on)), "use_graphs")

@@ -53,7 +53,10 @@ static int fail(const char *what, int rc) {
 }
 
 /* Uniform +-scale init of TD/train.m:236-251 from srand48(42), in the same draw order
- * (per layer Wq Wk Wv Wo W1 W2 W3, then the embedding), uploaded tensor by tensor. */
+ * (per layer Wq Wk Wv Wo W1 W2 W3, then the embedding), uploaded tensor by tensor.  Each
+ * element is rounded once, as there: the float scale times the double draw is formed in
+ * double, then stored as float (the scale products scale_qd*res_scale and scale_d*res_scale
+ * are float products, evaluated first). */
 static int init_scratch(ne_ctx *ctx) {
   const float scale_d = 1.0f / sqrtf(DIM), scale_qd = 1.0f / sqrtf(Q_DIM), scale_h = 1.0f / sqrtf(HIDDEN);
   const float res_scale = 1.0f / sqrtf(2.0f * NLAYERS);
@@ -66,10 +69,10 @@ static int init_scratch(ne_ctx *ctx) {
   srand48(42);
   for (int L = 0; L < NLAYERS && !rc; L++)
     for (int j = 0; j < 7 && !rc; j++) {
-      for (size_t i = 0; i < sz[j]; i++) buf[i] = sc[j] * (float)(2 * drand48() - 1);
+      for (size_t i = 0; i < sz[j]; i++) buf[i] = (float)(sc[j] * (2 * drand48() - 1));
       rc = ne_set_tensor(ctx, NE_PARAM, 9 * L + j, buf, sz[j]);
     }
-  for (size_t i = 0; i < (size_t)VOCAB * DIM && !rc; i++) buf[i] = 0.02f * (float)(2 * drand48() - 1);
+  for (size_t i = 0; i < (size_t)VOCAB * DIM && !rc; i++) buf[i] = (float)(0.02f * (2 * drand48() - 1));
   if (!rc) rc = ne_set_tensor(ctx, NE_PARAM, 9 * NLAYERS + 1, buf, (size_t)VOCAB * DIM);
   free(buf);
   return rc; /* RMSNorm (and QK-norm) gains start at 1 in a new context */
@@ -244,6 +247,18 @@ int main(int argc, char *argv[]) {
     if (print_now || ckpt_now) last_loss = loss;
     if (!adam_now) ne_sync(ctx);
     double step_ms = now_ms() - t_step;
+    /* TD/train.m:763-778: timing, then the step line with the range of the final hidden state
+     * and of the input gradient, printed before the update (the time excludes it) */
+    if (print_now) {
+      float xs[4] = {0.f, 0.f, 0.f, 0.f};
+      if ((rc = ne_step_stats(ctx, xs))) {
+        fail("ne_step_stats", rc);
+        break;
+      }
+      printf("  timing: step=%.1f (fwd+bwd on GPU)\n", step_ms);
+      printf("step %-4d loss=%.4f  lr=%.2e  %.1fms/step  x[%.2f,%.2f] dy[%.3e,%.3e]\n", step, loss, lr, step_ms,
+             xs[0], xs[1], xs[2], xs[3]);
+    }
 
     if (adam_now) {
       const double t_adam = now_ms();
@@ -268,10 +283,14 @@ int main(int argc, char *argv[]) {
         ne_grad_scale_info(ctx, &gs, NULL, NULL);
         printf("  [adam] step %d skipped: 16-bit gradient overflow, internal scale now %g\n", step, gs);
       } else if ((step + 1) % 10 == 0) {
-        printf("  grad_norm=%.4f\n", gnorm);
+        float gp[4] = {gnorm, 0.f, 0.f, 0.f};
+        if ((rc = ne_grad_norm_parts(ctx, gp))) {
+          fail("ne_grad_norm_parts", rc);
+          break;
+        }
+        printf("  grad_norm=%.4f  attn=%.4f ffn=%.4f embed=%.4f\n", gnorm, gp[1], gp[2], gp[3]);
       }
       const double adam_ms = now_ms() - t_adam;
-      step_ms += adam_ms;
       printf("  [adam] step %d: %.1fms (update+zero)\n", step, adam_ms);
       if (ckpt_now && last_loss < best_loss) {
         best_loss = last_loss;
@@ -295,10 +314,6 @@ int main(int argc, char *argv[]) {
     }
     total_train_ms += step_ms;
     total_steps_done++;
-    if (print_now) {
-      printf("  timing: step=%.1f (fwd+bwd on GPU, one stream)\n", step_ms);
-      printf("step %-4d loss=%.4f  lr=%.2e  %.1fms/step\n", step, loss, lr, step_ms);
-    }
   }
 
   const double wall = now_ms() - t_wall_start;

@@ -51,8 +51,10 @@ def scratch_init(cfg: Config) -> dict:
     shapes = layer_shapes(cfg)
 
     def draw(n, sc):
+        # float scale x double draw, formed in double and rounded once to float
+        # (TD/train.m:246-251: `scale*(2*drand48()-1)` stored into a float array)
         u = np.fromiter((2.0 * r() - 1.0 for _ in range(n)), np.float64, n)
-        return F32(sc) * u.astype(F32)
+        return (np.float64(F32(sc)) * u).astype(F32)
 
     P = {}
     for l in range(L):

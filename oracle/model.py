@@ -465,7 +465,7 @@ def optimizer_step(P, G, M, V, t, lr, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_sc
 
 
 def decode(cfg: Config, P: dict, prompt: np.ndarray, n_new: int, temperature: float = 0.0,
-           top_p: float = 1.0, uniforms=None, return_logits=False):
+           top_p: float = 1.0, uniforms=None, return_logits=False, forced=None):
     """Autoregressive generation.  prompt [B, P0] int.  Returns tokens [B, n_new] int32.
 
     Greedy when temperature < 1e-6 (generate.py:198-199).  Otherwise logits/temp ->
@@ -473,6 +473,11 @@ def decode(cfg: Config, P: dict, prompt: np.ndarray, n_new: int, temperature: fl
     uniforms[b, step] (np.random.choice's own method, generate.py:215).
     Residual scale cfg.res_alpha (1.0 = generate.py literal).  Per-step top-2 logit
     margins are returned when return_logits is set (for near-tie diagnostics).
+
+    forced [B, n_new] (sampling only): the tokens fed back are forced[b, step] instead of the
+    oracle's own picks, and the call returns (picks, dist) where dist[b, step] is how far the
+    uniform lies from the cumulative-probability boundary between the oracle's pick o and
+    forced[b, step] = f (0 when they agree): u - cdf[f] when f < o, cdf[f - 1] - u when f > o.
     """
     B, P0 = prompt.shape
     D, NH, NKV, HD, L = cfg.dim, cfg.n_heads, cfg.kv_heads, cfg.head_dim, cfg.n_layers
@@ -484,6 +489,7 @@ def decode(cfg: Config, P: dict, prompt: np.ndarray, n_new: int, temperature: fl
     out = np.zeros((B, n_new), np.int32)
     margins = []
     logit_rows = []
+    dist = np.zeros((B, n_new)) if forced is not None else None
     cur = prompt[:, 0].copy()
     scale = 1.0 / np.sqrt(HD)
     n_out = 0
@@ -534,14 +540,23 @@ def decode(cfg: Config, P: dict, prompt: np.ndarray, n_new: int, temperature: fl
                         pr = mk / mk.sum()
                     cdf = np.cumsum(pr.astype(np.float64))
                     cdf /= cdf[-1]
-                    nxt[b] = int(np.searchsorted(cdf, uniforms[b, n_out], side="right"))
+                    u = uniforms[b, n_out]
+                    nxt[b] = int(np.searchsorted(cdf, u, side="right"))
+                    if forced is not None:
+                        f = int(forced[b, n_out])
+                        if f < nxt[b]:
+                            dist[b, n_out] = u - cdf[f]
+                        elif f > nxt[b]:
+                            dist[b, n_out] = cdf[f - 1] - u
             if return_logits:
                 srt = np.sort(logits, axis=1)
                 margins.append(srt[:, -1] - srt[:, -2])
                 logit_rows.append(logits.copy())
             out[:, n_out] = nxt
+            cur = (forced[:, n_out] if forced is not None else nxt).astype(np.int32)
             n_out += 1
-            cur = nxt.astype(np.int32)
+    if forced is not None:
+        return out, dist
     if return_logits:
         return out, np.array(margins).T, np.array(logit_rows)
     return out

@@ -72,3 +72,15 @@ FMT = {
     "fp16": (ne.NE_FP16, torch.float16, lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32), 2.0 ** -11),
     "bf16": (ne.NE_BF16, torch.bfloat16, bf16_round, 2.0 ** -8),
 }
+
+
+def as_multiplied(P, dtype):
+    """The weights the device's GEMMs multiply: with bf16 activations the matrices and the
+    embedding are held and multiplied in bf16 (the weight shadow), so an oracle comparison of
+    the bf16 step runs the oracle on those rounded values (the gains stay fp32 on both sides).
+    fp16's rounding of the weights stays well inside the gradient bar, so NE_FP16 compares with
+    the fp32 weights."""
+    from oracle import model as om
+    if dtype == ne.NE_FP16:
+        return P
+    return {k: (v if om.is_gain(k) else om.round_bf16(v)) for k, v in P.items()}

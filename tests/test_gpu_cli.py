@@ -115,6 +115,16 @@ def test_scratch_init_and_dashboard_lines(tmp_path):
     losses = [float(m.group(2)) for m in RE_STEP.finditer(out)]
     assert all(abs(l - np.log(cfg.vocab)) < 0.5 for l in losses)
     assert "[ckpt saved" in out and "=== Efficiency Report ===" in out
+    # the step line's ranges and the grad-norm line's groups (TD/train.m:776, 828)
+    full = re.findall(r"step (\d+)\s+loss=\S+\s+lr=\S+\s+\S+ms/step\s+x\[(\S+),(\S+)\] dy\[(\S+),(\S+)\]", out)
+    assert [int(f[0]) for f in full] == steps
+    for f in full:
+        xmn, xmx, dmn, dmx = map(float, f[1:])
+        assert xmn < 0 < xmx and dmn < 0 < dmx
+    gl = re.findall(r"grad_norm=(\S+)\s+attn=(\S+) ffn=(\S+) embed=(\S+)", out)
+    assert len(gl) == 1
+    tot, att, ffn, emb = map(float, gl[0])
+    assert att > 0 and ffn > 0 and emb > 0 and att ** 2 + ffn ** 2 + emb ** 2 <= tot ** 2 * (1 + 1e-3)
     h, Pg, Mg, Vg = ock.read(ck)
     assert h["step"] == 100 and h["adam_t"] == 1
     want = od.scratch_init(cfg)
@@ -146,3 +156,26 @@ def test_resume_continues_the_run(tmp_path):
     # still holds step 100
     assert hb["step"] == 100
     assert out.count("[adam] step") == 3
+
+
+@pytest.mark.timeout(300)
+def test_seq512_model_header(tmp_path):
+    """The SEQ=512 build of Qwen3-0.6B (TD/models/qwen3_06b_seq512.h): the banner carries the
+    reference's model name, which TR/dashboard.py's RE_MODEL_NAME reads, and seq=512; two
+    steps from --scratch with the classifier over the data's ids run at the loss of an
+    untrained model (about ln of the compact vocabulary)."""
+    exe = os.path.join(ROOT, "neural-engine_amd", "train_qwen3_06b_seq512")
+    data = np.random.default_rng(7).integers(0, 60000, 20000).astype(np.uint16)
+    data.tofile(tmp_path / "d.bin")
+    cv = len(np.unique(data))
+    r = subprocess.run([exe, "--scratch", "--steps", "2", "--accum", "1", "--data", str(tmp_path / "d.bin"),
+                        "--ckpt", str(tmp_path / "c.bin")], cwd=tmp_path, capture_output=True, text=True,
+                       timeout=280)
+    print(r.stdout[-2000:], flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    m = re.search(r"ANE Dynamic Training: (.+?) \((\d+) layers", r.stdout)  # TR/dashboard.py RE_MODEL_NAME
+    assert m and m.group(1) == "Qwen3-0.6B-seq512" and m.group(2) == "28"
+    assert re.search(r"hd=128 hidden=3072 seq=512 vocab=151936", r.stdout)
+    assert f"{cv} active tokens" in r.stdout
+    loss = [float(x.group(2)) for x in RE_STEP.finditer(r.stdout)]
+    assert len(loss) == 1 and abs(loss[0] - np.log(cv)) < 1.0, loss

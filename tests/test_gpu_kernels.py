@@ -306,6 +306,49 @@ def test_flash_attention_fwd_bwd(fmt, B, S, NH, NKV, HD):
     assert np.abs(host(dqkv)[:, :NH * HD + NKV * HD]).max() == 0
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("fmt", FMTS)
+def test_flash_attention_at_scale(fmt):
+    """The at-scale shape, B=8 x S=2048 with Qwen3-0.6B's 16 query / 8 KV heads of 128: the
+    whole batch runs (the XCD block order covers the full grid); the float64 reference is
+    computed for sequences 0 and 7 and KV heads 0 and 7 with their query heads."""
+    dt, tdt, rnd, u = FMT[fmt]
+    B, S, NH, NKV, HD = 8, 2048, 16, 8, 128
+    T = B * S
+    rng = np.random.default_rng(2048)
+    q = rnd(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    k = rnd(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    v = rnd(rng.standard_normal((B, S, NKV, HD)).astype(np.float32))
+    do = rnd(rng.standard_normal((B, S, NH, HD)).astype(np.float32))
+    scale = 1.0 / math.sqrt(HD)
+    qd, kd, vd = dev(q.reshape(T, -1), tdt), dev(k.reshape(T, -1), tdt), dev(v.reshape(T, -1), tdt)
+    o, lse = zeros((T, NH * HD), tdt), zeros((T, NH))
+    call(L.ne_k_attn_fwd, dt, ptr(qd), NH * HD, ptr(kd), NKV * HD, ptr(vd), NKV * HD, ptr(o), NH * HD, ptr(lse), B, S,
+         NH, NKV, HD, scale, None)
+    delta, dq, dk = zeros((T, NH)), zeros((T, NH * HD)), zeros((T, NKV * HD))
+    dv = zeros((T, NKV * HD), tdt)
+    call(L.ne_k_attn_bwd, dt, ptr(qd), NH * HD, ptr(kd), NKV * HD, ptr(vd), NKV * HD, ptr(o), NH * HD, ptr(lse),
+         ptr(dev(do.reshape(T, -1), tdt)), NH * HD, ptr(delta), ptr(dq), NH * HD, ptr(dk), NKV * HD, ptr(dv),
+         NKV * HD, B, S, NH, NKV, HD, scale, None)
+    o_g = host(o).reshape(B, S, NH, HD)
+    lse_g = host(lse).reshape(B, S, NH)
+    dq_g = host(dq).reshape(B, S, NH, HD)
+    dk_g = host(dk).reshape(B, S, NKV, HD)
+    dv_g = host(dv).reshape(B, S, NKV, HD)
+    worst = 0.0
+    for b in (0, 7):
+        for kvh in (0, 7):
+            hs = slice(2 * kvh, 2 * kvh + 2)
+            o_r, lse_r, dq_r, dk_r, dv_r = _attn_ref(q[b:b + 1, :, hs], k[b:b + 1, :, kvh:kvh + 1],
+                                                     v[b:b + 1, :, kvh:kvh + 1], do[b:b + 1, :, hs], 2, 1, scale)
+            np.testing.assert_allclose(lse_g[b, :, hs], lse_r[0], rtol=1e-4, atol=1e-4)
+            e = (rel_l2(o_g[b, :, hs], o_r[0]), rel_l2(dq_g[b, :, hs], dq_r[0]),
+                 rel_l2(dk_g[b, :, kvh], dk_r[0, :, 0]), rel_l2(dv_g[b, :, kvh], dv_r[0, :, 0]))
+            worst = max(worst, max(e))
+            assert max(e) < 4 * u, (b, kvh, e)
+    print(f"\n  {fmt} B=8 S=2048 worst rel-L2 {worst:.2e}")
+
+
 # --------------------------------------------------------------- cross-entropy (LM head)
 
 @pytest.mark.parametrize("fmt", FMTS)

@@ -3,13 +3,14 @@ checkpoints) against the numpy oracle, at small shapes the oracle runs in second
 import numpy as np
 import pytest
 
-from gpu_util import need_gpu, rel_l2
+from gpu_util import as_multiplied, need_gpu, rel_l2
 import ne
 from oracle import ckpt, model as om
 
 pytestmark = pytest.mark.gpu
 
-# Tolerances of the step (fp32 master weights, bf16 activations/operands, fp32 accumulation)
+# Tolerances of the step (fp32 master weights and accumulation, 16-bit activations and GEMM
+# operands: fp16 by default, bf16 compared with the oracle on the bf16-rounded matrices)
 LOSS_RTOL = 1e-3
 GRAD_RL2 = 1e-2
 ADAM_RTOL = 1e-5
@@ -30,23 +31,25 @@ def shapes(cfg):
     return dict(om.tensor_list(cfg))
 
 
-def run_step(cfg, P, tok, loss_scale=256.0):
-    m = ne.Model.from_oracle(cfg, batch=tok.shape[0])
+def run_step(cfg, P, tok, loss_scale=256.0, dtype=ne.NE_FP16):
+    m = ne.Model.from_oracle(cfg, batch=tok.shape[0], dtype=dtype)
     m.set_params(P)
     loss = m.train_step(tok, loss_scale)
     G = m.get_all(shapes(cfg), ne.NE_GRAD)
     return m, loss, G
 
 
+@pytest.mark.parametrize("dtype", [ne.NE_FP16, ne.NE_BF16])
 @pytest.mark.parametrize("case", list(CASES))
-def test_train_step_matches_oracle(case):
+def test_train_step_matches_oracle(case, dtype):
     cfg = om.tiny(**CASES[case])
     P = om.init_params(cfg, seed=0, std=0.02)
     tok = om.tokens_for_step(cfg, 2, cfg.seq, seed=1)
-    print(f"\n[case {case}] tiny model B=2 S={cfg.seq}", flush=True)
-    m, loss, G = run_step(cfg, P, tok)
-    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
-    Go = om.backward(cfg, P, cache)
+    print(f"\n[case {case} dtype {dtype}] tiny model B=2 S={cfg.seq}", flush=True)
+    m, loss, G = run_step(cfg, P, tok, dtype=dtype)
+    Pm = as_multiplied(P, dtype)
+    lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0)
+    Go = om.backward(cfg, Pm, cache)
     assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
     errs = sorted(((rel_l2(G[n], Go[n]), n) for n in P), reverse=True)
     print(f"  loss gpu={loss:.6f} oracle={lo:.6f}; worst grad rel-L2: "
@@ -348,9 +351,8 @@ def _compact_case(vocab=1024, seed=5):
 def test_compact_vocab_step_matches_oracle(dtype):
     """Vocabulary compaction (TD/cpu_ops.h:384-431): classifier and softmax over the ids of
     the data (115 of 1024, padded to 128 columns), compact gradient added back to its rows;
-    two accumulated micro-steps, then back to the full vocabulary.  Gradients are checked in
-    the training format (fp16); with bf16 activations the loss is checked (bf16's 8-bit
-    mantissa puts the small QK-norm gain reductions at the 1e-2 bar by itself)."""
+    two accumulated micro-steps, then back to the full vocabulary.  The bf16 step is compared
+    with the oracle on the bf16-rounded matrices it multiplies."""
     cfg, data, ids, tok = _compact_case()
     P = om.init_params(cfg, seed=0, std=0.02)
     m = ne.Model.from_oracle(cfg, batch=2, dtype=dtype)
@@ -360,13 +362,14 @@ def test_compact_vocab_step_matches_oracle(dtype):
     loss = m.train_step(tok, 256.0)
     loss2 = m.train_step(tok2, 256.0)
     G = m.get_all(shapes(cfg), ne.NE_GRAD)
-    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
-    Go = om.backward(cfg, P, cache)
-    lo2, cache2 = om.forward(cfg, P, tok2, loss_scale=256.0, vocab_ids=ids)
-    Go2 = om.backward(cfg, P, cache2)
+    Pm = as_multiplied(P, dtype)
+    lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0, vocab_ids=ids)
+    Go = om.backward(cfg, Pm, cache)
+    lo2, cache2 = om.forward(cfg, Pm, tok2, loss_scale=256.0, vocab_ids=ids)
+    Go2 = om.backward(cfg, Pm, cache2)
     print(f"\n  compact loss gpu={loss:.6f}/{loss2:.6f} oracle={lo:.6f}/{lo2:.6f} (ln CV = {np.log(len(ids)):.4f})")
     assert abs(loss - lo) <= LOSS_RTOL * abs(lo) and abs(loss2 - lo2) <= LOSS_RTOL * abs(lo2)
-    for n in P if dtype == ne.NE_FP16 else ("embed", "rms_final"):
+    for n in P:
         assert rel_l2(G[n], Go[n] + Go2[n]) <= GRAD_RL2, (n, rel_l2(G[n], Go[n] + Go2[n]))
     unused = np.setdiff1d(np.arange(cfg.vocab), ids)
     assert np.abs(G["embed"].reshape(cfg.vocab, -1)[unused]).max() == 0
@@ -376,7 +379,7 @@ def test_compact_vocab_step_matches_oracle(dtype):
     m.zero_grads()
     m.set_vocab_map(None)
     loss_f = m.train_step(tok, 256.0)
-    lf, _ = om.forward(cfg, P, tok, loss_scale=256.0, want_grad_cache=False)
+    lf, _ = om.forward(cfg, Pm, tok, loss_scale=256.0, want_grad_cache=False)
     assert abs(loss_f - lf) <= LOSS_RTOL * abs(lf)
     m.close()
 
@@ -393,4 +396,52 @@ def test_compact_vocab_rejects_bad_maps_and_targets():
     bad[0, 5] = ids[0]                                       # a target outside the map
     with pytest.raises(ne.NEError):
         m.train_step(bad, 256.0)
+    m.close()
+
+
+def test_step_stats_and_grad_norm_parts():
+    """The step line's ranges (TD/train.m:770-777): x = the last layer's output, dy = the
+    gradient of loss * loss_scale with respect to the first layer's input, in the reference's
+    scale; with every input token distinct, dy's rows are the embedding-gradient rows of those
+    tokens in the oracle.  The grad-norm line's groups (TD/train.m:786-830) equal the float64
+    norms of the gradients read back, scaled by grad_scale."""
+    cfg = om.tiny(**CASES["qwen3"])
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = np.random.default_rng(4).permutation(cfg.vocab)[: 2 * (cfg.seq + 1)].reshape(2, cfg.seq + 1)
+    tok = tok.astype(np.int32)
+    m = ne.Model.from_oracle(cfg, batch=2)
+    m.set_params(P)
+    with pytest.raises(ne.NEError):
+        m.step_stats()          # no step yet
+    m.train_step(tok, 256.0)
+    xmn, xmx, dmn, dmx = m.step_stats()
+    lo, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    Go = om.backward(cfg, P, cache)
+    xL = cache["xL"]
+    dy = Go["embed"][tok[:, :-1].ravel()]
+    print(f"\n  x [{xmn:.4f}, {xmx:.4f}] oracle [{xL.min():.4f}, {xL.max():.4f}]; "
+          f"dy [{dmn:.3e}, {dmx:.3e}] oracle [{dy.min():.3e}, {dy.max():.3e}]")
+    assert abs(xmn - xL.min()) <= 1e-3 * np.abs(xL).max() and abs(xmx - xL.max()) <= 1e-3 * np.abs(xL).max()
+    assert abs(dmn - dy.min()) <= 2e-2 * np.abs(dy).max() and abs(dmx - dy.max()) <= 2e-2 * np.abs(dy).max()
+    sh = shapes(cfg)
+    G = m.get_all(sh, ne.NE_GRAD)
+    with pytest.raises(ne.NEError):
+        m.grad_norm_parts()     # no update yet
+    gn = m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=1.0)
+    tot, att, ffn, emb = m.grad_norm_parts()
+
+    def norm(names):
+        return float(np.sqrt(sum(np.sum(G[n].astype(np.float64) ** 2) for n in names))) / 256
+
+    layer = [n for n in G if n.startswith("layers.")]
+    want_att = norm([n for n in layer if n.split(".")[-1] in ("Wq", "Wk", "Wv", "Wo")])
+    want_ffn = norm([n for n in layer if n.split(".")[-1] in ("W1", "W2", "W3")])
+    print(f"  norms {tot:.6f} {att:.6f} {ffn:.6f} {emb:.6f}; float64 {norm(G):.6f} {want_att:.6f} "
+          f"{want_ffn:.6f} {norm(['embed']):.6f}")
+    assert abs(tot - gn) <= 1e-6 * gn and abs(tot - norm(G)) <= 1e-5 * norm(G)
+    assert abs(att - want_att) <= 1e-5 * want_att and abs(ffn - want_ffn) <= 1e-5 * want_ffn
+    assert abs(emb - norm(["embed"])) <= 1e-5 * norm(["embed"])
+    m.train_step(tok, 256.0)
+    with pytest.raises(ne.NEError):
+        m.grad_norm_parts()     # the gradients changed since
     m.close()

@@ -74,6 +74,62 @@ def test_adam_closed_form_t1():
     np.testing.assert_allclose(w, expect, rtol=1e-5, atol=1e-9)
 
 
+@pytest.mark.parametrize("grad_scale,clip", [(1.0, 0.0), (1 / 256, 0.0), (1.0, 1e-3)])
+def test_optimizer_step_constant_gradient_closed_form(grad_scale, clip):
+    """AdamW of TD/cpu_ops.h:266-303 over several steps with the wd rules of
+    TD/train.m:861-897.  With the same gradient g every step, the bias-corrected moments are
+    exactly m^ = g and v^ = g^2 at every t (m_t = (1 - b1^t) g, v_t = (1 - b2^t) g^2), so each
+    step moves w by -lr * (g/(|g| + eps) + wd * w): after n steps
+    w_n = k^n w_0 - lr * s * (1 - k^n) / (1 - k), k = 1 - lr * wd, s = g/(|g| + eps), and
+    wd = 0 for the norm gains (w_n = w_0 - n * lr * s).  A wrong bias-correction exponent,
+    weight decay applied to a gain or left off a matrix, or the clip factor applied to only
+    part of the gradients each break it.  The clip scales g by clip/||g|| (s is
+    scale-invariant up to eps, which the small gradients here make matter)."""
+    rng = np.random.default_rng(7)
+    P0 = {"layers.0.Wq": (rng.standard_normal(300) * 0.02).astype(np.float32),
+          "layers.0.rms_att": (1 + rng.standard_normal(40) * 0.1).astype(np.float32),
+          "embed": (rng.standard_normal(200) * 0.02).astype(np.float32)}
+    G0 = {k: (rng.standard_normal(v.shape) * 1e-6 / grad_scale).astype(np.float32) for k, v in P0.items()}
+    lr, b1, b2, eps, wd, n = 3e-4, 0.9, 0.95, 1e-8, 0.1, 6
+    P = {k: v.copy() for k, v in P0.items()}
+    M = {k: np.zeros_like(v) for k, v in P0.items()}
+    V = {k: np.zeros_like(v) for k, v in P0.items()}
+    norm = math.sqrt(sum(float(np.sum((g.astype(np.float64) * grad_scale) ** 2)) for g in G0.values()))
+    cs = clip / norm if (clip > 0 and norm > clip) else 1.0
+    for t in range(1, n + 1):
+        gn = om.optimizer_step(P, {k: v.copy() for k, v in G0.items()}, M, V, t, lr, b1, b2, eps, wd,
+                               grad_scale=grad_scale, clip=clip)
+        assert gn == pytest.approx(norm, rel=1e-6)
+    for k in P0:
+        g = G0[k].astype(np.float64) * grad_scale * cs
+        s = g / (np.abs(g) + eps)
+        w0 = P0[k].astype(np.float64)
+        if om.is_gain(k):
+            want = w0 - n * lr * s
+        else:
+            kk = 1 - lr * wd
+            want = kk ** n * w0 - lr * s * (1 - kk ** n) / (1 - kk)
+        # one fp32 rounding of w per step: n ulps of the largest element
+        np.testing.assert_allclose(P[k], want, rtol=0, atol=n * 2.0 ** -23 * np.abs(w0).max(), err_msg=k)
+        # the moments themselves: m_t = (1 - b1^t) g, v_t = (1 - b2^t) g^2
+        np.testing.assert_allclose(M[k], (1 - b1 ** n) * g, rtol=2e-6, atol=1e-30, err_msg=k)
+        np.testing.assert_allclose(V[k], (1 - b2 ** n) * g * g, rtol=2e-6, atol=1e-37, err_msg=k)
+
+
+def test_optimizer_step_decay_only_on_matrices():
+    """A zero gradient isolates weight decay: the matrices and the embedding shrink by
+    exactly lr*wd*w (m = v = 0 gives a zero Adam direction), the gains stay put."""
+    P = {"layers.0.W2": np.full(8, 0.5, np.float32), "rms_final": np.full(8, 1.5, np.float32),
+         "layers.0.q_norm": np.full(8, 2.0, np.float32), "embed": np.full(8, -0.25, np.float32)}
+    G = {k: np.zeros_like(v) for k, v in P.items()}
+    M = {k: np.zeros_like(v) for k, v in P.items()}
+    V = {k: np.zeros_like(v) for k, v in P.items()}
+    om.optimizer_step(P, G, M, V, 3, 1e-2, wd=0.1, clip=1.0)
+    assert np.all(P["layers.0.W2"] == np.float32(0.5 - 1e-2 * 0.1 * 0.5))
+    assert np.all(P["embed"] == np.float32(-0.25 + 1e-2 * 0.1 * 0.25))
+    assert np.all(P["rms_final"] == 1.5) and np.all(P["layers.0.q_norm"] == 2.0)
+
+
 def test_lr_schedule_and_clip_closed_form():
     assert om.lr_at(0, 3e-4, 100, 1000) == pytest.approx(3e-6, rel=1e-6)
     assert om.lr_at(99, 3e-4, 100, 1000) == pytest.approx(3e-4, rel=1e-6)
