@@ -248,6 +248,17 @@ int ne_k_attn_bwd(int dtype, const void *q, int64_t ldq, const void *k, int64_t 
                   const void *dout, int64_t lddo, float *delta, float *dq, int64_t lddq,
                   float *dk, int64_t lddk, void *dv, int64_t lddv, int B, int S, int NH, int NKV,
                   int HD, float scale, void *stream);
+/* ne_k_attn_bwd without the delta argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops): it allocates nothing on any call.  No
+ * counterpart in the reference.  Its delta scratch [B*S, NH] lives in a fixed device array
+ * of 2^20 floats (4 MiB per GPU, held until the process ends): B*S*NH above 2^20 is rejected
+ * with NE_ERR_ARG.  Every call on a GPU shares that GPU's array, so calls that overlap on one
+ * GPU (other streams, other threads) race; calls ordered on one stream do not. */
+int ne_k_attn_bwd_noalloc(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
+                          const void *v, int64_t ldv, const void *o, int64_t ldo, const float *lse,
+                          const void *dout, int64_t lddo, float *dq, int64_t lddq, float *dk,
+                          int64_t lddk, void *dv, int64_t lddv, int B, int S, int NH, int NKV,
+                          int HD, float scale, void *stream);
 /* Fused LM-head + softmax cross-entropy (TD/train.m:493-524, TD/cpu_ops.h:348-382):
  * logits = x[T,D] . E[V,D]^T are produced tile by tile and never stored.  Forward writes
  * lse[T] and loss[0] = mean(-log(p_tgt + 1e-10)); part is scratch [T, V/64*2] floats

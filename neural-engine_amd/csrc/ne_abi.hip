@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/ne.h"
 #include "ne_internal.h"
 
@@ -97,6 +99,55 @@ extern "C" int ne_k_attn_bwd(int dtype, const void *q, int64_t ldq, const void *
                              void *dv, int64_t lddv, int B, int S, int NH, int NKV, int HD, float scale,
                              void *stream) {
   CHECK_DT(dtype);
+  AttnArgs a = attn_args(q, ldq, k, ldk, v, ldv, B, S, NH, NKV, HD, scale);
+  a.o = (h16_t *)o; a.ldo = ldo; a.lse = (float *)lse;
+  a.dout = (const h16_t *)dout; a.lddo = lddo; a.delta = delta;
+  a.dq = dq; a.lddq = lddq; a.dk = dk; a.lddk = lddk; a.dv = (h16_t *)dv; a.lddv = lddv;
+  return launch_attn_bwd(dtype, a, S(stream));
+}
+
+// ---- ne_k_attn_bwd_noalloc: the attention backward with its delta scratch in a fixed
+// device array instead of a caller buffer (no allocation on any call) ----
+
+// delta [B*S, NH] of the backward (rowsum(dO * O)); each GPU holds its own copy, kept until
+// the process ends
+constexpr long NE_ATTN_SCRATCH_FLOATS = 1L << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[NE_ATTN_SCRATCH_FLOATS];
+
+// The device address of `scratch` on each GPU, looked up once per device on the first call
+// there (in host code the array's name is not a device address).
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[64];
+
+static int scratch_ptr(float **out) {
+  int dev = 0;
+  NE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return ne_fail(NE_ERR_ARG, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    NE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = (float *)g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int ne_k_attn_bwd_noalloc(int dtype, const void *q, int64_t ldq, const void *k, int64_t ldk,
+                                     const void *v, int64_t ldv, const void *o, int64_t ldo, const float *lse,
+                                     const void *dout, int64_t lddo, float *dq, int64_t lddq, float *dk,
+                                     int64_t lddk, void *dv, int64_t lddv, int B, int S, int NH, int NKV, int HD,
+                                     float scale, void *stream) {
+  CHECK_DT(dtype);
+  if (B <= 0 || S <= 0 || NH <= 0)
+    return ne_fail(NE_ERR_ARG, "attn_bwd_noalloc: B=%d S=%d NH=%d must be positive", B, S, NH);
+  if ((long)B * S * NH > NE_ATTN_SCRATCH_FLOATS)
+    return ne_fail(NE_ERR_ARG, "attn_bwd_noalloc: B*S*NH = %ld exceeds the fixed scratch of %ld rows x heads",
+                   (long)B * S * NH, NE_ATTN_SCRATCH_FLOATS);
+  float *delta = nullptr;
+  NE_CHECK(scratch_ptr(&delta));
+  // the delta kernel writes every element of delta before the backward reads it: nothing in
+  // the scratch needs clearing between calls
   AttnArgs a = attn_args(q, ldq, k, ldk, v, ldv, B, S, NH, NKV, HD, scale);
   a.o = (h16_t *)o; a.ldo = ldo; a.lse = (float *)lse;
   a.dout = (const h16_t *)dout; a.lddo = lddo; a.delta = delta;

@@ -31,7 +31,7 @@ EXPORTS = (
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
-    "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd",
+    "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
     "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
 )
@@ -129,6 +129,7 @@ def lib():
         "ne_k_qk_prep_bwd": (I, [I, P, P, P, L, P, P, P, P, P, P, P, P, P, F, I, I, I, I, I, P]),
         "ne_k_attn_fwd": (I, [I, P, L, P, L, P, L, P, L, P, I, I, I, I, I, F, P]),
         "ne_k_attn_bwd": (I, [I, P, L, P, L, P, L, P, L, P, P, L, P, P, L, P, L, P, L, I, I, I, I, I, F, P]),
+        "ne_k_attn_bwd_noalloc": (I, [I, P, L, P, L, P, L, P, L, P, P, L, P, L, P, L, P, L, I, I, I, I, I, F, P]),
         "ne_k_ce_fwd": (I, [I, P, P, P, I, I, I, P, P, P, P, P, P]),
         "ne_k_ce_bwd": (I, [I, P, P, P, P, I, I, I, F, P, P]),
         "ne_k_adam": (I, [I, P, P, P, P, P, L, L, F, F, F, F, F, I, P, I, P]),

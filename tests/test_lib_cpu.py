@@ -59,3 +59,15 @@ def test_kernel_entry_points_validate_shapes_before_launch():
 def test_tensor_names_match_oracle_order(qk):
     cfg = om.tiny(qk_norm=qk)
     assert ne.tensor_names(cfg.n_layers, qk) == [n for n, _ in om.tensor_list(cfg)]
+
+
+def test_attn_bwd_noalloc_rejects_oversized_inputs_without_device():
+    """The allocation-free attention backward checks its fixed scratch bound (B*S*NH <= 2^20)
+    before touching a device."""
+    L = ne.lib()
+    rc = L.ne_k_attn_bwd_noalloc(ne.NE_FP16, None, 0, None, 0, None, 0, None, 0, None, None, 0, None, 0, None, 0,
+                                 None, 0, 64, 2048, 16, 8, 128, 1.0, None)
+    assert rc == -1 and b"exceeds the fixed scratch" in L.ne_last_error()
+    rc = L.ne_k_attn_bwd_noalloc(ne.NE_FP16, None, 0, None, 0, None, 0, None, 0, None, None, 0, None, 0, None, 0,
+                                 None, 0, 0, 2048, 16, 8, 128, 1.0, None)
+    assert rc == -1 and b"must be positive" in L.ne_last_error()
