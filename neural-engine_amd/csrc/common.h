@@ -105,3 +105,22 @@ __device__ __forceinline__ float quad16_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
 }
+
+// One element of AdamW (TD/cpu_ops.h:266-303) with bias-corrected moments, every product and
+// sum written out (explicit fmaf, no contraction left to the compiler): the result does not
+// depend on how a kernel that inlines it is scheduled.
+struct AdamConst {
+  float gs, b1, b2, ob1, ob2, ibc1, ibc2, lr, eps;
+  __device__ __forceinline__ AdamConst(const float *gscale, float b1_, float b2_, float bc1, float bc2, float lr_,
+                                       float eps_)
+      : gs(gscale[0]), b1(b1_), b2(b2_), ob1(1.f - b1_), ob2(1.f - b2_), ibc1(1.f / bc1), ibc2(1.f / bc2),
+        lr(lr_), eps(eps_) {}
+};
+__device__ __forceinline__ void adam_elem(const AdamConst &k, float &p, float g, float &m, float &v, float wd) {
+  const float gg = g * k.gs;
+  m = fmaf(k.b1, m, k.ob1 * gg);
+  v = fmaf(k.b2, v, k.ob2 * (gg * gg));
+  const float mh = m * k.ibc1, vh = v * k.ibc2;
+  const float u = mh / (sqrtf(vh) + k.eps);
+  p = fmaf(-k.lr, fmaf(wd, p, u), p);
+}

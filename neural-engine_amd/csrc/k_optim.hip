@@ -11,22 +11,37 @@
 
 namespace {
 
-__global__ __launch_bounds__(256) void sumsq_kernel(const float *__restrict__ g, long n,
-                                                    double *__restrict__ partials) {
+// Sum of squares of g[0, n) over nb blocks (block b of them is `b`): partials[b].
+__device__ __forceinline__ void sumsq_block(const float *__restrict__ g, long n, int b, int nb,
+                                            double *__restrict__ partials) {
   __shared__ float red[4];
   const long n4 = n / 4;
   float acc = 0.f;
   const float4 *g4 = (const float4 *)g;
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+  for (long i = b * 256L + threadIdx.x; i < n4; i += (long)nb * 256) {
     const float4 v = g4[i];
     acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
-  if (blockIdx.x == 0)
+  if (b == 0)
     for (long i = n4 * 4 + threadIdx.x; i < n; i += 256) acc += g[i] * g[i];
   acc = wave_sum(acc);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) partials[blockIdx.x] = (double)red[0] + red[1] + red[2] + red[3];
+  if (threadIdx.x == 0) partials[b] = (double)red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void sumsq_kernel(const float *__restrict__ g, long n,
+                                                    double *__restrict__ partials) {
+  sumsq_block(g, n, blockIdx.x, gridDim.x, partials);
+}
+
+// Two ranges in one launch: the first half of the blocks sums g1 into partials[0, half), the
+// second g2 into partials[half, 2 half).
+__global__ __launch_bounds__(256) void sumsq2_kernel(const float *__restrict__ g1, long n1, const float *__restrict__ g2,
+                                                     long n2, double *__restrict__ partials) {
+  const int half = gridDim.x / 2;
+  if ((int)blockIdx.x < half) sumsq_block(g1, n1, blockIdx.x, half, partials);
+  else sumsq_block(g2, n2, blockIdx.x - half, half, partials + half);
 }
 
 // norm = grad_scale * sqrt(sum partials); factor = grad_scale * (clip / norm if norm > clip).
@@ -56,10 +71,8 @@ __global__ __launch_bounds__(256) void clip_finalize_kernel(const double *__rest
 // byte is touched once): measured at the streaming-copy ceiling of the device.
 template <typename HT, bool SHADOW>
 __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
-  const float gs = a.gscale[0];
+  const AdamConst k(a.gscale, a.b1, a.b2, a.bc1, a.bc2, a.lr, a.eps);
   const bool skip = a.skip && a.skip[0];
-  const float ob1 = 1.f - a.b1, ob2 = 1.f - a.b2;
-  const float ibc1 = 1.f / a.bc1, ibc2 = 1.f / a.bc2;
   const long n4 = a.n / 4;
   const long stride = (long)gridDim.x * 256;
   f32x4 *p4 = (f32x4 *)a.p, *g4 = (f32x4 *)a.g, *m4 = (f32x4 *)a.m, *v4 = (f32x4 *)a.v;
@@ -89,12 +102,10 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
       u16x4 b;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float gg = G[u][j] * gs;
-        M[u][j] = a.b1 * M[u][j] + ob1 * gg;
-        V[u][j] = a.b2 * V[u][j] + ob2 * (gg * gg);
-        const float mh = M[u][j] * ibc1, vh = V[u][j] * ibc2;
-        P[u][j] -= a.lr * (mh / (sqrtf(vh) + a.eps) + wd * P[u][j]);
-        b[j] = HT::h(P[u][j]);
+        float pj = P[u][j], mj = M[u][j], vj = V[u][j];
+        adam_elem(k, pj, G[u][j], mj, vj, wd);
+        P[u][j] = pj; M[u][j] = mj; V[u][j] = vj;
+        b[j] = HT::h(pj);
       }
       __builtin_nontemporal_store(P[u], p4 + i);
       __builtin_nontemporal_store(M[u], m4 + i);
@@ -145,6 +156,12 @@ int grid_for(long n) { return (int)std::max<long>(1, std::min<long>((n + 255) / 
 int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s) {
   hipLaunchKernelGGL(sumsq_kernel, dim3(nparts), dim3(256), 0, s, g, n, partials);
   return ne_hip_status(hipGetLastError(), "sumsq");
+}
+
+int launch_sumsq2(const float *g1, long n1, const float *g2, long n2, double *partials, int nparts_each,
+                  hipStream_t s) {
+  hipLaunchKernelGGL(sumsq2_kernel, dim3(2 * nparts_each), dim3(256), 0, s, g1, n1, g2, n2, partials);
+  return ne_hip_status(hipGetLastError(), "sumsq2");
 }
 
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,

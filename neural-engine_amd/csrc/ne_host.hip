@@ -152,11 +152,13 @@ struct WgradQueue {
     int fam, epi, M, N, K;
     const h16_t *dY; long ldy; const h16_t *X; long ldx; float *C; float u;
     long n; int nparts; double *part;  // M == 0: sum of squares of C[0, n) into part[0, nparts)
+    const float *C2; long n2;          // and, if C2, of C2[0, n2) into part[nparts, 2 nparts)
   };
   ne_ctx *c;
   bool on;
   std::vector<Job> jobs;
   int run(const Job &j, bool side) {
+    if (j.M == 0 && j.C2) return launch_sumsq2(j.C, j.n, j.C2, j.n2, j.part, j.nparts, side ? c->st2 : c->st);
     if (j.M == 0) return launch_sumsq(j.C, j.n, j.part, j.nparts, side ? c->st2 : c->st);
     return gemm_dw(c, side, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u);
   }
@@ -167,10 +169,10 @@ struct WgradQueue {
   }
   int add(int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X, long ldx, float *C,
           float u) {
-    return push({fam, epi, M, N, K, dY, ldy, X, ldx, C, u, 0, 0, nullptr});
+    return push({fam, epi, M, N, K, dY, ldy, X, ldx, C, u, 0, 0, nullptr, nullptr, 0});
   }
-  int sumsq(const float *g, long n, long slot, int nparts) {
-    return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, n, nparts, c->gn_part + slot});
+  int sumsq(const float *g, long n, long slot, int nparts, const float *g2 = nullptr, long n2 = 0) {
+    return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, n, nparts, c->gn_part + slot, g2, n2});
   }
   int flush() {
     if (!on || jobs.empty()) return 0;
@@ -226,7 +228,7 @@ float *qk_part(ne_ctx *c, int l) { return c->gpart + (long)(2 * c->L + 1) * c->r
 // gradients (its attention block Wqkv, Wo from lo[l].wqkv, then its FFN block W13, W2 from
 // lo[l].w13: GN_LAYER / 2 slots each), the embedding, the gains, then one slot per token row
 // for the change the embedding scatter makes to the row it updates.
-constexpr int GN_LAYER = 128, GN_EMBED = 512, GN_GAINS = 16;
+constexpr int GN_LAYER = 256, GN_EMBED = 512, GN_GAINS = 16;
 long gn_layer(const ne_ctx *c, int l) { (void)c; return (long)l * GN_LAYER; }
 long gn_embed(const ne_ctx *c) { return (long)c->L * GN_LAYER; }
 long gn_gains(const ne_ctx *c) { return gn_embed(c) + GN_EMBED; }
@@ -241,9 +243,8 @@ long layer_attn_params(const ne_ctx *c) { return (long)(c->QKV + c->Q) * c->D; }
 int gn_sum_all(ne_ctx *c) {
   for (int l = 0; l < c->L; l++) {
     const LayerOff &o = c->lo[l];
-    NE_CHECK(launch_sumsq(c->G + o.wqkv, layer_attn_params(c), c->gn_part + gn_layer(c, l), GN_LAYER / 2, c->st));
-    NE_CHECK(launch_sumsq(c->G + o.w13, layer_params(c) - layer_attn_params(c), c->gn_part + gn_layer(c, l) + GN_LAYER / 2,
-                          GN_LAYER / 2, c->st));
+    NE_CHECK(launch_sumsq2(c->G + o.wqkv, layer_attn_params(c), c->G + o.w13, layer_params(c) - layer_attn_params(c),
+                           c->gn_part + gn_layer(c, l), GN_LAYER / 2, c->st));
   }
   NE_CHECK(launch_sumsq(c->G + c->off_E, (long)c->V * c->D, c->gn_part + gn_embed(c), GN_EMBED, c->st));
   NE_CHECK(launch_sumsq(c->G + c->n_decay, c->n_params - c->n_decay, c->gn_part + gn_gains(c), GN_GAINS, c->st));
@@ -715,9 +716,8 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     }
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));
-    NE_CHECK(wq.sumsq(G + o.wqkv, layer_attn_params(c), gn_layer(c, l), GN_LAYER / 2));
-    NE_CHECK(wq.sumsq(G + o.w13, layer_params(c) - layer_attn_params(c), gn_layer(c, l) + GN_LAYER / 2,
-                      GN_LAYER / 2));
+    NE_CHECK(wq.sumsq(G + o.wqkv, layer_attn_params(c), gn_layer(c, l), GN_LAYER / 2, G + o.w13,
+                      layer_params(c) - layer_attn_params(c)));
     NE_CHECK(wq.flush());  // one hand-over per layer
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, dqkv, QKV, Pb + o.wqkv, D, c->dtmp, &sp_d));
     {

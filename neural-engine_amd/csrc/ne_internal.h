@@ -182,6 +182,10 @@ struct AdamArgs {
   int zero_grad;        // write g = 0 after the update
 };
 int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s);
+// Sums of squares of two ranges in one launch: g1 into partials[0, nparts_each), g2 into
+// partials[nparts_each, 2 nparts_each).
+int launch_sumsq2(const float *g1, long n1, const float *g2, long n2, double *partials, int nparts_each,
+                  hipStream_t s);
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
                          float *gscale_out, float *gnorm_out, hipStream_t s);
 int launch_adam(int dt, const AdamArgs &a, hipStream_t s);
