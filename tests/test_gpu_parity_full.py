@@ -14,11 +14,9 @@ benchmarked shapes.
 
 Tolerances: loss relative error <= 1e-3, per-tensor gradient relative L2 <= 1e-2, post-AdamW
 weights and moments within 1e-5 relative (an fp32-ulp floor at the tensor's scale), greedy
-tokens identical.  With bf16 activations the GEMMs multiply the bf16 weight shadow, and at
-these N(0, 0.02) weights the Wq / Wk gradients are ill-conditioned in the weights: rounding
-the matrices to bf16 alone (everything else exact fp32) moves them by 1.3e-2 relative L2 at
-Stories110M (fp16: 1.6e-3).  So the bf16 step is compared with the oracle run on the same
-bf16-rounded matrices, as the token loop is; the fp16 step with the oracle on the fp32 weights.
+tokens identical.  These are the bars of the fp16 training format.  The bf16 step is compared
+with the oracle run on the bf16-rounded matrices it multiplies (as the token loop is), with
+the bf16 gradient bar of gpu_util.grad_tol (4e-2; fp16 is the parity-qualified format).
 """
 import functools
 import os
@@ -27,15 +25,27 @@ import time
 import numpy as np
 import pytest
 
-from gpu_util import as_multiplied, need_gpu, rel_l2
+from gpu_util import as_multiplied, grad_tol, need_gpu, rel_l2
 import ne
 from oracle import model as om
 
 pytestmark = pytest.mark.gpu
 
 LOSS_RTOL = 1e-3
-GRAD_RL2 = 1e-2
 ADAM_RTOL = 1e-5
+# Roundings in one moment update: g times the clip scale, the (1 - b) g product, the square
+# for v, the fused multiply-add, plus one for the oracle's own order of operations.
+MOMENT_ULPS = 6
+
+
+def _within(got, want, bound, what):
+    """|got - want| <= bound elementwise (bound >= 0, same shape)."""
+    err = np.abs(got.astype(np.float64) - want)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {err.size} outside the bound; "
+                             f"worst at {i}: got {got[i]!r} want {want[i]!r} bound {bound[i]!r}")
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 DTYPES = {"fp16": ne.NE_FP16, "bf16": ne.NE_BF16}
 
@@ -52,12 +62,13 @@ def _qwen3_params(bf16=False):
     return {k: om.round_bf16(v) for k, v in P.items()} if bf16 else P
 
 
-def _check_grads(label, loss, lo, G, Go):
+def _check_grads(label, loss, lo, G, Go, dtype=ne.NE_FP16):
     errs = sorted(((rel_l2(G[n], Go[n]), n) for n in Go), reverse=True)
     print(f"[{label}] loss gpu={loss:.6f} oracle={lo:.6f} rel={abs(loss - lo) / lo:.2e}; worst grad rel-L2: "
           + ", ".join(f"{n}={e:.2e}" for e, n in errs[:4]), flush=True)
     assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
-    assert errs[0][0] <= GRAD_RL2, errs[0]
+    for e, n in errs:
+        assert e <= grad_tol(n, dtype), (n, e)
 
 
 def _compare_grads(cfg, P, tok, label, vocab_ids=None, dtype=ne.NE_FP16):
@@ -74,7 +85,7 @@ def _compare_grads(cfg, P, tok, label, vocab_ids=None, dtype=ne.NE_FP16):
     Go = om.backward(cfg, Pm, cache)
     del cache
     print(f"\n[{label}] gpu {t1 - t0:.1f}s oracle {time.time() - t1:.1f}s", flush=True)
-    _check_grads(label, loss, lo, G, Go)
+    _check_grads(label, loss, lo, G, Go, dtype)
     return m
 
 
@@ -84,33 +95,53 @@ def _compare_grads(cfg, P, tok, label, vocab_ids=None, dtype=ne.NE_FP16):
 @pytest.mark.parametrize("dtype", list(DTYPES))
 def test_stories110m_ten_steps(dtype):
     """Ten steps of fwd + bwd + AdamW (lr 3e-4, betas 0.9/0.95, eps 1e-8, wd 0.1, clip 1.0,
-    loss scale 256) on fresh batches: each step's loss and gradients against the oracle from
-    the same weights, then the update against the oracle's AdamW on the same gradients and
-    moments (TD/train.m:391-918)."""
+    loss scale 256) on fresh batches (TD/train.m:391-918).  Each step's loss and gradients are
+    checked against the oracle run from the weights that step used, and each update against
+    the oracle's AdamW on the same gradients and moments.  The state is read after each
+    step, whose forward ran beside the update enqueued by the optimizer step before it."""
     cfg = om.stories110m(res_alpha=om.train_alpha(12))
     sh = dict(om.tensor_list(cfg))
     P = om.init_params(cfg, seed=0, std=0.02)
     m = ne.Model.from_oracle(cfg, batch=1, dtype=DTYPES[dtype])
     m.set_params(P)
+    prev = None
+
+    def check_update(prev, step):
+        Pp, Gp, Mp, Vp = prev
+        M0 = {n: np.abs(x) for n, x in Mp.items()}
+        V0 = {n: x.copy() for n, x in Vp.items()}
+        gno = om.optimizer_step(Pp, Gp, Mp, Vp, step, 3e-4, grad_scale=1 / 256, clip=1.0)
+        P2, M2, V2 = m.get_all(sh), m.get_all(sh, ne.NE_ADAM_M), m.get_all(sh, ne.NE_ADAM_V)
+        for n in Pp:
+            np.testing.assert_allclose(P2[n], Pp[n], rtol=ADAM_RTOL, atol=2 ** -23 * np.abs(Pp[n]).max(), err_msg=n)
+            # 1e-5 relative (the two sides' clip scales differ by their gradient norms'
+            # summation order) plus, where m = b1 m + (1 - b1) g nearly cancels, a few float32
+            # roundings of the terms themselves rather than of the result.
+            g = np.abs(Gp[n])
+            _within(M2[n], Mp[n], ADAM_RTOL * np.abs(Mp[n]) + MOMENT_ULPS * 2 ** -24 * (0.9 * M0[n] + 0.1 * g),
+                    n + " (m)")
+            _within(V2[n], Vp[n], ADAM_RTOL * Vp[n] + MOMENT_ULPS * 2 ** -24 * (0.95 * V0[n] + 0.05 * g * g),
+                    n + " (v)")
+        return gno, P2, M2, V2
+
     for step in range(10):
         tok = om.tokens_for_step(cfg, 1, 256, seed=1000 + step)
-        Pg = m.get_all(sh)
-        Mg, Vg = m.get_all(sh, ne.NE_ADAM_M), m.get_all(sh, ne.NE_ADAM_V)
         loss = m.train_step(tok, 256.0)
+        if prev is None:
+            Pg, Mg, Vg = m.get_all(sh), m.get_all(sh, ne.NE_ADAM_M), m.get_all(sh, ne.NE_ADAM_V)
+        else:
+            gno, Pg, Mg, Vg = check_update(prev, step)
+            assert abs(gn - gno) <= 1e-5 * gno, (gn, gno)
         G = m.get_all(sh, ne.NE_GRAD)
         Pm = as_multiplied(Pg, DTYPES[dtype])
         lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0)
         Go = om.backward(cfg, Pm, cache)
         del cache, Pm
-        _check_grads(f"{dtype} step {step}", loss, lo, G, Go)
+        _check_grads(f"{dtype} step {step}", loss, lo, G, Go, DTYPES[dtype])
         gn = m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=1.0)
-        gno = om.optimizer_step(Pg, G, Mg, Vg, step + 1, 3e-4, grad_scale=1 / 256, clip=1.0)
-        assert abs(gn - gno) <= 1e-5 * gno, (gn, gno)
-        P2, M2, V2 = m.get_all(sh), m.get_all(sh, ne.NE_ADAM_M), m.get_all(sh, ne.NE_ADAM_V)
-        for n in Pg:
-            np.testing.assert_allclose(P2[n], Pg[n], rtol=ADAM_RTOL, atol=2 ** -23 * np.abs(Pg[n]).max(), err_msg=n)
-            np.testing.assert_allclose(M2[n], Mg[n], rtol=ADAM_RTOL, atol=2 ** -23 * np.abs(Mg[n]).max(), err_msg=n)
-            np.testing.assert_allclose(V2[n], Vg[n], rtol=ADAM_RTOL, atol=2 ** -23 * np.abs(Vg[n]).max(), err_msg=n)
+        prev = (Pg, G, Mg, Vg)
+    gno, *_ = check_update(prev, 10)
+    assert abs(gn - gno) <= 1e-5 * gno, (gn, gno)
     assert m.state().adam_t == 10 and m.grad_scale_info()[1] == 0
     m.close()
 
