@@ -36,6 +36,10 @@ PEAK_MFMA_16 = 2.5e15      # MI355X dense fp16/bf16 MFMA, flop/s
 # AdamW HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated)
 # on Qwen3-0.6B: equal to its algorithmic 30 B/param (profiles/adam_hbm_counters_qwen3-0.6b.md)
 ADAM_TRAFFIC_B_PER_PARAM = 30.0
+ADAM_TRAFFIC_SOURCE = ("not measured in this run: the committed counter report "
+                       "(profiles/adam_hbm_counters_qwen3-0.6b.md, rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                       "copy-calibrated) measured 30 B/param, the algorithmic bytes; `bench.py --counters DIR` "
+                       "measures it in the same invocation")
 
 WORKLOADS = {
     "qwen3-0.6b-s256-b1": dict(dim=1024, hidden=3072, n_heads=16, kv_heads=8, head_dim=128, n_layers=28,
@@ -174,27 +178,59 @@ def mfma_ceiling(blocks=1024, iters=4096):
     return res
 
 
-def cpu_baseline(wname, w, n_runs=5):
-    """The numpy oracle (fwd + bwd + AdamW) on this host's cores: one warm-up step, then the
-    median of n_runs full steps of the same workload (about 20 s for Qwen3-0.6B, S=256)."""
+def _om_config(w):
     from oracle import model as om
-    cfg = om.Config(dim=w["dim"], hidden=w["hidden"], n_heads=w["n_heads"], kv_heads=w["kv_heads"],
-                    head_dim=w["head_dim"], n_layers=w["n_layers"], vocab=w["vocab"], seq=w["seq"],
-                    rope_theta=w["rope_theta"], qk_norm=w["qk_norm"], res_alpha=1.0 / math.sqrt(2.0 * w["n_layers"]))
-    P = om.init_params(cfg, seed=0, std=0.02)
+    return om.Config(dim=w["dim"], hidden=w["hidden"], n_heads=w["n_heads"], kv_heads=w["kv_heads"],
+                     head_dim=w["head_dim"], n_layers=w["n_layers"], vocab=w["vocab"], seq=w["seq"],
+                     rope_theta=w["rope_theta"], qk_norm=w["qk_norm"],
+                     res_alpha=1.0 / math.sqrt(2.0 * w["n_layers"]))
+
+
+def _median_s(fn, n_runs):
+    """fn() once as a warm-up, then the median wall time of n_runs calls."""
+    fn()
+    ts = []
+    for _ in range(n_runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _train_leg(w, n_runs, P=None):
+    """Median s/step of the oracle's fwd + bwd + AdamW on fresh batches of workload w
+    (P is updated in place)."""
+    from oracle import model as om
+    cfg = _om_config(w)
+    P = om.init_params(cfg, seed=0, std=0.02) if P is None else P
     M = {k: np.zeros_like(v) for k, v in P.items()}
     V = {k: np.zeros_like(v) for k, v in P.items()}
-    times = []
-    for i, tok in enumerate(batches(w, n_runs + 1)):
-        t0 = time.perf_counter()
-        _, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    toks, it = batches(w, n_runs + 1), iter(range(n_runs + 1))
+
+    def step():
+        i = next(it)
+        _, cache = om.forward(cfg, P, toks[i], loss_scale=256.0)
         G = om.backward(cfg, P, cache)
         del cache
         om.optimizer_step(P, G, M, V, i + 1, 3e-4, grad_scale=1.0 / 256, clip=1.0)
-        if i > 0:
-            times.append(time.perf_counter() - t0)
-        del G
-    step_s = float(np.median(times))
+    return _median_s(step, n_runs)
+
+
+def cpu_baseline(wname, w, n_runs=5, legs=True):
+    """The numpy oracle on this host's cores, each timing the median of n_runs after one
+    warm-up.  The headline value is the full training step (fwd + bwd + AdamW) of the
+    benchmarked workload (about 20 s for Qwen3-0.6B, S=256).  `legs` adds the other CPU
+    timings of the same plan: the Stories110M forward + cross-entropy (B=1, S=256) and its
+    full training step, and the Qwen3-0.6B token loop at batch 1 and 32 (bf16-rounded
+    weights held in fp32, every position one full pass with the LM head, as the oracle's
+    token loop runs it) on a short sample: an 8-token prompt and 4 new tokens."""
+    import dataclasses
+    from oracle import model as om
+    P = om.init_params(_om_config(w), seed=0, std=0.02)
+    # the token loop's weights: the same seed-0 draw rounded to bf16, taken before AdamW moves P
+    Pd = {k: om.round_bf16(v) for k, v in P.items()} if legs and wname.startswith("qwen3") else None
+    step_s = _train_leg(w, n_runs, P=P)
+    del P
     threads, blas = os.cpu_count() or 1, "unknown"
     try:
         from threadpoolctl import threadpool_info
@@ -203,10 +239,37 @@ def cpu_baseline(wname, w, n_runs=5):
             threads, blas = info[0]["num_threads"], f"{info[0]['internal_api']} {info[0].get('version')}"
     except Exception:
         pass
-    return {"value": w["batch"] * w["seq"] / step_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"median of {n_runs} full steps (fwd+bwd+AdamW, after 1 warm-up) of {wname} on the numpy "
-                      f"oracle: {step_s:.2f} s/step; numpy BLAS {blas}, {threads} threads; "
-                      f"host CPU {platform.processor() or platform.machine()}"}
+    out = {"value": w["batch"] * w["seq"] / step_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"median of {n_runs} full steps (fwd+bwd+AdamW, after 1 warm-up) of {wname} on the numpy "
+                     f"oracle: {step_s:.2f} s/step; numpy BLAS {blas}, {threads} threads; "
+                     f"host CPU {platform.processor() or platform.machine()}"}
+    if not legs:
+        return out
+    res = []
+    ws = WORKLOADS["stories110m-s256-b1"]
+    cfg_s = _om_config(ws)
+    Ps = om.init_params(cfg_s, seed=0, std=0.02)
+    tok = batches(ws, 1)[0]
+    fwd_s = _median_s(lambda: om.forward(cfg_s, Ps, tok, want_grad_cache=False), n_runs)
+    res.append({"leg": "stories110m-s256-b1 forward + cross-entropy", "value": ws["seq"] / fwd_s,
+                "unit": "tokens/s", "s_per_run": fwd_s})
+    st_s = _train_leg(ws, n_runs, P=Ps)
+    res.append({"leg": "stories110m-s256-b1 training step (fwd+bwd+AdamW)", "value": ws["seq"] / st_s,
+                "unit": "tokens/s", "s_per_run": st_s})
+    del Ps
+    if wname.startswith("qwen3"):
+        cfg_d = dataclasses.replace(_om_config({**w, "seq": 64}), res_alpha=1.0)
+        p0, n_new = 8, 4
+        for B in (1, 32):
+            prompt = np.random.default_rng(2).integers(0, w["vocab"], (B, p0)).astype(np.int32)
+            d_s = _median_s(lambda: om.decode(cfg_d, Pd, prompt, n_new), n_runs)
+            npos = p0 + n_new - 1
+            res.append({"leg": f"{wname.split('-s')[0]} token loop, batch {B} (greedy)",
+                        "value": B * npos / d_s, "unit": "tokens/s (sequence positions processed)",
+                        "s_per_run": d_s,
+                        "sample": f"prompt {p0} + {n_new} new tokens = {npos} positions per sequence"})
+    out["legs"] = res
+    return out
 
 
 def train_summary(w, r, ceiling=None):
@@ -226,6 +289,117 @@ def train_summary(w, r, ceiling=None):
                           "step_tflops": fl["total"] / (r["ms"] / 1e3) / 1e12}}
 
 
+def _short(name):
+    """Kernel name without its return type, namespace and argument list."""
+    n = name.replace("(anonymous namespace)::", "")
+    if n.startswith("void "):
+        n = n[5:]
+    if n.endswith(")"):  # drop the trailing balanced (...) group: the argument list
+        depth = 0
+        for i in range(len(n) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(n[i], 0)
+            if depth == 0:
+                n = n[:i]
+                break
+    return n
+
+
+def counters_run(child_args, outdir, timeout_s=600):
+    """The per-kernel counter report of one benchmark invocation: this process never touches the
+    GPU; it runs the benchmark as child processes under rocprofv3 (a kernel trace with
+    statistics, then one pass each of the FETCH_SIZE and WRITE_SIZE counters, their bytes
+    scaled by three plain 1 GiB device copies run first in the same process) and returns the
+    trace run's JSON result with a `counters` object added."""
+    import csv
+    import subprocess
+    me = [sys.executable, os.path.abspath(__file__)]
+    os.makedirs(outdir, exist_ok=True)
+    cmds = {
+        "trace": ["rocprofv3", "--kernel-trace", "--stats", "-f", "csv", "-d", os.path.join(outdir, "trace"), "-o",
+                  "run", "--"] + me + child_args + ["--no-graphs", "--no-cpu"],
+        "fetch": ["rocprofv3", "--pmc", "FETCH_SIZE", "-f", "csv", "-d", os.path.join(outdir, "fetch"), "-o", "run",
+                  "--"] + me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale", "--calib-copy"],
+        "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "-f", "csv", "-d", os.path.join(outdir, "write"), "-o", "run",
+                  "--"] + me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale", "--calib-copy"],
+    }
+    result = None
+    for key, cmd in cmds.items():
+        print(f"[counters] {key}: {' '.join(cmd)}", file=sys.stderr, flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
+        lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        if key == "trace":
+            if not lines:
+                raise RuntimeError(f"rocprofv3 trace run printed no result (rc {r.returncode}): {r.stderr[-2000:]}")
+            result = json.loads(lines[-1])
+        elif r.returncode != 0 and not lines:
+            raise RuntimeError(f"rocprofv3 {key} pass failed (rc {r.returncode}): {r.stderr[-2000:]}")
+    stats = []
+    with open(os.path.join(outdir, "trace", "run_kernel_stats.csv")) as f:
+        for row in csv.DictReader(f):
+            stats.append({"kernel": _short(row["Name"]), "calls": int(row["Calls"]),
+                          "avg_us": float(row["AverageNs"]) / 1e3, "total_ms": float(row["TotalDurationNs"]) / 1e6,
+                          "pct": float(row["Percentage"])})
+    stats.sort(key=lambda d: -d["total_ms"])
+
+    def pmc(key):
+        rows = list(csv.DictReader(open(os.path.join(outdir, key, "run_counter_collection.csv"))))
+        copies = sorted((float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]), reverse=True)[:3]
+        scale = (1 << 30) / (sum(copies) / len(copies) * 1024) if copies else None
+        per = {}
+        for r in rows:
+            k = _short(r["Kernel_Name"])
+            s_, n_ = per.get(k, (0.0, 0))
+            per[k] = (s_ + float(r["Counter_Value"]) * 1024, n_ + 1)
+        return scale, per
+    fs, fetch = pmc("fetch")
+    wsc, write = pmc("write")
+    hbm = []
+    for k in fetch:
+        if k in write and fs and wsc:
+            rd = fetch[k][0] * fs / fetch[k][1]
+            wr = write[k][0] * wsc / write[k][1]
+            hbm.append({"kernel": k, "launches": fetch[k][1], "read_MB_per_launch": rd / 1e6,
+                        "write_MB_per_launch": wr / 1e6})
+    hbm.sort(key=lambda d: -(d["read_MB_per_launch"] + d["write_MB_per_launch"]) * d["launches"])
+    result["counters"] = {"kernel_stats": stats[:30], "hbm_bytes": hbm[:30],
+                          "calibration": {"fetch_bytes_per_KiB": fs * 1024 if fs else None,
+                                          "write_bytes_per_KiB": wsc * 1024 if wsc else None,
+                                          "how": "three 1 GiB device copies (__amd_rocclr_copyBuffer) in the "
+                                                 "counter passes"},
+                          "commands": {k: " ".join(v) for k, v in cmds.items()}}
+    # the roofline kernel's HBM traffic per pass, from the counter passes
+    rk = result["roofline"]["kernel"].split(" ")[0]
+    for h in hbm:
+        if h["kernel"].split("<")[0] == rk:
+            result["roofline"]["traffic"] = (h["read_MB_per_launch"] + h["write_MB_per_launch"]) * 1e6 * \
+                result["roofline"]["launches_per_pass"]
+            result["roofline"]["traffic_source"] = ("rocprofv3 FETCH_SIZE + WRITE_SIZE of this invocation's counter "
+                                                    "passes, copy-calibrated, mean per launch x launches per pass")
+    return result
+
+
+def counters_markdown(res):
+    """A short text summary of a counters_run result (for profiles/)."""
+    c = res["counters"]
+    out = [f"# rocprofv3 per-kernel report: {res['config']['workload']}", "",
+           f"Step: {res['ms_per_step']:.3f} ms, {res['value']:.0f} tokens/s (traced run, eager launches).", "",
+           "Commands (one `python bench.py --counters` invocation runs them as child processes):", ""]
+    out += [f"    {v}" for v in c["commands"].values()]
+    out += ["", "| kernel | calls | avg µs | total ms | % |", "|---|---:|---:|---:|---:|"]
+    out += [f"| `{d['kernel']}` | {d['calls']} | {d['avg_us']:.2f} | {d['total_ms']:.2f} | {d['pct']:.2f} |"
+            for d in c["kernel_stats"]]
+    out += ["", "HBM bytes per launch (FETCH_SIZE, WRITE_SIZE; calibrated: "
+            f"{c['calibration']['fetch_bytes_per_KiB']:.0f} and {c['calibration']['write_bytes_per_KiB']:.0f} "
+            "bytes per KiB unit):", "", "| kernel | launches | read MB | write MB |", "|---|---:|---:|---:|"]
+    out += [f"| `{d['kernel']}` | {d['launches']} | {d['read_MB_per_launch']:.2f} | {d['write_MB_per_launch']:.2f} |"
+            for d in c["hbm_bytes"]]
+    r = res["roofline"]
+    out += ["", f"Roofline kernel `{r['kernel'].split(' ')[0]}`: {r['achieved']:.0f} GB/s of {r['peak']:.0f} "
+            f"(frac {r['frac']:.3f}); traffic per pass {r['traffic'] / 1e9 if r['traffic'] else float('nan'):.2f} GB "
+            f"against {r['bytes_per_pass'] / 1e9:.2f} GB algorithmic.", ""]
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,10 +416,32 @@ def main():
     ap.add_argument("--no-overlap", action="store_true",
                     help="run the weight-gradient GEMMs in order on the step's stream instead of on a "
                          "second stream beside the activation-gradient chain")
+    ap.add_argument("--counters", metavar="DIR",
+                    help="run this benchmark under rocprofv3 as child processes (kernel statistics and HBM byte "
+                         "counters, written under DIR) and add the per-kernel report to the result")
+    ap.add_argument("--counters-md", metavar="FILE", help="with --counters: also write the report as text to FILE")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run three plain 1 GiB device copies (a known-size kernel that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
     a = ap.parse_args()
+    if a.counters:
+        child, skip = [], False
+        for x in sys.argv[1:]:
+            if skip:
+                skip = False
+                continue
+            if x in ("--counters", "--counters-md"):
+                skip = True
+                continue
+            if x.startswith(("--counters=", "--counters-md=")):
+                continue
+            child.append(x)
+        res = counters_run(child, a.counters)
+        if a.counters_md:
+            with open(a.counters_md, "w") as f:
+                f.write(counters_markdown(res))
+        print(json.dumps(res), flush=True)
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(data-parallel sharding is a design note); run with --gpus 1", file=sys.stderr)
@@ -261,11 +457,20 @@ def main():
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
-    # one AdamW pass per step: 29 launches (embedding + gains, then one per layer) on the second
-    # stream, each between its own event pair; the pass time is the sum of their durations
+    # one AdamW pass per step: 1 + L launches (embedding + gains, then one per layer) on the
+    # second stream, each between its own event pair; the pass time is the sum of their durations
     adam_launches = max(r["adam"][1], 1) / a.steps
     adam_ms = r["adam"][0] / a.steps
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
+    roofline = {"bound": "hbm",
+                "kernel": "adam_kernel (fused AdamW; one pass over all parameters per step, in "
+                          f"{adam_launches:.0f} launches: embedding + gains, then one per layer)",
+                "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
+                "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
+                "traffic_source": ADAM_TRAFFIC_SOURCE,
+                "bytes_per_pass": adam_bytes, "pass_ms": adam_ms, "launches_per_pass": adam_launches,
+                "bytes_per_launch": adam_bytes / adam_launches, "avg_launch_ms": adam_ms / adam_launches}
     out = {
         "metric": "Qwen3-0.6B train tokens/s + step ms on 1 MI355X; MFMA util %; decode tok/s",
         "value": summ["tokens_per_s"],
@@ -282,16 +487,7 @@ def main():
         "config": {"workload": a.workload, "global_batch": w["batch"], "seq_len": w["seq"],
                    "tokens_per_step": w["batch"] * w["seq"], "params": npar, "parallelism": "single GPU",
                    "precision": "fp32 master weights + AdamW state, fp16 activations/operands, fp32 accumulate"},
-        "roofline": {"bound": "hbm",
-                     "kernel": "adam_kernel (fused AdamW; one pass over all parameters per step, in "
-                               f"{adam_launches:.0f} launches: embedding + gains, then one per layer)",
-                     "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
-                     "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
-                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated "
-                                       "(profiles/adam_hbm_counters_qwen3-0.6b.md)",
-                     "bytes_per_pass": adam_bytes, "pass_ms": adam_ms, "launches_per_pass": adam_launches,
-                     "bytes_per_launch": adam_bytes / adam_launches, "avg_launch_ms": adam_ms / adam_launches},
+        "roofline": roofline,
         "dominant_family": dom,
         "kernel_ms_per_step": fam_ms,
         "mfma_util": summ["mfma_util"],
