@@ -33,12 +33,12 @@ import ne  # noqa: E402
 
 PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes/s
 PEAK_MFMA_16 = 2.5e15      # MI355X dense fp16/bf16 MFMA, flop/s
-# AdamW HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated)
-# on Qwen3-0.6B: equal to its algorithmic 30 B/param (profiles/adam_hbm_counters_qwen3-0.6b.md)
+# AdamW HBM bytes per parameter: rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated) on Qwen3-0.6B
+# measured its algorithmic 30 B/param (profiles/train_step_qwen3-0.6b_s256_b1_counters.md)
 ADAM_TRAFFIC_B_PER_PARAM = 30.0
-ADAM_TRAFFIC_SOURCE = ("not measured in this run: the committed counter report "
-                       "(profiles/adam_hbm_counters_qwen3-0.6b.md, rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                       "copy-calibrated) measured 30 B/param, the algorithmic bytes; `bench.py --counters DIR` "
+ADAM_TRAFFIC_SOURCE = ("algorithmic (30 B/param), not measured in this run; the committed counter report "
+                       "profiles/train_step_qwen3-0.6b_s256_b1_counters.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                       "copy-calibrated) measured the same 17.88 GB per pass; `bench.py --counters DIR` "
                        "measures it in the same invocation")
 
 WORKLOADS = {
@@ -304,35 +304,44 @@ def _short(name):
     return n
 
 
-def counters_run(child_args, outdir, timeout_s=600):
-    """The per-kernel counter report of one benchmark invocation: this process never touches the
-    GPU; it runs the benchmark as child processes under rocprofv3 (a kernel trace with
-    statistics, then one pass each of the FETCH_SIZE and WRITE_SIZE counters, their bytes
-    scaled by three plain 1 GiB device copies run first in the same process) and returns the
-    trace run's JSON result with a `counters` object added."""
+def counters_run(child_args, outdir, timeout_s=900):
+    """The per-kernel counter report of one benchmark invocation, for the training step of its
+    workload: this process never touches the GPU; it runs the benchmark as child processes under
+    rocprofv3, eager launches, no decode, no CPU leg: a kernel trace with statistics, one pass
+    each of the FETCH_SIZE and WRITE_SIZE counters (their bytes scaled by three plain 1 GiB
+    device copies run first in the same process) and one of MfmaUtil with the fp16/bf16 MFMA
+    op count.  Returns the trace run's JSON result with a `counters` object added."""
     import csv
     import subprocess
     me = [sys.executable, os.path.abspath(__file__)]
     os.makedirs(outdir, exist_ok=True)
+    run = me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale"]
+    pmc_run = run + ["--steps", "3", "--warmup", "1"]
+
+    def prof(key, what):
+        return ["rocprofv3"] + what + ["-f", "csv", "-d", os.path.join(outdir, key), "-o", "run", "--"]
     cmds = {
-        "trace": ["rocprofv3", "--kernel-trace", "--stats", "-f", "csv", "-d", os.path.join(outdir, "trace"), "-o",
-                  "run", "--"] + me + child_args + ["--no-graphs", "--no-cpu"],
-        "fetch": ["rocprofv3", "--pmc", "FETCH_SIZE", "-f", "csv", "-d", os.path.join(outdir, "fetch"), "-o", "run",
-                  "--"] + me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale", "--calib-copy"],
-        "write": ["rocprofv3", "--pmc", "WRITE_SIZE", "-f", "csv", "-d", os.path.join(outdir, "write"), "-o", "run",
-                  "--"] + me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale", "--calib-copy"],
+        "trace": prof("trace", ["--kernel-trace", "--stats"]) + run,
+        "fetch": prof("fetch", ["--pmc", "FETCH_SIZE"]) + pmc_run + ["--calib-copy"],
+        "write": prof("write", ["--pmc", "WRITE_SIZE"]) + pmc_run + ["--calib-copy"],
+        "mfma": prof("mfma", ["--pmc", "MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_F16"]) + pmc_run,
     }
     result = None
     for key, cmd in cmds.items():
         print(f"[counters] {key}: {' '.join(cmd)}", file=sys.stderr, flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
         lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        if not lines:
+            raise RuntimeError(f"rocprofv3 {key} pass printed no result (rc {r.returncode}): {r.stderr[-2000:]}")
         if key == "trace":
-            if not lines:
-                raise RuntimeError(f"rocprofv3 trace run printed no result (rc {r.returncode}): {r.stderr[-2000:]}")
             result = json.loads(lines[-1])
-        elif r.returncode != 0 and not lines:
-            raise RuntimeError(f"rocprofv3 {key} pass failed (rc {r.returncode}): {r.stderr[-2000:]}")
+    shown = {k: " ".join(v).replace(me[1], "bench.py").replace(sys.executable, "python3") for k, v in cmds.items()}
+    return counters_collect(outdir, result, shown)
+
+
+def counters_collect(outdir, result, commands):
+    """Join the trace and counter passes under outdir into result["counters"] (see counters_run)."""
+    import csv
     stats = []
     with open(os.path.join(outdir, "trace", "run_kernel_stats.csv")) as f:
         for row in csv.DictReader(f):
@@ -340,63 +349,87 @@ def counters_run(child_args, outdir, timeout_s=600):
                           "avg_us": float(row["AverageNs"]) / 1e3, "total_ms": float(row["TotalDurationNs"]) / 1e6,
                           "pct": float(row["Percentage"])})
     stats.sort(key=lambda d: -d["total_ms"])
+    avg_us = {d["kernel"]: d["avg_us"] for d in stats}
 
     def pmc(key):
-        rows = list(csv.DictReader(open(os.path.join(outdir, key, "run_counter_collection.csv"))))
-        copies = sorted((float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]), reverse=True)[:3]
-        scale = (1 << 30) / (sum(copies) / len(copies) * 1024) if copies else None
-        per = {}
-        for r in rows:
+        """{kernel: {counter: (sum over dispatches, dispatches)}} of a counter pass, and the
+        per-dispatch values of the device copies."""
+        per, copies = {}, []
+        for r in csv.DictReader(open(os.path.join(outdir, key, "run_counter_collection.csv"))):
             k = _short(r["Kernel_Name"])
-            s_, n_ = per.get(k, (0.0, 0))
-            per[k] = (s_ + float(r["Counter_Value"]) * 1024, n_ + 1)
-        return scale, per
-    fs, fetch = pmc("fetch")
-    wsc, write = pmc("write")
-    hbm = []
-    for k in fetch:
-        if k in write and fs and wsc:
-            rd = fetch[k][0] * fs / fetch[k][1]
-            wr = write[k][0] * wsc / write[k][1]
-            hbm.append({"kernel": k, "launches": fetch[k][1], "read_MB_per_launch": rd / 1e6,
-                        "write_MB_per_launch": wr / 1e6})
-    hbm.sort(key=lambda d: -(d["read_MB_per_launch"] + d["write_MB_per_launch"]) * d["launches"])
-    result["counters"] = {"kernel_stats": stats[:30], "hbm_bytes": hbm[:30],
-                          "calibration": {"fetch_bytes_per_KiB": fs * 1024 if fs else None,
-                                          "write_bytes_per_KiB": wsc * 1024 if wsc else None,
+            c = per.setdefault(k, {})
+            s_, n_ = c.get(r["Counter_Name"], (0.0, 0))
+            c[r["Counter_Name"]] = (s_ + float(r["Counter_Value"]), n_ + 1)
+            if "copyBuffer" in k:
+                copies.append(float(r["Counter_Value"]))
+        return per, copies
+
+    def copy_scale(copies):
+        """Bytes per counter unit: the three 1 GiB copies are the three largest copy dispatches."""
+        vals = sorted(copies, reverse=True)[:3]
+        return (1 << 30) / (sum(vals) / len(vals)) if len(vals) == 3 else None
+    (fetch, fc), (write, wc), (mfma, _) = pmc("fetch"), pmc("write"), pmc("mfma")
+    fs, wsc = copy_scale(fc), copy_scale(wc)
+    rows = []
+    for d in stats:
+        k = d["kernel"]
+        row = dict(d)
+        if k in fetch and "FETCH_SIZE" in fetch[k] and fs:
+            v, n = fetch[k]["FETCH_SIZE"]
+            row["read_MB_per_launch"] = v / n * fs / 1e6
+        if k in write and "WRITE_SIZE" in write[k] and wsc:
+            v, n = write[k]["WRITE_SIZE"]
+            row["write_MB_per_launch"] = v / n * wsc / 1e6
+        if k in mfma and "MfmaUtil" in mfma[k]:
+            v, n = mfma[k]["MfmaUtil"]
+            row["mfma_util_pct"] = v / n
+            if "SQ_INSTS_VALU_MFMA_MOPS_F16" in mfma[k]:
+                v, n = mfma[k]["SQ_INSTS_VALU_MFMA_MOPS_F16"]
+                row["mfma_tflops"] = v / n * 512 / (avg_us[k] * 1e-6) / 1e12
+        rows.append(row)
+    result["counters"] = {"kernels": rows[:40],
+                          "calibration": {"fetch_bytes_per_unit": fs, "write_bytes_per_unit": wsc,
                                           "how": "three 1 GiB device copies (__amd_rocclr_copyBuffer) in the "
-                                                 "counter passes"},
-                          "commands": {k: " ".join(v) for k, v in cmds.items()}}
+                                                 "byte-counter passes"},
+                          "commands": commands}
     # the roofline kernel's HBM traffic per pass, from the counter passes
     rk = result["roofline"]["kernel"].split(" ")[0]
-    for h in hbm:
-        if h["kernel"].split("<")[0] == rk:
-            result["roofline"]["traffic"] = (h["read_MB_per_launch"] + h["write_MB_per_launch"]) * 1e6 * \
+    for row in rows:
+        if row["kernel"].split("<")[0] == rk and "read_MB_per_launch" in row and "write_MB_per_launch" in row:
+            result["roofline"]["traffic"] = (row["read_MB_per_launch"] + row["write_MB_per_launch"]) * 1e6 * \
                 result["roofline"]["launches_per_pass"]
             result["roofline"]["traffic_source"] = ("rocprofv3 FETCH_SIZE + WRITE_SIZE of this invocation's counter "
                                                     "passes, copy-calibrated, mean per launch x launches per pass")
     return result
 
 
-def counters_markdown(res):
-    """A short text summary of a counters_run result (for profiles/)."""
+def counters_markdown(res, made_by):
+    """A short text summary of a counters_run result (for profiles/); made_by: the command."""
     c = res["counters"]
-    out = [f"# rocprofv3 per-kernel report: {res['config']['workload']}", "",
-           f"Step: {res['ms_per_step']:.3f} ms, {res['value']:.0f} tokens/s (traced run, eager launches).", "",
-           "Commands (one `python bench.py --counters` invocation runs them as child processes):", ""]
+    cal = c["calibration"]
+    out = [f"# rocprofv3 per-kernel report: training step of {res['config']['workload']}", "",
+           f"Made by `{made_by}` (one run: its child processes below).", "",
+           f"Traced run (eager launches, kernels serialised by the tracer where counters are read): "
+           f"{res['ms_per_step']:.3f} ms per step.", "",
+           "Commands of the child processes:", ""]
     out += [f"    {v}" for v in c["commands"].values()]
-    out += ["", "| kernel | calls | avg µs | total ms | % |", "|---|---:|---:|---:|---:|"]
-    out += [f"| `{d['kernel']}` | {d['calls']} | {d['avg_us']:.2f} | {d['total_ms']:.2f} | {d['pct']:.2f} |"
-            for d in c["kernel_stats"]]
-    out += ["", "HBM bytes per launch (FETCH_SIZE, WRITE_SIZE; calibrated: "
-            f"{c['calibration']['fetch_bytes_per_KiB']:.0f} and {c['calibration']['write_bytes_per_KiB']:.0f} "
-            "bytes per KiB unit):", "", "| kernel | launches | read MB | write MB |", "|---|---:|---:|---:|"]
-    out += [f"| `{d['kernel']}` | {d['launches']} | {d['read_MB_per_launch']:.2f} | {d['write_MB_per_launch']:.2f} |"
-            for d in c["hbm_bytes"]]
+    out += ["", "Durations from the kernel trace; HBM bytes per launch from FETCH_SIZE and WRITE_SIZE scaled by "
+            f"{cal['fetch_bytes_per_unit']:.0f} and {cal['write_bytes_per_unit']:.0f} bytes per counter unit (the "
+            "factors that make three 1 GiB device copies read and write 1 GiB each); MfmaUtil as rocprofv3 derives "
+            "it; MFMA TFLOP/s = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 / average duration.", "",
+            "| kernel | calls | avg µs | total ms | % | read MB | write MB | MfmaUtil % | MFMA TFLOP/s |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+
+    def f(d, k, fmt):
+        return format(d[k], fmt) if k in d else "–"
+    out += [f"| `{d['kernel']}` | {d['calls']} | {d['avg_us']:.2f} | {d['total_ms']:.2f} | {d['pct']:.2f} | "
+            f"{f(d, 'read_MB_per_launch', '.2f')} | {f(d, 'write_MB_per_launch', '.2f')} | "
+            f"{f(d, 'mfma_util_pct', '.1f')} | {f(d, 'mfma_tflops', '.0f')} |" for d in c["kernels"]]
     r = res["roofline"]
     out += ["", f"Roofline kernel `{r['kernel'].split(' ')[0]}`: {r['achieved']:.0f} GB/s of {r['peak']:.0f} "
-            f"(frac {r['frac']:.3f}); traffic per pass {r['traffic'] / 1e9 if r['traffic'] else float('nan'):.2f} GB "
-            f"against {r['bytes_per_pass'] / 1e9:.2f} GB algorithmic.", ""]
+            f"(frac {r['frac']:.3f}) in the traced run; HBM traffic per pass "
+            f"{r['traffic'] / 1e9 if r['traffic'] else float('nan'):.2f} GB against {r['bytes_per_pass'] / 1e9:.2f} GB "
+            "algorithmic.", ""]
     return "\n".join(out)
 
 
@@ -439,7 +472,7 @@ def main():
         res = counters_run(child, a.counters)
         if a.counters_md:
             with open(a.counters_md, "w") as f:
-                f.write(counters_markdown(res))
+                f.write(counters_markdown(res, " ".join(["python3", "bench.py"] + sys.argv[1:])))
         print(json.dumps(res), flush=True)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -486,7 +519,9 @@ def main():
         "data": "synthetic: N(0,0.02) weights from seed 0, uniform token ids (fresh batch per step)",
         "config": {"workload": a.workload, "global_batch": w["batch"], "seq_len": w["seq"],
                    "tokens_per_step": w["batch"] * w["seq"], "params": npar, "parallelism": "single GPU",
-                   "precision": "fp32 master weights + AdamW state, fp16 activations/operands, fp32 accumulate"},
+                   "precision": "fp32 master weights + AdamW state, fp16 activations/operands, fp32 accumulate "
+                                "(fp16 is the training format; bf16 operands are supported, with their Wq/Wk/QK-norm "
+                                "gradients tested at 4e-2 relative L2 instead of 1e-2)"},
         "roofline": roofline,
         "dominant_family": dom,
         "kernel_ms_per_step": fam_ms,

@@ -608,6 +608,8 @@ __global__ __launch_bounds__(1024) void dec_argmax_kernel(const float *__restric
     best = rv[0]; bi = ri[0];
     for (int w = 1; w < 16; w++)
       if (rv[w] > best || (rv[w] == best && ri[w] < bi)) { best = rv[w]; bi = ri[w]; }
+    // no logit above -inf (all NaN or -inf): token 0, so the next lookup stays in the table
+    if (bi == 0x7fffffff) bi = 0;
     tok[b] = bi;
     out[(long)b * ctx + gen_step(st)] = bi;
   }

@@ -191,6 +191,22 @@ def test_decode_greedy_matches_oracle(case, dtype):
     m.close()
 
 
+@pytest.mark.parametrize("B", [3, 6])
+def test_decode_long_cache_splits_match_oracle(B):
+    """A cache of 4200 positions (scores of every position in LDS) with a 150-token prompt:
+    B=3 takes the VALU GEMVs, B=6 the MFMA GEMVs."""
+    cfg = om.tiny(**CASES["qwen3"], vocab=1024)
+    P = _held_params(cfg, ne.NE_BF16, std=0.05)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, (B, 150)).astype(np.int32)
+    m = ne.Model.from_oracle(cfg, decode_batch=B, decode_ctx=4200, dtype=ne.NE_BF16)
+    m.set_params(P)
+    got = m.decode(prompt, 40)
+    want, margins, _ = om.decode(cfg, P, prompt, 40, return_logits=True)
+    print(f"\n  min top-2 margin {margins.min():.3e}")
+    np.testing.assert_array_equal(got, want)
+    m.close()
+
+
 def test_decode_sampling_matches_oracle():
     cfg = om.tiny(**CASES["qwen3"], vocab=1024)
     P = _held_params(cfg, ne.NE_BF16, std=0.3)
