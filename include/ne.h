@@ -120,6 +120,16 @@ int ne_use_graphs(ne_ctx *ctx, int on);
  * counterpart there: it is for timing, and for checking that the two orders agree. */
 int ne_overlap_weight_grads(ne_ctx *ctx, int on);
 
+/* Which RMSNorm backward the step uses for the attention, FFN and final norms.  ref = 0
+ * (default): the exact gradient of y = x*r*g, dx = r*g*dy - x*r^3*sum(dy*x*g)/D.  ref = 1:
+ * the reference's formula, dx = (dy - x*r^2*sum(dy*x*g)/D)*r*g, as rmsnorm_bwd /
+ * rmsnorm_bwd_add compute it (TD/cpu_ops.h:146-153, 188-189, 255-256; called from TD/train.m:527, 603, 751);
+ * its projection term carries one more gain factor, so the two agree while the gains are
+ * 1.0 and drift apart as they train.  For runs that must follow a reference run's trajectory.
+ * The gain gradients are the same under both; the QK-norm backward (no counterpart in the
+ * reference) stays exact. */
+int ne_rmsnorm_bwd_formula(ne_ctx *ctx, int ref);
+
 /* Scale grads by grad_scale, global L2 norm, clip to `clip` (if > 0), AdamW with
  * bias-corrected moments (t = ++adam_t), weight decay wd on matrices and the embedding
  * (0 on the RMSNorm / QK-norm gains), refresh the 16-bit shadow, zero the grads.  gnorm_out

@@ -189,11 +189,14 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_fwd_kernel(float *__restrict__
 //   dx = r*g*dy - x*r^3*sum(dy*x*g)/D (+ resid);  dg += sum_t dy*x*r
 //   dxb = 16-bit(bscale * dx)  (the alpha-scaled operand of the next GEMM); the gain
 //   gradient is accumulated times dg_scale (removes the backward's internal scale)
-// Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).  A block walks
+// Replaces TD/cpu_ops.h:108-261 (rmsnorm_bwd / rmsnorm_bwd_add).  With REF the
+// reference's own formula is used instead, dx = (dy - x*r^2*sum(dy*x*g)/D)*r*g
+// (TD/cpu_ops.h:146-153, 188-189, 255-256), whose projection term carries one more
+// factor g than the exact gradient; both agree while every gain is 1.  A block walks
 // rows_per_block rows; each thread keeps the gain-gradient sums of its own columns and
 // writes them as the block's partial row (or adds them atomically without `part`).  With
 // split-K partials (sp.n > 0) dy is formed from them.
-template <typename HT>
+template <typename HT, bool REF>
 __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
     const float *__restrict__ dy, const float *__restrict__ x, const float *__restrict__ g,
     const float *__restrict__ rr, const float *__restrict__ resid, float *__restrict__ dx,
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
     float rn = 0.f;
     if (row + 1 < r1) load_row(row + 1, dyn, xn, rsn, rn);
     dot = block_sum_row(dot, red, row & 1);
-    const float c = r * r * r * dot * invD;
+    const float c = REF ? r * r * dot * invD : r * r * r * dot * invD;
     float4 *dxr = (float4 *)(dx + (long)row * D);
     u16x4 *dbr = dxb ? (u16x4 *)(dxb + (long)row * D) : nullptr;
 #pragma unroll
@@ -254,10 +257,17 @@ __global__ __launch_bounds__(RMS_NT) void rmsnorm_bwd_kernel(
       if (i < D4) {
         const float4 w = gw[j];
         float4 o;
-        o.x = r * w.x * dyv[j].x - xv[j].x * c;
-        o.y = r * w.y * dyv[j].y - xv[j].y * c;
-        o.z = r * w.z * dyv[j].z - xv[j].z * c;
-        o.w = r * w.w * dyv[j].w - xv[j].w * c;
+        if (REF) {
+          o.x = (dyv[j].x - xv[j].x * c) * r * w.x;
+          o.y = (dyv[j].y - xv[j].y * c) * r * w.y;
+          o.z = (dyv[j].z - xv[j].z * c) * r * w.z;
+          o.w = (dyv[j].w - xv[j].w * c) * r * w.w;
+        } else {
+          o.x = r * w.x * dyv[j].x - xv[j].x * c;
+          o.y = r * w.y * dyv[j].y - xv[j].y * c;
+          o.z = r * w.z * dyv[j].z - xv[j].z * c;
+          o.w = r * w.w * dyv[j].w - xv[j].w * c;
+        }
         if (resid) {
           o.x += rsv[j].x; o.y += rsv[j].y; o.z += rsv[j].z; o.w += rsv[j].w;
         }
@@ -638,15 +648,17 @@ long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD) {
 
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg, float dg_scale, int T,
-                       int D, int *ovf, float *part, hipStream_t s, const SplitIn &sp, bool defer_colsum) {
+                       int D, int *ovf, float *part, hipStream_t s, const SplitIn &sp, bool defer_colsum,
+                       bool ref_formula) {
   if (D % 4 || D > 4 * RMS_NT * RMS_VPT)
     return ne_fail(NE_ERR_ARG, "rmsnorm_bwd: D=%d must be a multiple of 4 <= 2048", D);
   if (T <= 0) return 0;
   const int rows = rms_rows(T);
   const int nb = (T + rows - 1) / rows;
   NE_CHECK(DISPATCH_H16(dt, [&] {
-    hipLaunchKernelGGL(rmsnorm_bwd_kernel<HT>, dim3(nb), dim3(RMS_NT), 0, s, dy, x, g, r, resid, dx, dxb, bscale, dg,
-                       dg_scale, T, D, rows, ovf, part, sp);
+    auto kernel = ref_formula ? rmsnorm_bwd_kernel<HT, true> : rmsnorm_bwd_kernel<HT, false>;
+    hipLaunchKernelGGL(kernel, dim3(nb), dim3(RMS_NT), 0, s, dy, x, g, r, resid, dx, dxb, bscale, dg, dg_scale, T, D,
+                       rows, ovf, part, sp);
     return ne_hip_status(hipGetLastError(), "rmsnorm_bwd");
   }()));
   if (part && !defer_colsum) {

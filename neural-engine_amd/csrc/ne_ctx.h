@@ -111,6 +111,7 @@ struct ne_ctx {
   std::vector<GraphEntry> graphs;
   bool use_graphs = true;
   bool overlap_wgrad = true;  // weight-gradient GEMMs on st2 (ne_overlap_weight_grads)
+  bool rms_bwd_ref = false;   // the reference's RMSNorm backward formula (ne_rmsnorm_bwd_formula)
   float *h_scalar = nullptr; // pinned [4]
   int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};

@@ -674,7 +674,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, c->xL, P + c->off_gfinal, c->rf, nullptr, c->dx,
                                 c->dbf + 2 * (size_t)(c->L - 1) * TD, alpha, G + c->off_gfinal, u, T, D,
-                                ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true));
+                                ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true, c->rms_bwd_ref));
   }
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
@@ -691,7 +691,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     {
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x2, P + o.g_ffn, a.r2, c->dx, c->dx2, dbf_att, alpha, G + o.g_ffn,
-                                  u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 1 + 2 * l), c->st, sp_d, true));
+                                  u, T, D, ovf + OVF_NORM_BWD, norm_part(c, 1 + 2 * l), c->st, sp_d, true, c->rms_bwd_ref));
     }
     // attention: dbf_att = alpha * dx2
     SplitIn sp_o;
@@ -725,7 +725,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
       // the bottom layer needs no 16-bit copy (the embedding scatter reads the fp32 dx)
       NE_CHECK(launch_rmsnorm_bwd(dt, c->dtmp, a.x_in, P + o.g_att, a.r1, c->dx2, c->dx,
                                   l > 0 ? c->dbf + 2 * (size_t)(l - 1) * TD : nullptr, alpha, G + o.g_att, u, T, D,
-                                  ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st, sp_d, true));
+                                  ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st, sp_d, true, c->rms_bwd_ref));
     }
   }
   NE_CHECK(wq.join());
@@ -841,6 +841,18 @@ extern "C" int ne_overlap_weight_grads(ne_ctx *c, int on) {
   for (auto &e : c->graphs) (void)hipGraphExecDestroy(e.exec);
   c->graphs.clear();
   c->overlap_wgrad = on != 0;
+  return 0;
+}
+
+extern "C" int ne_rmsnorm_bwd_formula(ne_ctx *c, int ref) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  if (c->rms_bwd_ref == (ref != 0)) return 0;
+  NE_CHECK(adam_join(c));
+  NE_HIP(hipStreamSynchronize(c->st));
+  // the captured steps bake the kernel choice in
+  for (auto &e : c->graphs) (void)hipGraphExecDestroy(e.exec);
+  c->graphs.clear();
+  c->rms_bwd_ref = ref != 0;
   return 0;
 }
 

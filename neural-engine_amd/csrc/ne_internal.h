@@ -102,11 +102,12 @@ int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *
 long rmsnorm_bwd_part_elems(int T, int D);
 long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD);
 // With sp.n > 0, dy is formed from split-K partials (SplitIn) instead of read.  With
-// defer_colsum the partials are left for one colsum_batch launch (ColsumJob) later.
+// defer_colsum the partials are left for one colsum_batch launch (ColsumJob) later.  With
+// ref_formula dx follows the reference's formula (gain factor on the projection term too).
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
                        const float *resid, float *dx, h16_t *dxb, float bscale, float *dg,
                        float dg_scale, int T, int D, int *ovf, float *part, hipStream_t s,
-                       const SplitIn &sp = SplitIn(), bool defer_colsum = false);
+                       const SplitIn &sp = SplitIn(), bool defer_colsum = false, bool ref_formula = false);
 // Ordered column sums of per-block partial rows: out[j] += sum_r part[r * n + j], r ascending
 // in the fixed grouping of colsum_kernel, for several independent jobs in one launch.
 struct ColsumJob {

@@ -27,7 +27,7 @@ OVF_SITES = ("norm_fwd", "qkv", "h13", "swiglu", "dlogits", "norm_bwd", "dh13", 
 EXPORTS = (
     "ne_create", "ne_destroy", "ne_last_error", "ne_sync", "ne_num_tensors", "ne_tensor_numel",
     "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_overlap_weight_grads", "ne_optimizer_step",
-    "ne_zero_grads",
+    "ne_rmsnorm_bwd_formula", "ne_zero_grads",
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
@@ -108,6 +108,7 @@ def lib():
         "ne_train_step": (I, [P, P, F, P]),
         "ne_use_graphs": (I, [P, I]),
         "ne_overlap_weight_grads": (I, [P, I]),
+        "ne_rmsnorm_bwd_formula": (I, [P, I]),
         "ne_optimizer_step": (I, [P, F, F, F, F, F, F, F, P]),
         "ne_zero_grads": (I, [P]),
         "ne_grad_scale_info": (I, [P, C.POINTER(C.c_float), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
@@ -264,6 +265,11 @@ class Model:
 
     def overlap_weight_grads(self, on=True):
         check(lib().ne_overlap_weight_grads(self._h, int(on)), "overlap_weight_grads")
+
+    def rmsnorm_bwd_formula(self, ref=True):
+        """ref=True: the reference's RMSNorm backward (extra gain factor on the projection
+        term, TD/cpu_ops.h:108-261); False: the exact gradient (default)."""
+        check(lib().ne_rmsnorm_bwd_formula(self._h, int(ref)), "rmsnorm_bwd_formula")
 
     def set_vocab_map(self, ids):
         """Vocabulary compaction: classifier + softmax over these embedding rows (None: all)."""

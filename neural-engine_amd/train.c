@@ -11,7 +11,9 @@
  * data file (vocabulary compaction, TD/cpu_ops.h:384-431, TD/train.m:286-292).
  *
  * Differences, all on purpose: weights, gradients and Adam state live on the GPU and never
- * cross to the host during training; the RMSNorm backward is the exact gradient.
+ * cross to the host during training; the RMSNorm backward is the exact gradient
+ * (--rmsnorm-bwd-ref selects the reference's formula, TD/cpu_ops.h:146-153, 188-189, 255-256,
+ * for runs that must follow a reference run).
  * Extensions: --full-vocab runs the full-vocabulary softmax instead of the compaction,
  * --tokens32 reads int32 token ids (uint16 cannot hold Qwen3's vocabulary), --qk-norm and
  * --rope-theta select Qwen3's per-head QK-RMSNorm and RoPE base, --ckpt overrides the
@@ -90,7 +92,7 @@ int main(int argc, char *argv[]) {
   const float loss_scale = 256.0f;
   const float res_alpha = 1.0f / sqrtf(2.0f * NLAYERS);
   const float min_lr_frac = 0.1f;
-  int do_resume = 0, from_scratch = 0, tokens32 = 0, qk_norm = QK_NORM, bf16 = 0, full_vocab = 0;
+  int do_resume = 0, from_scratch = 0, tokens32 = 0, qk_norm = QK_NORM, bf16 = 0, full_vocab = 0, norm_ref = 0;
   float rope_theta = ROPE_THETA;
   const char *data_path = DEFAULT_DATA_PATH;
   const char *ckpt_path = CKPT_PATH;
@@ -109,6 +111,7 @@ int main(int argc, char *argv[]) {
     else if (strcmp(argv[i], "--tokens32") == 0) tokens32 = 1;
     else if (strcmp(argv[i], "--bf16") == 0) bf16 = 1;
     else if (strcmp(argv[i], "--full-vocab") == 0) full_vocab = 1;
+    else if (strcmp(argv[i], "--rmsnorm-bwd-ref") == 0) norm_ref = 1;
   }
   if (accum_steps < 1) accum_steps = 1;
   float lr = max_lr;
@@ -123,6 +126,11 @@ int main(int argc, char *argv[]) {
   ne_ctx *ctx = ne_create(&cfg);
   if (!ctx) {
     printf("ERROR: ne_create: %s\n", ne_last_error());
+    return 1;
+  }
+  if (norm_ref && ne_rmsnorm_bwd_formula(ctx, 1) != 0) {
+    printf("ERROR: ne_rmsnorm_bwd_formula: %s\n", ne_last_error());
+    ne_destroy(ctx);
     return 1;
   }
   const double create_ms = now_ms() - t_create;

@@ -22,7 +22,8 @@ TD = ane-training/training/training_dynamic):
                           compact embedding gradient is scattered back to its rows
 * RMSNorm bwd             exact gradient of TD/cpu_ops.h:20-60 (the reference's
                           TD/cpu_ops.h:108-261 carries an extra gain factor on the
-                          projection term; identical while gains are 1.0)
+                          projection term; identical while gains are 1.0); that formula
+                          as an option (backward(norm_bwd_ref=True))
 * grad scale/norm/clip    TD/train.m:785-849
 * LR schedule             TD/train.m:851-858
 * AdamW                   TD/cpu_ops.h:266-303, wd=0 for norm gains (TD/train.m:861-897)
@@ -170,11 +171,19 @@ def rmsnorm(x, w, eps):
     return ((x / rms) * w).astype(F32), (F32(1.0) / rms).astype(F32)
 
 
-def rmsnorm_bwd(dy, x, w, r):
-    """Exact gradient of y = x*r*w, r = (mean(x^2)+eps)^-1/2.  Returns (dx, dw)."""
+def rmsnorm_bwd(dy, x, w, r, ref: bool = False):
+    """Exact gradient of y = x*r*w, r = (mean(x^2)+eps)^-1/2.  Returns (dx, dw).
+
+    ref=True gives the reference's formula instead (TD/cpu_ops.h:146-153, 188-189 rmsnorm_bwd;
+    255-256 rmsnorm_bwd_add, whose residual the caller adds here): dot = sum(dy*x*w)*r^2/D,
+    dx = (dy - x*dot)*r*w.  Its projection term carries one more factor w than the exact
+    gradient; the two agree at w = 1.  dw (TD/cpu_ops.h:153, 192) is the same under both."""
     D = x.shape[-1]
     dot = np.sum(dy * x * w, axis=-1, keepdims=True, dtype=F32)
-    dx = r * (w * dy) - x * (r * r * r) * dot / F32(D)
+    if ref:
+        dx = (dy - x * (dot * (r * r) / F32(D))) * r * w
+    else:
+        dx = r * (w * dy) - x * (r * r * r) * dot / F32(D)
     dw = np.sum((dy * x * r).reshape(-1, D), axis=0, dtype=F32)
     return dx.astype(F32), dw.astype(F32)
 
@@ -320,8 +329,11 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
     return loss, cache
 
 
-def backward(cfg: Config, P: dict, cache: dict) -> dict:
-    """Analytic fp32 backward of forward(); returns grads keyed like P (loss_scale included)."""
+def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> dict:
+    """Analytic fp32 backward of forward(); returns grads keyed like P (loss_scale included).
+
+    norm_bwd_ref: the attention, FFN and final RMSNorms use the reference's backward formula
+    (rmsnorm_bwd(ref=True); TD/train.m:527, 603, 751); the QK-norms stay exact."""
     B, S = cache["B"], cache["S"]
     D, NH, NKV, HD = cfg.dim, cfg.n_heads, cfg.kv_heads, cfg.head_dim
     r_gqa = cfg.gqa_ratio
@@ -340,7 +352,7 @@ def backward(cfg: Config, P: dict, cache: dict) -> dict:
     else:                                                 # vocab_scatter_grads, TD/cpu_ops.h:425-431
         G["embed"][ids] += dE_cls
         dxf = dlog @ P["embed"][ids]
-    dx, dg = rmsnorm_bwd(dxf, cache["xL"], P["rms_final"], cache["rf"])
+    dx, dg = rmsnorm_bwd(dxf, cache["xL"], P["rms_final"], cache["rf"], norm_bwd_ref)
     G["rms_final"] += dg
 
     for l in reversed(range(cfg.n_layers)):
@@ -359,7 +371,7 @@ def backward(cfg: Config, P: dict, cache: dict) -> dict:
         G[g("W1")] += (dh1.reshape(B * S, -1).T @ x2n).astype(F32)
         G[g("W3")] += (dh3.reshape(B * S, -1).T @ x2n).astype(F32)
         dx2n = dh1 @ p("W1") + dh3 @ p("W3")
-        dxr, dg = rmsnorm_bwd(dx2n, c["x2"], p("rms_ffn"), c["r2"])
+        dxr, dg = rmsnorm_bwd(dx2n, c["x2"], p("rms_ffn"), c["r2"], norm_bwd_ref)
         G[g("rms_ffn")] += dg
         dx2 = (dx + dxr).astype(F32)
         # attention
@@ -397,7 +409,7 @@ def backward(cfg: Config, P: dict, cache: dict) -> dict:
         G[g("Wk")] += (dk.T @ xn).astype(F32)
         G[g("Wv")] += (dvf.T @ xn).astype(F32)
         dxn = (dq @ p("Wq") + dk @ p("Wk") + dvf @ p("Wv")).reshape(B, S, D)
-        dxr, dg = rmsnorm_bwd(dxn, c["x_in"], p("rms_att"), c["r1"])
+        dxr, dg = rmsnorm_bwd(dxn, c["x_in"], p("rms_att"), c["r1"], norm_bwd_ref)
         G[g("rms_att")] += dg
         dx = (dx2 + dxr).astype(F32)
 

@@ -97,6 +97,40 @@ def test_resume_one_step_matches_oracle(tmp_path, compact):
         assert float(np.mean(d > 0.5 * lr)) <= 0.05, n
 
 
+def test_resume_reference_norm_formula(tmp_path):
+    """--rmsnorm-bwd-ref: a checkpoint with trained (non-unit) gains, one step; the first Adam
+    moment (the clipped gradient) follows the oracle's reference-formula backward and not the
+    exact one."""
+    cfg = tiny_cfg()
+    P = om.init_params(cfg, seed=0, std=0.02)
+    rng = np.random.default_rng(3)
+    for n in P:
+        if om.is_gain(n):
+            P[n] = (1 + 0.5 * rng.standard_normal(P[n].shape)).astype(np.float32)
+    Z = {k: np.zeros_like(v) for k, v in P.items()}
+    ck = str(tmp_path / "ck.bin")
+    ock.write(ck, cfg, P, Z, Z, step=99, total_steps=100, lr=3e-4, loss=0.0)
+    data = write_data(tmp_path / "data.bin", cfg, n_ids=300)
+    ids = om.vocab_map_build(data, cfg.vocab)
+    run_cli(["--resume", "--ckpt", ck, "--data", str(tmp_path / "data.bin"), "--accum", "1", "--warmup", "1",
+             "--lr", "3e-4", "--rmsnorm-bwd-ref"], tmp_path)
+    (pos,) = od.window_positions(len(data), cfg.seq, 99, 1)
+    tok = data[pos:pos + cfg.seq + 1].astype(np.int32)[None]
+    _, cache = om.forward(cfg, P, tok, loss_scale=256.0, vocab_ids=ids)
+    lr = om.lr_at(99, 3e-4, 1, 100)
+    Mo = {}
+    for ref in (True, False):
+        M = {k: np.zeros_like(v) for k, v in P.items()}
+        V = {k: np.zeros_like(v) for k, v in P.items()}
+        om.optimizer_step({k: v.copy() for k, v in P.items()}, om.backward(cfg, P, cache, norm_bwd_ref=ref), M, V,
+                          1, lr, grad_scale=1 / 256, clip=1.0)
+        Mo[ref] = M
+    _, _, Mg, _ = ock.read(ck)
+    for n in P:
+        assert rel_l2(Mg[n], Mo[True][n]) <= 1e-2, n
+    assert max(rel_l2(Mg[n], Mo[False][n]) for n in P) > 5e-2
+
+
 def test_scratch_init_and_dashboard_lines(tmp_path):
     """--scratch: srand48(42) uniform init of TD/train.m:236-251 (kept exact by lr 0), 100
     accumulated micro-steps, one update, checkpoint at step 100; stdout in the reference's

@@ -59,6 +59,41 @@ def test_train_step_matches_oracle(case, dtype):
     m.close()
 
 
+@pytest.mark.parametrize("dtype", [ne.NE_FP16, ne.NE_BF16])
+def test_reference_norm_formula_step_matches_oracle(dtype):
+    """ne_rmsnorm_bwd_formula: with trained (non-unit) gains the step follows the oracle's
+    reference-formula backward when switched on and the exact one when switched off again; the
+    one-stream step replays a captured graph, so the switch must drop it."""
+    cfg = om.tiny(**CASES["qwen3"])
+    P = om.init_params(cfg, seed=0, std=0.02)
+    rng = np.random.default_rng(3)
+    for n in P:
+        if om.is_gain(n):
+            P[n] = (1 + 0.5 * rng.standard_normal(P[n].shape)).astype(np.float32)
+    tok = om.tokens_for_step(cfg, 2, cfg.seq, seed=1)
+    print(f"\n[dtype {dtype}] tiny qwen3 model B=2 S={cfg.seq}, gains 1 +- 0.5", flush=True)
+    m = ne.Model.from_oracle(cfg, batch=2, dtype=dtype)
+    m.set_params(P)
+    m.overlap_weight_grads(False)
+    Pm = as_multiplied(P, dtype)
+    lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0)
+    for ref in (False, True, False):
+        m.rmsnorm_bwd_formula(ref)
+        m.zero_grads()
+        loss = m.train_step(tok, 256.0)
+        G = m.get_all(shapes(cfg), ne.NE_GRAD)
+        Go = om.backward(cfg, Pm, cache, norm_bwd_ref=ref)
+        Gx = om.backward(cfg, Pm, cache, norm_bwd_ref=not ref)
+        assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
+        worst = max((rel_l2(G[n], Go[n]) / grad_tol(n, dtype), n) for n in P)
+        other = max((rel_l2(G[n], Gx[n]) / grad_tol(n, dtype), n) for n in P)
+        print(f"  ref={ref}: worst grad rel-L2 / tol {worst[0]:.2f} ({worst[1]}); "
+              f"against the other formula {other[0]:.2f} ({other[1]})", flush=True)
+        assert worst[0] <= 1.0, worst
+        assert other[0] > 1.0, other
+    m.close()
+
+
 def test_step_with_ragged_vocab_tiles():
     """A vocabulary that is not a multiple of 256 (65,664 = 256.5 tiles) with 256 tokens: the
     classifier / CE GEMMs and the embedding-gradient GEMM take tiles that divide it.  A store

@@ -178,6 +178,79 @@ def test_backward_matches_float64_autograd(kw):
         assert rel_l2(G[n], TG[n]) < 2e-4, n
 
 
+def _ref_rmsnorm_bwd_loops(dy, x, w, resid=None):
+    """The reference's rmsnorm_bwd / rmsnorm_bwd_add as its scalar loops run them, on its
+    channel-major [d, S] layout, in float64 (TD/cpu_ops.h:108-192, 198-261): ss and dot over
+    channels, rrms recomputed from x with eps 1e-5, dot scaled by rrms^2/d, then per channel
+    tmp = (dy - x*dot)*rrms, dx = tmp*w (+ residual), dw += sum_s dy*x*rrms."""
+    d, S = x.shape
+    ss = [0.0] * S
+    dot = [0.0] * S
+    for i in range(d):
+        for s in range(S):
+            ss[s] += float(x[i, s]) * float(x[i, s])
+            dot[s] += float(dy[i, s]) * float(x[i, s]) * float(w[i])
+    rrms = [1.0 / math.sqrt(ss[s] / d + 1e-5) for s in range(S)]
+    dot = [dot[s] * rrms[s] * rrms[s] / d for s in range(S)]
+    dx = np.zeros((d, S))
+    dw = np.zeros(d)
+    for i in range(d):
+        for s in range(S):
+            tmp = (float(dy[i, s]) - float(x[i, s]) * dot[s]) * rrms[s]
+            dx[i, s] = tmp * float(w[i]) + (float(resid[i, s]) if resid is not None else 0.0)
+            dw[i] += float(dy[i, s]) * float(x[i, s]) * rrms[s]
+    return dx, dw
+
+
+def test_rmsnorm_bwd_reference_formula_matches_reference_loops():
+    """backward's norm_bwd_ref option (the reference's formula) against the reference's loops
+    on the transposed layout, with and without the fused residual; and at unit gains both
+    formulas agree (the exact one is pinned by autograd above)."""
+    rng = np.random.default_rng(21)
+    S, d = 5, 12
+    x = rng.standard_normal((S, d)).astype(np.float32)
+    dy = rng.standard_normal((S, d)).astype(np.float32)
+    res = rng.standard_normal((S, d)).astype(np.float32)
+    w = (1 + 0.4 * rng.standard_normal(d)).astype(np.float32)
+    _, r = om.rmsnorm(x, w, 1e-5)
+    dx, dw = om.rmsnorm_bwd(dy, x, w, r, ref=True)
+    for resid in (None, res):
+        want, want_dw = _ref_rmsnorm_bwd_loops(dy.T, x.T, w, None if resid is None else resid.T)
+        got = dx + (0 if resid is None else resid)
+        np.testing.assert_allclose(got, want.T, rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(dw, want_dw, rtol=1e-5, atol=1e-6)
+    # the gain placement matters: with non-unit gains the exact gradient differs
+    dx_exact, dw_exact = om.rmsnorm_bwd(dy, x, w, r)
+    assert rel_l2(dx_exact, dx) > 1e-2
+    np.testing.assert_array_equal(dw_exact, dw)
+    one = np.ones(d, np.float32)
+    _, r1 = om.rmsnorm(x, one, 1e-5)
+    np.testing.assert_allclose(om.rmsnorm_bwd(dy, x, one, r1, ref=True)[0], om.rmsnorm_bwd(dy, x, one, r1)[0],
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_backward_reference_norm_formula_threads_through_the_model():
+    """norm_bwd_ref reaches the final, FFN and attention norms: equal to the exact backward at
+    unit gains; with trained gains the final gain's gradient (above every norm) is unchanged
+    and the gradients below it move."""
+    cfg = om.tiny(qk_norm=True, dim=64, hidden=128, head_dim=16, vocab=97)
+    P = om.init_params(cfg, seed=5, std=0.1)
+    tok = om.tokens_for_step(cfg, 2, 12, seed=4)
+    _, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    G0, G1 = om.backward(cfg, P, cache), om.backward(cfg, P, cache, norm_bwd_ref=True)
+    for n in P:
+        assert rel_l2(G1[n], G0[n]) < 1e-5, n
+    rng = np.random.default_rng(9)
+    for n in P:
+        if om.is_gain(n):
+            P[n] = (1 + 0.3 * rng.standard_normal(P[n].shape)).astype(np.float32)
+    _, cache = om.forward(cfg, P, tok, loss_scale=256.0)
+    G0, G1 = om.backward(cfg, P, cache), om.backward(cfg, P, cache, norm_bwd_ref=True)
+    np.testing.assert_array_equal(G1["rms_final"], G0["rms_final"])
+    for n in ("layers.1.W1", "layers.1.rms_ffn", "layers.1.Wq", "layers.0.rms_att", "embed"):
+        assert rel_l2(G1[n], G0[n]) > 1e-3, n
+
+
 def test_compact_vocab_backward_matches_float64_autograd():
     """Vocab compaction (TD/cpu_ops.h:384-431): classifier over the ids present in the data,
     gradient scattered back to those embedding rows; pinned by autograd of the sub-matrix."""
