@@ -316,6 +316,132 @@ __global__ __launch_bounds__(WV * 64) void gemv_mfma_kernel(const h16_t *__restr
   }
 }
 
+// ------------------------------------------- GEMV, batch 5..32, bf16 weights, exact ----
+
+// x = hi + mid + lo, three bf16 values obtained by truncation: hi keeps the top 8 significant
+// bits of x, mid the next 8 of the remainder x - hi, lo what is left, so the sum is exact and
+// each product of a bf16 weight with a part is exact in fp32.
+__device__ __forceinline__ void split3(float x, uint16_t &hi, uint16_t &mid, uint16_t &lo) {
+  const uint32_t u = __float_as_uint(x) & 0xFFFF0000u;
+  const float r1 = x - __uint_as_float(u);
+  const uint32_t u1 = __float_as_uint(r1) & 0xFFFF0000u;
+  const float r2 = r1 - __uint_as_float(u1);
+  hi = (uint16_t)(u >> 16);
+  mid = (uint16_t)(u1 >> 16);
+  lo = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+enum { BF3_WS = 0, BF3_GATE = 1, BF3_PLAIN = 2 };
+
+// Products of bf16 weight rows W [N, K] with fp32 x rows [Bp, K] (row stride ldx) on
+// v_mfma_f32_16x16x32_bf16: each x value is split into three bf16 parts (split3) and every
+// weight fragment meets the three, so the sums are of the exact products (fp32 accumulation,
+// as the fp32-MFMA GEMV).  A block has 4 * NTW waves: wave w takes batch tile w / 4 (16
+// sequences) and K slice w % 4 of the block's K range (KS steps of 32), holds that slice of x
+// as bf16 parts in registers for all its RT row tiles of 16 weight rows, and the four K
+// slices are summed in LDS in slice order.  x is read once per block for RT * 16 rows
+// (the 16-row fp32-MFMA GEMV reads it once per 16 rows, 4x its weight bytes at batch 32).
+//  BF3_WS:    split blockIdx.y's sums to ws slice [blockIdx.y][Bp, N] (every sequence row);
+//  BF3_GATE:  W = [W1; W3] (gate_n rows each), one split: row tiles 0..RT/2-1 are W1 rows
+//             j0 + 16 rt.., the rest the same rows of W3; writes out[b, j] = silu(h1) * h3
+//             (generate.py:190) for b < B;
+//  BF3_PLAIN: one split, out[b, n] = sums for b < B (the LM head's logits).
+template <int NTW, int RT, int KS, int MODE>
+__global__ __launch_bounds__(NTW * 256) void gemv_bf3_kernel(const h16_t *__restrict__ W, long ldw,
+                                                             const float *__restrict__ x, long ldx,
+                                                             float *__restrict__ out, long ldo, int N, int B,
+                                                             int Bp, long gate_n) {
+  __shared__ f32x4 red[3][NTW][RT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ksl = w & 3, t = w >> 2;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int kb = (blockIdx.y * 4 + ksl) * KS * 32 + g * 8;  // this lane's k in step 0
+  constexpr int HALF = RT / 2;
+  auto wrow = [&](int rt) -> long {
+    if constexpr (MODE == BF3_GATE) {
+      const long j = (long)blockIdx.x * 16 * HALF + (rt % HALF) * 16 + r16;
+      return rt < HALF ? j : gate_n + j;
+    } else {
+      return (long)blockIdx.x * 16 * RT + rt * 16 + r16;
+    }
+  };
+  // the weight stream first: every fragment of the wave in flight at once
+  u16x8 wf[RT][KS];
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+    const h16_t *wr = W + wrow(rt) * ldw + kb;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) wf[rt][ks] = __builtin_nontemporal_load((const u16x8 *)(wr + ks * 32));
+  }
+  const int b = t * 16 + r16;
+  u16x8 xh[KS], xm[KS], xl[KS];
+  {
+    const float *xr = x + (long)b * ldx + kb;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      const float4 a0 = *(const float4 *)(xr + ks * 32), a1 = *(const float4 *)(xr + ks * 32 + 4);
+      const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        uint16_t h, m, l;
+        split3(v[e], h, m, l);
+        xh[ks][e] = h; xm[ks][e] = m; xl[ks][e] = l;
+      }
+    }
+  }
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+    acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      const bf16x8 a = H16B::op(wf[rt][ks]);
+      acc[rt] = H16B::mfma16(a, H16B::op(xh[ks]), acc[rt]);
+      acc[rt] = H16B::mfma16(a, H16B::op(xm[ks]), acc[rt]);
+      acc[rt] = H16B::mfma16(a, H16B::op(xl[ks]), acc[rt]);
+    }
+  }
+  // acc[rt][i] = sum over this K slice for weight row (tile rt) 4g + i, sequence b
+  if (ksl > 0) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) red[ksl - 1][t][rt][lane] = acc[rt];
+  }
+  __syncthreads();
+  if (ksl != 0) return;
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+#pragma unroll
+    for (int q = 0; q < 3; q++) acc[rt] += red[q][t][rt][lane];
+  }
+  if constexpr (MODE == BF3_WS) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+      const long n = (long)blockIdx.x * 16 * RT + rt * 16 + g * 4;
+      *(f32x4 *)(out + ((long)blockIdx.y * Bp + b) * N + n) = acc[rt];
+    }
+  } else if constexpr (MODE == BF3_GATE) {
+    if (b < B) {
+#pragma unroll
+      for (int rt = 0; rt < HALF; rt++) {
+        float4 o;
+        float *op = &o.x;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float h1 = acc[rt][i], h3 = acc[rt + HALF][i];
+          op[i] = h1 * (1.f / (1.f + expf(-h1))) * h3;
+        }
+        *(float4 *)(out + (long)b * ldo + (long)blockIdx.x * 16 * HALF + rt * 16 + g * 4) = o;
+      }
+    }
+  } else {
+    if (b < B) {
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++)
+        *(f32x4 *)(out + (long)b * ldo + (long)blockIdx.x * 16 * RT + rt * 16 + g * 4) = acc[rt];
+    }
+  }
+}
+
 // One block per sequence b: out[b, :] = alpha * (ordered sum of the split-K partials, split 0
 // first) + resid[b, :], and (gn != null) xn[b, :] = out[b, :] / rms * gn, the RMSNorm of the
 // new row (generate.py:81-84, rms = sqrt(mean(out^2) + eps)) that the next GEMV reads.
@@ -860,6 +986,90 @@ int gemv_big(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, lon
   return 0;
 }
 
+// Batch 5..32 with bf16 weights: the GEMV on gemv_bf3_kernel when its shape allows (returns
+// 1 after launching; 0: not applicable, nothing launched).  mode BF3_WS: the split-K partials
+// go to d->ws and *nz receives the split count; BF3_GATE: W = [W1; W3] (N rows each), gate
+// [Bp, N] -> out; BF3_PLAIN: out [Bp, ldo] = products.
+int gemv_bf3(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, long ldx, int mode, float *out,
+             long ldo, int *nz) {
+  Dec *d = (Dec *)c->dec;
+  if (c->dt != NE_BF16 || K % 128) return 0;
+  int ks = 0, rt = 2, ksplit = 1;
+  if (mode == BF3_WS) {
+    for (int cand : {2, 3, 1})
+      if (K % (128 * cand) == 0 && K / (128 * cand) <= 8) {
+        ks = cand;
+        break;
+      }
+    if (!ks) return 0;
+    ksplit = K / (128 * ks);
+    rt = (N % 64 == 0 && (N / 64) * ksplit >= 192) ? 4 : 2;
+    if (N % (16 * rt) || (long)ksplit * d->Bp * N > d->ws_elems) return 0;
+  } else {
+    ks = K / 128;
+    if (ks != 1 && ks != 6 && ks != 8) return 0;
+    if (N % (mode == BF3_GATE ? 16 : 32)) return 0;
+  }
+  const int ntw = d->Bp / 16;
+  const dim3 grid(mode == BF3_GATE ? N / 16 : N / (16 * rt), ksplit);
+  float *dst = mode == BF3_WS ? d->ws : out;
+  const long ldd = mode == BF3_WS ? N : ldo;
+  bool done = false;
+  auto go = [&](auto kernel, int nt) {
+    hipLaunchKernelGGL(kernel, grid, dim3(nt * 256), 0, c->st, W, (long)K, x, ldx, dst, ldd, N, B, d->Bp, (long)N);
+    done = true;
+  };
+#define NE_BF3(NTW_)                                                                                 \
+  if (mode == BF3_WS) {                                                                              \
+    if (rt == 4 && ks == 2) go(gemv_bf3_kernel<NTW_, 4, 2, BF3_WS>, NTW_);                           \
+    else if (rt == 4 && ks == 3) go(gemv_bf3_kernel<NTW_, 4, 3, BF3_WS>, NTW_);                      \
+    else if (rt == 4 && ks == 1) go(gemv_bf3_kernel<NTW_, 4, 1, BF3_WS>, NTW_);                      \
+    else if (rt == 2 && ks == 2) go(gemv_bf3_kernel<NTW_, 2, 2, BF3_WS>, NTW_);                      \
+    else if (rt == 2 && ks == 3) go(gemv_bf3_kernel<NTW_, 2, 3, BF3_WS>, NTW_);                      \
+    else if (rt == 2 && ks == 1) go(gemv_bf3_kernel<NTW_, 2, 1, BF3_WS>, NTW_);                      \
+  } else if (mode == BF3_GATE) {                                                                     \
+    if (ks == 8) go(gemv_bf3_kernel<NTW_, 2, 8, BF3_GATE>, NTW_);                                    \
+    else if (ks == 6) go(gemv_bf3_kernel<NTW_, 2, 6, BF3_GATE>, NTW_);                               \
+    else go(gemv_bf3_kernel<NTW_, 2, 1, BF3_GATE>, NTW_);                                            \
+  } else {                                                                                           \
+    if (ks == 8) go(gemv_bf3_kernel<NTW_, 2, 8, BF3_PLAIN>, NTW_);                                   \
+    else if (ks == 6) go(gemv_bf3_kernel<NTW_, 2, 6, BF3_PLAIN>, NTW_);                              \
+    else go(gemv_bf3_kernel<NTW_, 2, 1, BF3_PLAIN>, NTW_);                                           \
+  }
+  if (ntw == 1) {
+    NE_BF3(1)
+  } else {
+    NE_BF3(2)
+  }
+#undef NE_BF3
+  if (!done) return 0;
+  NE_CHECK(ne_hip_status(hipGetLastError(), "decode gemv (bf16 parts)"));
+  if (nz) *nz = ksplit;
+  return 1;
+}
+
+// Wo / W2 on gemv_bf3_kernel with the split-K sum, residual and RMSNorm of gemv_big's
+// workspace form (gemv_reduce_rows_kernel); returns 0 when not applicable.
+int gemv_bf3_resid(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, long ldx, float *out, long ldo,
+                   const float *resid, float alpha, const float *gn, float *xn) {
+  Dec *d = (Dec *)c->dec;
+  int ks = 0;
+  const int rc = gemv_bf3(c, B, W, N, K, x, ldx, BF3_WS, nullptr, 0, &ks);
+  if (rc <= 0) return rc;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(B), dim3(256), 0, c->st, d->ws, ks, d->Bp, N, out, ldo, resid, alpha, gn, xn,
+                       c->c.norm_eps);
+  };
+  if (N > 1024) go(gemv_reduce_rows_kernel<0>);
+  else if (ks == 1) go(gemv_reduce_rows_kernel<1>);
+  else if (ks == 2) go(gemv_reduce_rows_kernel<2>);
+  else if (ks == 4) go(gemv_reduce_rows_kernel<4>);
+  else if (ks == 8) go(gemv_reduce_rows_kernel<8>);
+  else go(gemv_reduce_rows_kernel<0>);
+  NE_CHECK(ne_hip_status(hipGetLastError(), "decode gemv reduce"));
+  return 1;
+}
+
 // qkv: the q|k|v rows [Bp, QKV], or (qnz > 1) qnz split-K partial slices of them.
 int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const float *qkv, int qnz) {
   Dec *d = (Dec *)c->dec;
@@ -914,7 +1124,9 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
       NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->qkv, 1));
     } else {
       int qnz = 0;
-      NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, D, d->ws, cap, nullptr, 0, nullptr, 1.f, &qnz));
+      int rc = gemv_bf3(c, B, Pb + o.wqkv, QKV, D, d->xn, D, BF3_WS, nullptr, 0, &qnz);
+      if (rc < 0) return rc;
+      if (!rc) NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, D, d->ws, cap, nullptr, 0, nullptr, 1.f, &qnz));
       NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->ws, qnz));
     }
     if (small) {
@@ -925,11 +1137,20 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
       NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.w2, D, H, d->xn, H, nullptr, d->x, D, d->x, alpha));
     } else {
       const float *g_next = l + 1 < c->L ? Pf + c->lo[l + 1].g_att : Pf + c->off_gfinal;
-      NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, Q, d->ws, cap, d->x, D, d->x, alpha, nullptr, Pf + o.g_ffn,
-                        d->xn));
-      NE_CHECK(gemv_big(c, B, Pb + o.w13, H, D, d->xn, D, nullptr, 0, d->gate, H, nullptr, 1.f, nullptr, nullptr,
-                        nullptr, true));
-      NE_CHECK(gemv_big(c, B, Pb + o.w2, D, H, d->gate, H, d->ws, cap, d->x, D, d->x, alpha, nullptr, g_next, d->xn));
+      int rc = gemv_bf3_resid(c, B, Pb + o.wo, D, Q, d->att, Q, d->x, D, d->x, alpha, Pf + o.g_ffn, d->xn);
+      if (rc < 0) return rc;
+      if (!rc)
+        NE_CHECK(gemv_big(c, B, Pb + o.wo, D, Q, d->att, Q, d->ws, cap, d->x, D, d->x, alpha, nullptr, Pf + o.g_ffn,
+                          d->xn));
+      rc = gemv_bf3(c, B, Pb + o.w13, H, D, d->xn, D, BF3_GATE, d->gate, H, nullptr);
+      if (rc < 0) return rc;
+      if (!rc)
+        NE_CHECK(gemv_big(c, B, Pb + o.w13, H, D, d->xn, D, nullptr, 0, d->gate, H, nullptr, 1.f, nullptr, nullptr,
+                          nullptr, true));
+      rc = gemv_bf3_resid(c, B, Pb + o.w2, D, H, d->gate, H, d->x, D, d->x, alpha, g_next, d->xn);
+      if (rc < 0) return rc;
+      if (!rc)
+        NE_CHECK(gemv_big(c, B, Pb + o.w2, D, H, d->gate, H, d->ws, cap, d->x, D, d->x, alpha, nullptr, g_next, d->xn));
     }
   }
   if (gen) {
@@ -940,7 +1161,9 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
         hipLaunchKernelGGL(dec_argmax_kernel, dim3(B), dim3(1024), 0, c->st, d->amv, d->ami, V / (4 * pick_rpw(V)),
                            d->st, d->ctx, d->tok, d->out);
     } else {
-      NE_CHECK(gemv_big(c, B, Pb + c->off_E, V, D, d->xn, D, nullptr, 0, d->logits, V, nullptr, 1.f, nullptr));
+      const int rc = gemv_bf3(c, B, Pb + c->off_E, V, D, d->xn, D, BF3_PLAIN, d->logits, V, nullptr);
+      if (rc < 0) return rc;
+      if (!rc) NE_CHECK(gemv_big(c, B, Pb + c->off_E, V, D, d->xn, D, nullptr, 0, d->logits, V, nullptr, 1.f, nullptr));
       if (greedy) {
         hipLaunchKernelGGL(dec_argmax_part_kernel, dim3(BIG_ARGMAX, B), dim3(256), 0, c->st, d->logits, V, BIG_ARGMAX,
                            d->amv, d->ami);
