@@ -1009,6 +1009,9 @@ int gemv_bf3(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, lon
     ks = K / 128;
     if (ks != 1 && ks != 6 && ks != 8) return 0;
     if (N % (mode == BF3_GATE ? 16 : 32)) return 0;
+    // the LM head: 128 rows per block (x read once per 128 rows: 1.61 -> 1.57 ms per batch-32
+    // position against 32)
+    if (mode == BF3_PLAIN && N % 128 == 0) rt = 8;
   }
   const int ntw = d->Bp / 16;
   const dim3 grid(mode == BF3_GATE ? N / 16 : N / (16 * rt), ksplit);
@@ -1031,6 +1034,10 @@ int gemv_bf3(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *x, lon
     if (ks == 8) go(gemv_bf3_kernel<NTW_, 2, 8, BF3_GATE>, NTW_);                                    \
     else if (ks == 6) go(gemv_bf3_kernel<NTW_, 2, 6, BF3_GATE>, NTW_);                               \
     else go(gemv_bf3_kernel<NTW_, 2, 1, BF3_GATE>, NTW_);                                            \
+  } else if (rt == 8) {                                                                              \
+    if (ks == 8) go(gemv_bf3_kernel<NTW_, 8, 8, BF3_PLAIN>, NTW_);                                   \
+    else if (ks == 6) go(gemv_bf3_kernel<NTW_, 8, 6, BF3_PLAIN>, NTW_);                              \
+    else go(gemv_bf3_kernel<NTW_, 8, 1, BF3_PLAIN>, NTW_);                                           \
   } else {                                                                                           \
     if (ks == 8) go(gemv_bf3_kernel<NTW_, 2, 8, BF3_PLAIN>, NTW_);                                   \
     else if (ks == 6) go(gemv_bf3_kernel<NTW_, 2, 6, BF3_PLAIN>, NTW_);                              \
