@@ -676,8 +676,10 @@ int bwd_hd(const AttnArgs &a, hipStream_t s) {
   if (a.part && a.NH != a.NKV) {
     hipLaunchKernelGGL((attn_bwd_kernel<HT, HD, NW, RG, true>), grid, dim3(NW * 64), 0, s, a, nblk, a.NH);
     NE_HIP(hipGetLastError());
-    const long n4 = (long)a.B * a.S * a.NKV * HD / 4;
-    hipLaunchKernelGGL(gqa_reduce_kernel<HT>, dim3((int)std::min<long>((n4 + 255) / 256, 4096)), dim3(256), 0, s, a);
+    if (!a.defer_gqa) {
+      const long n4 = (long)a.B * a.S * a.NKV * HD / 4;
+      hipLaunchKernelGGL(gqa_reduce_kernel<HT>, dim3((int)std::min<long>((n4 + 255) / 256, 4096)), dim3(256), 0, s, a);
+    }
   } else {
     hipLaunchKernelGGL((attn_bwd_kernel<HT, HD, NW, RG, false>), grid, dim3(NW * 64), 0, s, a, nblk, a.NKV);
   }

@@ -525,13 +525,34 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
     const float *__restrict__ cosb, const float *__restrict__ sinb, const float *__restrict__ gq,
     const float *__restrict__ gk, const float *__restrict__ rq, const float *__restrict__ rk,
     h16_t *__restrict__ dqkv, float *__restrict__ dgq, float *__restrict__ dgk, float dg_scale, int T,
-    int S, int NH, int NKV, int HD, int tok_per_block, int *ovf, float *__restrict__ part) {
+    int S, int NH, int NKV, int HD, int tok_per_block, int *ovf, float *__restrict__ part,
+    const float *__restrict__ kvpart, int *ovf_v) {
   bool bad = false;
   __shared__ float red[256 * 2];
   const int half = HD / 2;
   const int i = threadIdx.x % half;
   const int sub = threadIdx.x / half, nsub = 256 / half;
   const int h = blockIdx.y;
+  const int ratio = NH / NKV;
+  if (h >= NH + NKV) {
+    // dV of kv head h - NH - NKV: the head-order sum of its query heads' partials (kvpart's
+    // second half), rounded to 16 bits into dqkv's v columns
+    const int kvh = h - NH - NKV;
+    const float *pv = kvpart + (long)T * NH * HD;
+    const long t0 = (long)blockIdx.x * tok_per_block, t1 = min((long)T, t0 + tok_per_block);
+    for (long t = t0 + sub; t < t1; t += nsub) {
+      float2 sv = make_float2(0.f, 0.f);
+      for (int r = 0; r < ratio; r++) {
+        const float2 y = *(const float2 *)(pv + t * NH * HD + (long)(kvh * ratio + r) * HD + 2 * i);
+        sv.x += y.x; sv.y += y.y;
+      }
+      const h16_t o0 = HT::h(sv.x), o1 = HT::h(sv.y);
+      bad |= HT::bad(o0) | HT::bad(o1);
+      *(uint32_t *)(dqkv + t * ld + (long)(NH + NKV) * HD + (long)kvh * HD + 2 * i) = (uint32_t)o0 | ((uint32_t)o1 << 16);
+    }
+    flag_overflow(ovf_v, bad);
+    return;
+  }
   const bool isq = h < NH;
   const int hh = isq ? h : h - NH;
   const long col = (isq ? 0 : (long)NH * HD) + (long)hh * HD + 2 * i;
@@ -545,8 +566,18 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
   const long t0 = (long)blockIdx.x * tok_per_block;
   const long t1 = min((long)T, t0 + tok_per_block);
   for (long t = t0 + sub; t < t1; t += nsub) {
-    const float *d = isq ? dq + t * (long)NH * HD + (long)hh * HD : dk + t * (long)NKV * HD + (long)hh * HD;
-    const float2 dd = *(const float2 *)(d + 2 * i);
+    float2 dd;
+    if (isq) {
+      dd = *(const float2 *)(dq + t * (long)NH * HD + (long)hh * HD + 2 * i);
+    } else if (kvpart) {  // dK: the head-order sum of the query heads' partials
+      dd = make_float2(0.f, 0.f);
+      for (int r = 0; r < ratio; r++) {
+        const float2 y = *(const float2 *)(kvpart + t * (long)NH * HD + (long)(hh * ratio + r) * HD + 2 * i);
+        dd.x += y.x; dd.y += y.y;
+      }
+    } else {
+      dd = *(const float2 *)(dk + t * (long)NKV * HD + (long)hh * HD + 2 * i);
+    }
     const int pos = t % S;
     const float c = cosb[pos * half + i], s = sinb[pos * half + i];
     float d0 = dd.x * c + dd.y * s;
@@ -709,14 +740,15 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk, float dg_scale,
                        int T, int S, int NH, int NKV, int HD, int *ovf, float *part, hipStream_t s,
-                       bool defer_colsum) {
+                       bool defer_colsum, const float *kvpart, int *ovf_v) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
+  if (kvpart && (ld % 2 || NH % NKV)) return ne_fail(NE_ERR_ARG, "qk_prep: bad layout for the dK/dV partials");
   const int tpb = qk_tpb(T);
   const int nbx = (T + tpb - 1) / tpb;
-  dim3 grid(nbx, NH + NKV);
+  dim3 grid(nbx, NH + NKV + (kvpart ? NKV : 0));
   NE_CHECK(DISPATCH_H16(dt, [&] {
-    if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part);
-    else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part);
+    if (gq) hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, true>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part, kvpart, ovf_v);
+    else hipLaunchKernelGGL((qk_prep_bwd_kernel<HT, false>), grid, dim3(256), 0, s, dq, dk, qkv, ld, cosb, sinb, gq, gk, rq, rk, dqkv, dgq, dgk, dg_scale, T, S, NH, NKV, HD, tpb, ovf, part, kvpart, ovf_v);
     return ne_hip_status(hipGetLastError(), "qk_prep_bwd");
   }()));
   if (gq && part && !defer_colsum) {

@@ -706,13 +706,14 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
       at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = dqkv + Q + KV; at.lddv = QKV;
       at.part = c->NH != c->NKV ? c->attn_part : nullptr;
+      at.defer_gqa = at.part != nullptr;  // the QK-prep backward sums the per-query-head dK/dV
       at.ovf = ovf + OVF_DV;
       NE_CHECK(launch_attn_bwd(dt, at, c->st));
       NE_CHECK(launch_qk_prep_bwd(dt, c->dq, c->dk, a.qkv, QKV, c->cosb, c->sinb, c->c.qk_norm ? P + o.gq : nullptr,
                                   c->c.qk_norm ? P + o.gk : nullptr, a.rq, a.rk, dqkv,
                                   c->c.qk_norm ? G + o.gq : nullptr, c->c.qk_norm ? G + o.gk : nullptr, u, T, S,
                                   c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->c.qk_norm ? qk_part(c, l) : nullptr,
-                                  c->st, true));
+                                  c->st, true, at.part, ovf + OVF_DV));
     }
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
     NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));

@@ -130,7 +130,8 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
                        const float *cosb, const float *sinb, const float *gq, const float *gk,
                        const float *rq, const float *rk, h16_t *dqkv, float *dgq, float *dgk,
                        float dg_scale, int T, int S, int NH, int NKV, int HD, int *ovf, float *part,
-                       hipStream_t s, bool defer_colsum = false);
+                       hipStream_t s, bool defer_colsum = false, const float *kvpart = nullptr,
+                       int *ovf_v = nullptr);
 
 // ---- attention (k_attn.hip): causal, GQA kv head = q head / (NH/NKV) ----
 struct AttnArgs {
@@ -147,6 +148,8 @@ struct AttnArgs {
   h16_t *dv; long lddv;          // [T, NKV*HD] 16-bit
   float *part;                   // nullable: [2][T, NH*HD] fp32 per-query-head dK/dV partials
                                  // (GQA only: one block per query head, then a head-order sum)
+  bool defer_gqa;                // with part: leave the per-query-head dK/dV partials in part
+                                 // (launch_qk_prep_bwd with kvpart sums them; dk, dv unwritten)
   SplitIn dsp;                   // split-K partials of dout (its GEMM's reduction, done by the
                                  // delta kernel, which writes dout); dsp.n = 0: dout is written
   int *ovf_dout;                 // overflow flag of dout's 16-bit rounding (with dsp)
