@@ -347,6 +347,24 @@ def test_decode_sampling_mfma_path():
     m.close()
 
 
+@pytest.mark.parametrize("B", [6, 32])
+def test_decode_stories_widths_batched(B):
+    """Stories110M widths (dim 768, hidden 2048, 12 heads of 64, vocab 32000; two layers) with
+    bf16 weights at batch 6 and 32: the batched GEMVs split K = 768 and 2048 three and eight
+    ways, and the SwiGLU gate and the LM head take K = 768 in one split."""
+    cfg = om.stories110m(n_layers=2)
+    P = _held_params(cfg, ne.NE_BF16, std=0.05)
+    prompt = np.random.default_rng(30 + B).integers(0, cfg.vocab, (B, 4)).astype(np.int32)
+    print(f"\n[B={B}] stories widths, 2 layers", flush=True)
+    m = ne.Model.from_oracle(cfg, decode_batch=B, decode_ctx=32, dtype=ne.NE_BF16)
+    m.set_params(P)
+    got = m.decode(prompt, 12)
+    want, margins, _ = om.decode(cfg, P, prompt, 12, return_logits=True)
+    print(f"  min top-2 margin {margins.min():.3e}")
+    np.testing.assert_array_equal(got, want)
+    m.close()
+
+
 @pytest.mark.parametrize("compact", [False, True])
 def test_step_identical_across_launch_modes(compact):
     """The step gives bit-identical losses and gradients over two accumulating micro-steps
