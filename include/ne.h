@@ -233,6 +233,16 @@ int ne_k_rmsnorm_bwd(int dtype, const float *dy, const float *x, const float *g,
 int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, const void *A, int64_t lda,
               const void *B, int64_t ldb, void *C, int64_t ldc, const void *R, int64_t ldr,
               float alpha, void *stream);
+/* The weight-gradient GEMMs of one layer as one launch: C_p[M_p,N_p] fp32 (= or, with
+ * accumulate, +=) alpha * A_p^T.B_p for p < n (n <= 4), A_p[K,M_p] (row pitch lda[p]) and
+ * B_p[K,N_p] (ldb[p]) 16-bit, on 256x256 tiles each over the whole K range (no split-K).  Only
+ * for shapes the step runs this way: every M_p and N_p a multiple of 256, K >= 8192 and a
+ * multiple of 64, at least 192 tiles in all (else NE_ERR_ARG).  Replaces the per-layer
+ * cblas_sgemm weight gradients of TD/train.m:554-738 that the reference runs on its
+ * concurrent dispatch queue. */
+int ne_k_gemm_wgrad_group(int dtype, int n, const int *M, const int *N, int K, const void *const *A,
+                          const int64_t *lda, const void *const *B, const int64_t *ldb, float *const *C,
+                          int accumulate, float alpha, void *stream);
 /* Per-head QK-RMSNorm (gq/gk NULL: off) + interleaved RoPE of the q and k column blocks of
  * qkv [T, ld] at positions t % S with fp32 tables cos/sin [S, HD/2]; writes qr, kr and the
  * norm factors rq [T,NH], rk [T,NKV].  TD/mil_dynamic.h:133-169. */

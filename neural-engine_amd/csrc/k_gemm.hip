@@ -161,8 +161,9 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
 // lane for EPI_CE_FWD); they take KM_EVEN or KM_PAD.
 enum { KM_TAIL = 0, KM_EVEN = 1, KM_PAD = 2 };
 
+// One output tile (mt, nt) of split kz: the body of the plain and the grouped kernel.
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI, int KMODE>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const int nt, const int kz) {
   constexpr int NTHREADS = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
@@ -178,36 +179,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  // Tile order.  Work-groups go to the NX = 8 XCDs round-robin (work-group w to XCD w % 8),
-  // and each XCD has its own L2.  The tiles are laid out in grouped order (groups of GM M
-  // tiles, the M tiles of a group in turn for each N tile, so consecutive tiles share a B
-  // tile and a group's A tiles recur), and XCD x takes one contiguous stretch of that
-  // sequence: the M tiles that share a B tile run on the same XCD and find it in its L2, as
-  // do the recurring A tiles.  (Handing consecutive tiles to different XCDs made every XCD
-  // fetch each B tile: 4x the weight bytes for a 256-token forward GEMM.)  GM = 4: a group's
-  // A tiles (4 x 512 KB at K = 1024) stay in the 4 MB L2 beside the streaming B tiles; 8 did
-  // not fit, and the 16k-token step ran 1.2% slower with it.
-  constexpr int GM = 4, NX = 8;
-  int mt, nt;
-  {
-    const int num_m = gridDim.y, num_n = gridDim.x;
-    const int T = num_m * num_n;
-    const int pid = blockIdx.y * num_n + blockIdx.x;
-    const int x = pid % NX, q = T / NX, rem = T % NX;
-    const int u = x * q + min(x, rem) + pid / NX;  // a bijection of [0, T)
-    const int grp = u / (GM * num_n), first_m = grp * GM;
-    const int gsz = min(num_m - first_m, GM);
-    const int r = u - grp * GM * num_n;
-    mt = first_m + r % gsz;
-    nt = r / gsz;
-  }
   const int n0 = nt * BN, m0 = mt * BM;
   const h16_t *A = (const h16_t *)g.A;
   const h16_t *B = (const h16_t *)g.B;
   // K steps of this split: [kt0, kt1)
   const int nkt = g.K / BK;
-  const int kt0 = (int)((long)nkt * blockIdx.z / g.split);
-  const int kt1 = (int)((long)nkt * (blockIdx.z + 1) / g.split);
+  const int kt0 = (int)((long)nkt * kz / g.split);
+  const int kt1 = (int)((long)nkt * (kz + 1) / g.split);
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -334,8 +312,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     return;
   }
 
-  if (g.split > 1) {  // fp32 partial tile -> workspace slice blockIdx.z
-    float *ws = g.ws + (long)blockIdx.z * g.M * g.N;
+  if (g.split > 1) {  // fp32 partial tile -> workspace slice kz
+    float *ws = g.ws + (long)kz * g.M * g.N;
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -435,6 +413,55 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
     }
   }
   flag_overflow(g.ovf, bad);
+}
+
+// Tile order.  Work-groups go to the 8 XCDs round-robin (work-group w to XCD w % 8), and
+// each XCD has its own L2.  The tiles are laid out in grouped order (groups of GM M tiles,
+// the M tiles of a group in turn for each N tile, so consecutive tiles share a B tile and a
+// group's A tiles recur), and XCD x takes one contiguous stretch of that sequence: the M
+// tiles that share a B tile run on the same XCD and find it in its L2, as do the recurring A
+// tiles.  (Handing consecutive tiles to different XCDs made every XCD fetch each B tile: 4x
+// the weight bytes for a 256-token forward GEMM.)  GM = 4: a group's A tiles (4 x 512 KB at
+// K = 1024) stay in the 4 MB L2 beside the streaming B tiles; 8 did not fit, and the
+// 16k-token step ran 1.2% slower with it.
+//
+// xcd_stretch: the position in the launch's tile sequence of work-group pid of T (a
+// bijection of [0, T)); grouped_tile: tile u of an num_m x num_n output in grouped order.
+__device__ __forceinline__ int xcd_stretch(int pid, int T) {
+  constexpr int NX = 8;
+  const int x = pid % NX, q = T / NX, rem = T % NX;
+  return x * q + min(x, rem) + pid / NX;
+}
+
+__device__ __forceinline__ void grouped_tile(int u, int num_m, int num_n, int &mt, int &nt) {
+  constexpr int GM = 4;
+  const int grp = u / (GM * num_n), first_m = grp * GM;
+  const int gsz = min(num_m - first_m, GM);
+  const int r = u - grp * GM * num_n;
+  mt = first_m + r % gsz;
+  nt = r / gsz;
+}
+
+template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI, int KMODE>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
+  const int num_m = gridDim.y, num_n = gridDim.x;
+  int mt, nt;
+  grouped_tile(xcd_stretch(blockIdx.y * num_n + blockIdx.x, num_m * num_n), num_m, num_n, mt, nt);
+  gemm_body<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KMODE>(g, mt, nt, blockIdx.z);
+}
+
+// Several GEMMs of one shape class in one launch (the weight gradients of a layer): problem
+// p owns the work-groups [first[p], first[p + 1]) of the tile sequence, which the XCDs take
+// in contiguous stretches as above.  No split-K: each tile runs its whole K range.
+template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_group_kernel(GemmGroup gg) {
+  const int u = xcd_stretch(blockIdx.x, gg.first[gg.n]);
+  int p = 0;
+  while (p + 1 < gg.n && u >= gg.first[p + 1]) p++;
+  const GemmArgs &g = gg.g[p];
+  int mt, nt;
+  grouped_tile(u - gg.first[p], g.M / BM, g.N / BN, mt, nt);
+  gemm_body<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KM_TAIL>(g, mt, nt, 0);
 }
 
 // Ordered sum of the split-K partials (split 0 first) followed by the epilogue; four
@@ -578,6 +605,43 @@ int gemm_ce_tiles(int M, int N, int K) {
   const int nm = ragged_main(M, N, K);
   if (!nm) return N / tile_bn(gemm_tile(M, N, K));
   return nm / 256 + (N - nm) / tile_bn(gemm_tile(M, N - nm, K));
+}
+
+bool gemm_group_fits(const GemmArgs *g, int n) {
+  if (n < 1 || n > GEMM_GROUP_MAX) return false;
+  long tiles = 0;
+  for (int i = 0; i < n; i++) {
+    if (g[i].M <= 0 || g[i].N <= 0 || g[i].M % 256 || g[i].N % 256 || g[i].K < 8192 || g[i].K % 64) return false;
+    tiles += (long)(g[i].M / 256) * (g[i].N / 256);
+  }
+  return tiles >= 192 && tiles < (1L << 30);
+}
+
+int gemm_group_launch(int dt, int epi, const GemmArgs *g, int n, hipStream_t s) {
+  if (!gemm_group_fits(g, n)) return ne_fail(NE_ERR_ARG, "gemm group: shapes do not take the grouped path");
+  if (epi != EPI_F32 && epi != EPI_F32_ACC) return ne_fail(NE_ERR_ARG, "gemm group: epilogue %d", epi);
+  if (dt != 0 && dt != 1) return ne_fail(NE_ERR_ARG, "gemm: unknown 16-bit format %d", dt);
+  GemmGroup gg = {};
+  gg.n = n;
+  gg.first[0] = 0;
+  for (int i = 0; i < n; i++) {
+    if ((g[i].lda % 8) || (g[i].ldb % 8) || (((uintptr_t)g[i].A | (uintptr_t)g[i].B) & 15))
+      return ne_fail(NE_ERR_ARG, "gemm: operands need 16-byte aligned rows (ld %% 8 == 0)");
+    gg.g[i] = g[i];
+    gg.g[i].split = 1;
+    gg.g[i].n_tiles = g[i].N / 256;
+    gg.first[i + 1] = gg.first[i] + (g[i].M / 256) * (g[i].N / 256);
+  }
+  const dim3 grid(gg.first[n]), block(512);
+  if (dt == 0) {
+    if (epi == EPI_F32) hipLaunchKernelGGL((gemm_group_kernel<H16B, 256, 256, 64, 4, 2, false, false, EPI_F32>), grid, block, 0, s, gg);
+    else hipLaunchKernelGGL((gemm_group_kernel<H16B, 256, 256, 64, 4, 2, false, false, EPI_F32_ACC>), grid, block, 0, s, gg);
+  } else {
+    if (epi == EPI_F32) hipLaunchKernelGGL((gemm_group_kernel<H16F, 256, 256, 64, 4, 2, false, false, EPI_F32>), grid, block, 0, s, gg);
+    else hipLaunchKernelGGL((gemm_group_kernel<H16F, 256, 256, 64, 4, 2, false, false, EPI_F32_ACC>), grid, block, 0, s, gg);
+  }
+  NE_HIP(hipGetLastError());
+  return 0;
 }
 
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {

@@ -57,6 +57,21 @@ extern "C" int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, co
   return gemm_launch(dtype, layout, epi, g, S(stream));
 }
 
+extern "C" int ne_k_gemm_wgrad_group(int dtype, int n, const int *M, const int *N, int K, const void *const *A,
+                                     const int64_t *lda, const void *const *B, const int64_t *ldb,
+                                     float *const *C, int accumulate, float alpha, void *stream) {
+  CHECK_DT(dtype);
+  if (n < 1 || n > GEMM_GROUP_MAX || !M || !N || !A || !lda || !B || !ldb || !C)
+    return ne_fail(NE_ERR_ARG, "ne_k_gemm_wgrad_group: n = %d (1..%d) or a NULL array", n, GEMM_GROUP_MAX);
+  GemmArgs g[GEMM_GROUP_MAX] = {};
+  for (int i = 0; i < n; i++) {
+    g[i].M = M[i]; g[i].N = N[i]; g[i].K = K;
+    g[i].A = A[i]; g[i].lda = lda[i]; g[i].B = B[i]; g[i].ldb = ldb[i]; g[i].C = C[i]; g[i].ldc = N[i];
+    g[i].alpha = alpha;
+  }
+  return gemm_group_launch(dtype, accumulate ? EPI_F32_ACC : EPI_F32, g, n, S(stream));
+}
+
 extern "C" int ne_k_qk_prep_fwd(int dtype, const void *qkv, int64_t ld, const float *cosb, const float *sinb,
                                 const float *gq, const float *gk, void *qr, void *kr, float *rq, float *rk,
                                 int T, int S, int NH, int NKV, int HD, float eps, void *stream) {

@@ -142,10 +142,11 @@ int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h
   return gemm_launch(c->dt, GEMM_TN, epi, g, side ? c->st2 : c->st);
 }
 
-// Weight-gradient GEMMs of the backward.  With `on`, they are queued and handed to st2 in
-// batches: flush() makes st2 wait for everything enqueued on st so far (inside a stream
-// capture, a graph edge) and enqueues the batch there; join() makes st wait for st2.
-// Without, each runs at once, in order, on st (per-kernel-family event timing records on st).
+// Weight-gradient GEMMs of the backward, queued and run in batches by flush().  With `on`,
+// the batches go to st2: flush() makes st2 wait for everything enqueued on st so far (inside a
+// stream capture, a graph edge) and enqueues the batch there; join() makes st wait for st2.
+// Without, a batch runs in order on st where flush() is called (per-kernel-family event
+// timing records on st).
 // Also queued: the sum of squares of a finished part of G into its partial slots (sumsq()).
 struct WgradQueue {
   struct Job {
@@ -163,7 +164,6 @@ struct WgradQueue {
     return gemm_dw(c, side, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u);
   }
   int push(const Job &j) {
-    if (!on) return run(j, false);
     jobs.push_back(j);
     return 0;
   }
@@ -174,17 +174,45 @@ struct WgradQueue {
   int sumsq(const float *g, long n, long slot, int nparts, const float *g2 = nullptr, long n2 = 0) {
     return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, n, nparts, c->gn_part + slot, g2, n2});
   }
-  int flush() {
-    if (!on || jobs.empty()) return 0;
-    NE_HIP(hipEventRecord(c->ev_fork, c->st));
-    NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
-    for (const Job &j : jobs) NE_CHECK(run(j, true));
+  // Consecutive GEMM jobs with one epilogue, K and scale that gemm_group_fits (a long step's
+  // weight gradients of a layer) run as one launch without split-K, in both schedules, so the
+  // two give the same sums.
+  int run_batch(bool side) {
+    for (size_t i = 0; i < jobs.size();) {
+      size_t e = i;
+      GemmArgs ga[GEMM_GROUP_MAX];
+      while (e < jobs.size() && e - i < (size_t)GEMM_GROUP_MAX && jobs[e].M > 0 && jobs[e].epi == jobs[i].epi &&
+             jobs[e].K == jobs[i].K && jobs[e].u == jobs[i].u) {
+        const Job &j = jobs[e];
+        GemmArgs &g = ga[e - i];
+        g = GemmArgs();
+        g.M = j.M; g.N = j.N; g.K = j.K;
+        g.A = j.dY; g.lda = j.ldy; g.B = j.X; g.ldb = j.ldx; g.C = j.C; g.ldc = j.N;
+        g.alpha = j.u;
+        e++;
+      }
+      if (e - i >= 2 && gemm_group_fits(ga, (int)(e - i))) {
+        ProfScope ps(c, jobs[i].fam);
+        NE_CHECK(gemm_group_launch(c->dt, jobs[i].epi, ga, (int)(e - i), side ? c->st2 : c->st));
+        i = e;
+      } else {
+        NE_CHECK(run(jobs[i], side));
+        i++;
+      }
+    }
     jobs.clear();
     return 0;
   }
+  int flush() {
+    if (jobs.empty()) return 0;
+    if (!on) return run_batch(false);
+    NE_HIP(hipEventRecord(c->ev_fork, c->st));
+    NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
+    return run_batch(true);
+  }
   int join() {
-    if (!on) return 0;
     NE_CHECK(flush());
+    if (!on) return 0;
     NE_HIP(hipEventRecord(c->ev_join, c->st2));
     NE_HIP(hipStreamWaitEvent(c->st, c->ev_join, 0));
     return 0;

@@ -67,6 +67,15 @@ struct GemmArgs {
   int part_ld;               // EPI_CE_FWD: partial slots per row (0: N / BN)
 };
 
+// Up to GEMM_GROUP_MAX GEMMs run as one launch (gemm_group_launch): problem p's tiles are
+// the work-groups [first[p], first[p + 1]).
+constexpr int GEMM_GROUP_MAX = 4;
+struct GemmGroup {
+  GemmArgs g[GEMM_GROUP_MAX];
+  int first[GEMM_GROUP_MAX + 1];
+  int n;
+};
+
 // Split-K partials of a GEMM whose reduction is folded into its consumer: element e of the
 // result is base[e] + alpha * sum_{z < n} part[z * slice + e] (z ascending, the order of the
 // GEMM's own reduction).  n = 0: no partials.
@@ -82,6 +91,13 @@ struct SplitIn {
 // split, C is not written and the partials stay in a.ws (M*N floats per split).
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
 int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per row it writes
+// Weight-gradient GEMMs (layout TN, fp32 out: EPI_F32 or EPI_F32_ACC, one epilogue for all)
+// of n <= GEMM_GROUP_MAX problems as one launch of 256x256 tiles, each over its whole K range
+// (no split-K, no workspace).  gemm_group_fits: whether a set of shapes takes this path (every
+// M and N a multiple of 256, K >= 8192, and at least 192 tiles in all: a long reduction into
+// outputs that alone would need split-K to fill the CUs).
+bool gemm_group_fits(const GemmArgs *g, int n);
+int gemm_group_launch(int dt, int epi, const GemmArgs *g, int n, hipStream_t s);
 // Measurement kernel: MFMA chains without memory traffic (shape 0 = 32x32x16, 1 = 16x16x32).
 int launch_mfma_ceiling(int dt, int shape, int blocks, int iters, float *out, hipStream_t s);
 

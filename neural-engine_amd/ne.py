@@ -31,7 +31,7 @@ EXPORTS = (
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
-    "ne_k_gemm", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
+    "ne_k_gemm", "ne_k_gemm_wgrad_group", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
     "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
 )
@@ -126,6 +126,7 @@ def lib():
         "ne_k_rmsnorm_fwd": (I, [I, P, P, P, P, I, I, F, P]),
         "ne_k_rmsnorm_bwd": (I, [I, P, P, P, P, P, P, P, F, P, F, I, I, P]),
         "ne_k_gemm": (I, [I, I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
+        "ne_k_gemm_wgrad_group": (I, [I, I, P, P, I, P, P, P, P, P, I, F, P]),
         "ne_k_qk_prep_fwd": (I, [I, P, L, P, P, P, P, P, P, P, P, I, I, I, I, I, F, P]),
         "ne_k_qk_prep_bwd": (I, [I, P, P, P, L, P, P, P, P, P, P, P, P, P, F, I, I, I, I, I, P]),
         "ne_k_attn_fwd": (I, [I, P, L, P, L, P, L, P, L, P, I, I, I, I, I, F, P]),

@@ -2,6 +2,7 @@
 numpy oracle (oracle/model.py) and float64 numpy restatements of the same op, in both
 16-bit formats.  Tolerances scale with the format's unit roundoff u (fp16 2^-11, bf16 2^-8):
 a single rounding of the output gives rel-L2 ~ u/sqrt(3)."""
+import ctypes
 import math
 
 import numpy as np
@@ -47,6 +48,42 @@ def test_gemm_f32_layouts(fmt, layout, shape):
     ref = 0.5 * (A.astype(np.float64) @ B.astype(np.float64))
     err = np.abs(host(c) - ref).max() / np.abs(ref).max()
     assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_gemm_wgrad_group(fmt, accumulate):
+    """A layer's weight-gradient GEMMs of a 16k-token step as one launch (whole-K 256x256 tiles,
+    the problems' tiles in one grid): each C_p = alpha * A_p^T B_p (+ C_p) against a float64
+    product of the same 16-bit operands, and bit-identical to the same GEMM run alone through
+    ne_k_gemm (no split-K there either: the same K order for every output element)."""
+    dt, tdt, rnd, _ = FMT[fmt]
+    K = 8192
+    shapes = [(4096, 1024), (1024, 2048), (6144, 1024)]  # 64 + 32 + 96 tiles of 256x256
+    n = len(shapes)
+    rng = np.random.default_rng(7 + accumulate)
+    As = [dev(rnd(rng.standard_normal((K, M)).astype(np.float32)), tdt) for M, _ in shapes]
+    Bs = [dev(rnd(rng.standard_normal((K, N)).astype(np.float32)), tdt) for _, N in shapes]
+    C0 = [rng.standard_normal((M, N)).astype(np.float32) for M, N in shapes]
+    Cs = [dev(c) if accumulate else zeros(c.shape) for c in C0]
+    arr = lambda ct, xs: (ct * n)(*xs)
+    call(L.ne_k_gemm_wgrad_group, dt, n, arr(ctypes.c_int, [M for M, _ in shapes]),
+         arr(ctypes.c_int, [N for _, N in shapes]), K, arr(ctypes.c_void_p, [a.data_ptr() for a in As]),
+         arr(ctypes.c_int64, [M for M, _ in shapes]), arr(ctypes.c_void_p, [b.data_ptr() for b in Bs]),
+         arr(ctypes.c_int64, [N for _, N in shapes]), arr(ctypes.c_void_p, [c.data_ptr() for c in Cs]),
+         accumulate, 0.5, None)
+    for p, (M, N) in enumerate(shapes):
+        ref = 0.5 * (As[p].double().T @ Bs[p].double())
+        if accumulate:
+            ref += torch.as_tensor(C0[p], dtype=torch.float64, device="cuda")
+        ref = ref.cpu().numpy()
+        got = host(Cs[p])
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        assert err < 1e-5, (p, err)
+        alone = dev(C0[p]) if accumulate else zeros((M, N))
+        call(L.ne_k_gemm, dt, 3, 2 if accumulate else 1, M, N, K, ptr(As[p]), M, ptr(Bs[p]), N, ptr(alone), N,
+             None, 0, 0.5, None)
+        np.testing.assert_array_equal(host(alone), got, err_msg=f"problem {p}")
 
 
 @pytest.mark.parametrize("fmt", FMTS)

@@ -55,6 +55,23 @@ def test_kernel_entry_points_validate_shapes_before_launch():
     assert rc == -1
 
 
+def test_wgrad_group_refuses_shapes_off_its_path():
+    """The grouped weight-gradient GEMM takes only the long-step shapes (M, N multiples of 256,
+    K >= 8192, at least 192 tiles); anything else is refused on the host, before a launch."""
+    L = ne.lib()
+    n = 2
+    arr = lambda ct, xs: (ct * n)(*xs)
+    nul = arr(ctypes.c_void_p, [None, None])
+    lds = arr(ctypes.c_int64, [1024, 1024])
+    for M, N, K in [((4096, 6144), (1024, 1024), 4096), ((4096, 1024), (1024, 1024), 8192),
+                    ((4096, 6144), (1000, 1024), 8192)]:
+        rc = L.ne_k_gemm_wgrad_group(ne.NE_FP16, n, arr(ctypes.c_int, M), arr(ctypes.c_int, N), K, nul, lds, nul,
+                                     lds, nul, 0, 1.0, None)
+        assert rc == -1 and b"grouped path" in L.ne_last_error(), (M, N, K)
+    rc = L.ne_k_gemm_wgrad_group(ne.NE_FP16, 5, None, None, 8192, None, None, None, None, None, 0, 1.0, None)
+    assert rc == -1
+
+
 @pytest.mark.parametrize("qk", [False, True])
 def test_tensor_names_match_oracle_order(qk):
     cfg = om.tiny(qk_norm=qk)
