@@ -227,7 +227,9 @@ int ne_k_rmsnorm_bwd(int dtype, const float *dy, const float *x, const float *g,
 /* C = epi(alpha * A.B) on 16-bit MFMA.  layout 0: A[M,K] B[N,K] (forward, weights [out,in]);
  * 2: A[M,K] B[K,N] (input gradient); 3: A[K,M] B[K,N] (weight gradient).  epi 0: C 16-bit,
  * 1: C fp32, 2: C fp32 +=, 3: C fp32 = R fp32 + result, 4: SwiGLU backward (result =
- * dgate, R = h13 16-bit [M,2N], C = dh13 16-bit [M,2N]).  M, N, K multiples of 64.
+ * dgate, R = h13 16-bit [M,2N], C = dh13 16-bit [M,2N]), 7: SwiGLU forward (layout 0, B =
+ * [W1;W3] [N,K]: C = h13 16-bit [M,N] and R, written here, = gate silu(h1)*h3 16-bit [M,N/2];
+ * N a multiple of 128).  M, N, K multiples of 64.
  * Replaces the matmuls of TD/mil_dynamic.h:14-35, 57-234, 238-306, 320-576 and the
  * cblas_sgemm calls of TD/train.m:500-524, 554-738. */
 int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, const void *A, int64_t lda,

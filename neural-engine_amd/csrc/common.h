@@ -58,6 +58,18 @@ struct H16F {
   }
 };
 
+// SwiGLU gate silu(h1) * h3 of two 16-bit values, rounded to fp32 and then to 16 bits.  The
+// compiler may fuse the product and the 16-bit rounding into one mixed-precision FMA (a single
+// rounding), in some kernels and not in others; the empty asm holds the fp32 product in a
+// register so that every kernel computing the gate gets the same bits.
+template <typename HT>
+__device__ __forceinline__ h16_t swiglu_gate(h16_t a, h16_t b) {
+  const float h1 = HT::f(a), h3 = HT::f(b);
+  float g = h1 / (1.f + __expf(-h1)) * h3;
+  asm volatile("" : "+v"(g));
+  return HT::h(g);
+}
+
 // Dispatch a templated launcher on the runtime format id: DISPATCH_H16(dt, fn<HT>(args)).
 #define DISPATCH_H16(dt, ...)            \
   ((dt) == 1 ? [&] { using HT = H16F; return __VA_ARGS__; }() \

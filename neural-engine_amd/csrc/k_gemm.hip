@@ -73,6 +73,21 @@ struct Stage {
     }
   }
 
+  // K-contiguous rows from two places: tile rows [0, half) at lo + row * ld, the rest at
+  // hi + row * ld (lo and hi already offset to this tile's rows)
+  __device__ __forceinline__ void load_split(const h16_t *lo, const h16_t *hi, long ld, int half, int k0, int tid) {
+    static_assert(KC, "load_split: K-contiguous operand");
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int c = tid + i * NT;
+      if (NCH % NT == 0 || c < NCH) {
+        int row, col8;
+        idx(c, row, col8);
+        v[i] = *(const u16x8 *)((row < half ? lo : hi) + (long)row * ld + k0 + col8 * 8);
+      }
+    }
+  }
+
   __device__ __forceinline__ void zero() {
 #pragma unroll
     for (int i = 0; i < PER; i++) v[i] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -223,10 +238,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
   // Stage j of the split is loaded from K step kt0 + min(j, n - 1): the loads past the end
   // repeat the last step (valid memory, never computed), so the loop body has no branch and
   // one register allocation covers every split length.
+  // SwiGLU forward: the tile's first BN/2 B rows are W1 rows n0/2.., the rest the W3 rows of
+  // the same columns (B rows N/2 + n0/2..), so h1 and h3 of a column meet in one work-group
+  const h16_t *Blo = B + (long)(n0 / 2) * g.ldb, *Bhi = B + ((long)g.N / 2 + n0 / 2 - BN / 2) * g.ldb;
   auto load = [&](SA &a, SB &b, int j) {
     const int kt = kt0 + min(j, n - 1);
     a.load(A, g.lda, m0, kt * BK, tid);
-    b.load(B, g.ldb, n0, kt * BK, tid);
+    if constexpr (EPI == EPI_SWIGLU_FWD) b.load_split(Blo, Bhi, g.ldb, BN / 2, kt * BK, tid);
+    else b.load(B, g.ldb, n0, kt * BK, tid);
     if constexpr (KMODE == KM_PAD)
       if (j >= n) a.zero();  // the padding step adds nothing
   };
@@ -309,6 +328,58 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
       p[0] = mx;
       p[1] = s;
     }
+    return;
+  }
+
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    // Wave column wn = 0 holds h1, wn = 1 h3 of the same output columns n0/2 + (local column)
+    // in the same lanes and registers (a wave's N extent is BN/2).  Each rounds its values to
+    // 16 bits and writes them to h13; the h3 waves pass theirs through LDS, and the h1 waves
+    // write the gate from the two 16-bit values, as a separate SwiGLU pass over h13 would.
+    static_assert(WN == 2 && TN * 2 == BN, "SwiGLU forward: two wave columns of BN/2");
+    static_assert(WM * FM * FN * 16 * 64 <= SA::ELEMS + SB::ELEMS, "SwiGLU forward: exchange fits an LDS buffer");
+    h16_t *xch = lds0;
+    h16_t *h13 = (h16_t *)g.C, *gate = (h16_t *)g.C2;
+    const int H = g.N / 2;
+    bool bad = false, badg = false;
+    lds_barrier();  // the last K step's fragment reads of lds0 are done
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int col = H + n0 / 2 + j * 32 + (lane & 31);
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const h16_t o = HT::h(acc[i][j][e] * alpha);
+            bad |= HT::bad(o);
+            h13[(long)row * g.ldc + col] = o;
+            xch[(((wm * FM + i) * FN + j) * 16 + e) * 64 + lane] = o;
+          }
+        }
+    }
+    lds_barrier();
+    if (wn == 0) {
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int col = n0 / 2 + j * 32 + (lane & 31);
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const h16_t o1 = HT::h(acc[i][j][e] * alpha), o3 = xch[(((wm * FM + i) * FN + j) * 16 + e) * 64 + lane];
+            bad |= HT::bad(o1);
+            h13[(long)row * g.ldc + col] = o1;
+            const h16_t og = swiglu_gate<HT>(o1, o3);
+            badg |= HT::bad(og);
+            gate[(long)row * g.ldc2 + col] = og;
+          }
+        }
+    }
+    flag_overflow(g.ovf, bad);
+    flag_overflow(g.ovf2, badg);
     return;
   }
 
@@ -518,7 +589,7 @@ int launch_t(GemmArgs g, hipStream_t s) {
   }
   NE_HIP(hipGetLastError());
   if (g.split > 1 && !g.defer_reduce) {
-    if constexpr (EPI != EPI_CE_FWD && EPI != EPI_CE_BWD) {
+    if constexpr (EPI != EPI_CE_FWD && EPI != EPI_CE_BWD && EPI != EPI_SWIGLU_FWD) {
       const long n4 = (long)g.M * g.N / 4;
       const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
       if (g.split == 2) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 2>), dim3(blocks), dim3(256), 0, s, g);
@@ -560,6 +631,9 @@ int launch_l(int epi, GemmArgs g, int tile, hipStream_t s) {
     case EPI_SWIGLU_BWD: return launch_e<HT, AKC, BKC, EPI_SWIGLU_BWD>(g, tile, s);
     case EPI_CE_FWD: return launch_e<HT, AKC, BKC, EPI_CE_FWD>(g, tile, s);
     case EPI_CE_BWD: return launch_e<HT, AKC, BKC, EPI_CE_BWD>(g, tile, s);
+    case EPI_SWIGLU_FWD:
+      if constexpr (AKC && BKC) return launch_e<HT, AKC, BKC, EPI_SWIGLU_FWD>(g, tile, s);
+      return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU forward epilogue takes layout 0 (A[M,K], B[N,K])");
   }
   return ne_fail(NE_ERR_ARG, "gemm: unknown epilogue %d", epi);
 }
@@ -644,6 +718,43 @@ int gemm_group_launch(int dt, int epi, const GemmArgs *g, int n, hipStream_t s) 
   return 0;
 }
 
+// Block tile and K splits of a shape (ws_elems < 0: no workspace, no split).  The cross-entropy
+// and SwiGLU-forward epilogues never split (they need whole sums in the tile).
+static void plan(int epi, int M, int N, int K, long ws_elems, int &tile, int &split) {
+  const bool nosplit_ok = epi != EPI_CE_FWD && epi != EPI_CE_BWD && epi != EPI_SWIGLU_FWD;
+  tile = gemm_tile(M, N, K);
+  // A long reduction into a small output (the weight gradients of a long step: K = tokens)
+  // takes the 256x256 tile too when split-K can give it a full wave of work-groups: its higher
+  // MFMA rate outweighs writing and summing the fp32 partials (a few % of the GEMM's time).
+  if (ws_elems >= 0 && nosplit_ok && tile != TILE_256 && M % 256 == 0 && N % 256 == 0 &&
+      K >= 8192) {
+    const long t256 = (long)(M / 256) * (N / 256);
+    int sp = 1;
+    while (t256 * sp < 256 && sp < 8 && (K / 64) / (sp * 2) >= 4 && (long)M * N * sp * 2 <= ws_elems) sp *= 2;
+    if (t256 * sp >= 256) tile = TILE_256;
+  }
+  // split K while too few work-groups would run (8-wave tiles: fewer than one per CU;
+  // 4-wave tiles: fewer than 3/4 of the CUs), keeping >= 4 K steps per split.  Each split
+  // adds an fp32 partial output to write and read back: at 256 tokens the partials of a
+  // layer's GEMMs outweighed its weights at two work-groups per CU (target 512: 8.84 ms per
+  // Qwen3-0.6B step, 256: 8.64, 192: 8.54, 128: 9.25).
+  split = 1;
+  if (ws_elems >= 0 && nosplit_ok) {
+    const long tiles = (long)(M / tile_bm(tile)) * (N / tile_bn(tile));
+    const long target = tile_bm(tile) == 256 ? 256 : 192;
+    const int nkt = K / 64;
+    while (tiles * split < target && nkt / (split * 2) >= 4 && split < 64 &&
+           (long)M * N * split * 2 <= ws_elems)
+      split *= 2;
+  }
+}
+
+int gemm_splits(int epi, int M, int N, int K, long ws_elems) {
+  int tile, split;
+  plan(epi, M, N, K, ws_elems, tile, split);
+  return split;
+}
+
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
     return ne_fail(NE_ERR_ARG, "gemm: M=%d N=%d K=%d must be positive multiples of 64", g.M, g.N, g.K);
@@ -654,8 +765,10 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
     return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU backward epilogue needs 16-byte aligned h13 / dh13 rows");
   if (epi == EPI_CE_BWD && ((g.ldc % 8) || ((uintptr_t)g.C & 15)))
     return ne_fail(NE_ERR_ARG, "gemm: the cross-entropy backward needs 16-byte aligned dlogits rows");
+  if (epi == EPI_SWIGLU_FWD && (!g.C || !g.C2 || g.ldc < g.N || g.ldc2 < g.N / 2 || g.N % 128))
+    return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU forward needs h13 [M,N] and gate [M,N/2] outputs, N %% 128 == 0");
   // ragged shapes: the main part of whole 256-wide tiles, then the rest (see ragged_main)
-  if (epi != EPI_SWIGLU_BWD && !g.defer_reduce) {
+  if (epi != EPI_SWIGLU_BWD && epi != EPI_SWIGLU_FWD && !g.defer_reduce) {
     const size_t ce = epi == EPI_H16 || epi == EPI_CE_BWD ? 2 : 4;  // C element size
     if (const int nm = ragged_main(g.M, g.N, g.K)) {  // split the columns
       GemmArgs a = g, b = g;
@@ -684,31 +797,9 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
         return gemm_launch(dt, layout, epi, b, s, nullptr);
       }
   }
-  int tile = gemm_tile(g.M, g.N, g.K);
-  // A long reduction into a small output (the weight gradients of a long step: K = tokens)
-  // takes the 256x256 tile too when split-K can give it a full wave of work-groups: its higher
-  // MFMA rate outweighs writing and summing the fp32 partials (a few % of the GEMM's time).
-  if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD && tile != TILE_256 && g.M % 256 == 0 && g.N % 256 == 0 &&
-      g.K >= 8192) {
-    const long t256 = (long)(g.M / 256) * (g.N / 256);
-    int sp = 1;
-    while (t256 * sp < 256 && sp < 8 && (g.K / 64) / (sp * 2) >= 4 && (long)g.M * g.N * sp * 2 <= g.ws_elems) sp *= 2;
-    if (t256 * sp >= 256) tile = TILE_256;
-  }
-  // split K while too few work-groups would run (8-wave tiles: fewer than one per CU;
-  // 4-wave tiles: fewer than 3/4 of the CUs), keeping >= 4 K steps per split.  Each split
-  // adds an fp32 partial output to write and read back: at 256 tokens the partials of a
-  // layer's GEMMs outweighed its weights at two work-groups per CU (target 512: 8.84 ms per
-  // Qwen3-0.6B step, 256: 8.64, 192: 8.54, 128: 9.25).
-  g.split = 1;
-  if (g.ws && epi != EPI_CE_FWD && epi != EPI_CE_BWD) {
-    const long tiles = (long)(g.M / tile_bm(tile)) * (g.N / tile_bn(tile));
-    const long target = tile_bm(tile) == 256 ? 256 : 192;
-    const int nkt = g.K / 64;
-    while (tiles * g.split < target && nkt / (g.split * 2) >= 4 && g.split < 64 &&
-           (long)g.M * g.N * g.split * 2 <= g.ws_elems)
-      g.split *= 2;
-  }
+  int tile, split;
+  plan(epi, g.M, g.N, g.K, g.ws ? g.ws_elems : -1, tile, split);
+  g.split = split;
   if (split_out) *split_out = g.split;
   return DISPATCH_H16(dt, launch_dt<HT>(layout, epi, g, tile, s));
 }

@@ -420,8 +420,7 @@ __global__ void swiglu_fwd_kernel(h16_t *__restrict__ h13, h16_t *__restrict__ g
     u16x4 o;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const float h1 = HT::f(a[j]), h3 = HT::f(b[j]);
-      o[j] = HT::h(h1 / (1.f + __expf(-h1)) * h3);
+      o[j] = swiglu_gate<HT>(a[j], b[j]);
       bad |= HT::bad(o[j]);
     }
     *(u16x4 *)(gate + e) = o;

@@ -48,12 +48,18 @@ extern "C" int ne_k_gemm(int dtype, int layout, int epi, int M, int N, int K, co
                          const void *B, int64_t ldb, void *C, int64_t ldc, const void *R, int64_t ldr,
                          float alpha, void *stream) {
   CHECK_DT(dtype);
-  if (epi == EPI_CE_FWD || epi == EPI_CE_BWD || epi < 0 || epi > EPI_CE_BWD)
+  if (epi == EPI_CE_FWD || epi == EPI_CE_BWD || epi < 0 || epi > EPI_SWIGLU_FWD)
     return ne_fail(NE_ERR_ARG, "ne_k_gemm: epilogue %d not available here (use ne_k_ce_*)", epi);
   GemmArgs g = {};
   g.M = M; g.N = N; g.K = K;
   g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.R = R; g.ldr = ldr;
   g.alpha = alpha;
+  if (epi == EPI_SWIGLU_FWD) {  // R is the gate output
+    g.C2 = const_cast<void *>(R);
+    g.ldc2 = ldr;
+    g.R = nullptr;
+    g.ldr = 0;
+  }
   return gemm_launch(dtype, layout, epi, g, S(stream));
 }
 

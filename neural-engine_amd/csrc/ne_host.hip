@@ -219,6 +219,29 @@ struct WgradQueue {
   }
 };
 
+// On short steps the W1|W3 GEMM writes the SwiGLU gate itself (one launch instead of the GEMM
+// and a pass over h13) when it would run unsplit: the same tile, sums and 16-bit roundings as
+// the two kernels, so the same h13 and gate bit for bit.  With split-K the SwiGLU kernel sums
+// the partials as before; on long steps (more than 2048 tokens) the separate pass, which
+// streams at full bandwidth, is cheaper than the gate work in the GEMM's epilogue, where the
+// waves of one work-group per CU all reach it together (16,384 tokens: 113.3 vs 114.3 ms per
+// Qwen3-0.6B step).
+bool swiglu_in_gemm(const ne_ctx *c) {
+  return c->T <= 2048 && (2 * c->H) % 128 == 0 && gemm_splits(EPI_H16, c->T, 2 * c->H, c->D, c->ws_elems) == 1;
+}
+
+int gemm_swiglu_fwd(ne_ctx *c, const h16_t *x2n, const h16_t *w13, h16_t *h13, h16_t *gate) {
+  ProfScope ps(c, NE_PROF_GEMM_FWD);
+  GemmArgs g = {};
+  g.M = c->T; g.N = 2 * c->H; g.K = c->D;
+  g.A = x2n; g.lda = c->D; g.B = w13; g.ldb = c->D;
+  g.C = h13; g.ldc = 2 * c->H; g.C2 = gate; g.ldc2 = c->H;
+  g.alpha = 1.f;
+  g.ovf = c->ovf + OVF_H13;
+  g.ovf2 = c->ovf + OVF_SWIGLU;
+  return gemm_launch(c->dt, GEMM_NT, EPI_SWIGLU_FWD, g, c->st);
+}
+
 // GEMM whose split-K reduction, when it splits, is left to the kernel that consumes C:
 // *sp then describes the partials in c->ws (C unwritten), else has n = 0 (C written).  C must
 // be [M, N] row-major with ldc = N; R (EPI_RESID) is the residual added after the sum.
@@ -645,9 +668,11 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_rmsnorm_fwd(dt, a.x2, P + o.g_ffn, a.x2n, a.r2, T, D, eps, ovf + OVF_NORM_FWD, c->st, sp_x));
     }
-    NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, &sp_h,
-                        nullptr, 1.f, ovf + OVF_H13));
-    {
+    if (swiglu_in_gemm(c)) {
+      NE_CHECK(gemm_swiglu_fwd(c, a.x2n, Pb + o.w13, a.h13, a.gate));
+    } else {
+      NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_H16, T, 2 * H, D, a.x2n, D, Pb + o.w13, D, a.h13, &sp_h,
+                          nullptr, 1.f, ovf + OVF_H13));
       ProfScope ps(c, NE_PROF_NORM);
       NE_CHECK(launch_swiglu_fwd(dt, a.h13, a.gate, T, H, ovf + OVF_SWIGLU, c->st, sp_h, ovf + OVF_H13));
     }

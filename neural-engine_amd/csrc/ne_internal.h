@@ -41,6 +41,7 @@ enum {
   EPI_SWIGLU_BWD = 4,  // result is dgate [M,N]; R = h13 16-bit [M,2N]; C = dh13 16-bit [M,2N]
   EPI_CE_FWD = 5,      // result is logits; writes per-(row, N-tile) max/sumexp + target logit
   EPI_CE_BWD = 6,      // C 16-bit = (exp(logit - lse) - onehot) * scale
+  EPI_SWIGLU_FWD = 7,  // B = [W1; W3] [N,K] (layout NT); C = h13 16-bit [M,N]; C2 = gate 16-bit [M,N/2]
 };
 
 struct GemmArgs {
@@ -56,6 +57,8 @@ struct GemmArgs {
   float *part;               // [M, n_tiles, 2] (EPI_CE_FWD): tile max, tile sum exp
   float *tgt_logit;          // [M] (EPI_CE_FWD)
   int *ovf;                  // 16-bit outputs: overflow flag (nullable)
+  void *C2; long ldc2;       // EPI_SWIGLU_FWD: the gate silu(h1) * h3
+  int *ovf2;                 // EPI_SWIGLU_FWD: the gate's overflow flag (nullable)
   float *ws;                 // split-K workspace (nullable: no split)
   long ws_elems;             // its capacity in floats
   int n_tiles;               // set by the launcher: N / BN
@@ -91,6 +94,8 @@ struct SplitIn {
 // split, C is not written and the partials stay in a.ws (M*N floats per split).
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
 int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per row it writes
+// K splits gemm_launch would use for this shape with a workspace of ws_elems floats (1: none).
+int gemm_splits(int epi, int M, int N, int K, long ws_elems);
 // Weight-gradient GEMMs (layout TN, fp32 out: EPI_F32 or EPI_F32_ACC, one epilogue for all)
 // of n <= GEMM_GROUP_MAX problems as one launch of 256x256 tiles, each over its whole K range
 // (no split-K, no workspace).  gemm_group_fits: whether a set of shapes takes this path (every

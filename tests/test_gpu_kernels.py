@@ -221,6 +221,30 @@ def test_swiglu_fwd(fmt):
     assert rel_l2(host(gate), ref) < u
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,H,D", [(256, 3072, 1024), (256, 2048, 768), (2048, 3072, 1024), (4096, 3072, 1024),
+                                   (128, 192, 256)])
+def test_gemm_swiglu_fwd_epilogue(fmt, T, H, D):
+    """The W1|W3 GEMM with the SwiGLU forward in its epilogue (B rows gathered so that h1 and h3
+    of a column share a work-group) writes the same h13 and gate, bit for bit, as the plain
+    16-bit GEMM followed by the SwiGLU kernel; the gate against silu(h1) * h3 of float64 sums."""
+    dt, tdt, rnd, u = FMT[fmt]
+    rng = np.random.default_rng(T + H)
+    x = rnd(rng.standard_normal((T, D)).astype(np.float32))
+    w13 = rnd((rng.standard_normal((2 * H, D)) / np.sqrt(D)).astype(np.float32))
+    xd, wd = dev(x, tdt), dev(w13, tdt)
+    h13, gate = zeros((T, 2 * H), tdt), zeros((T, H), tdt)
+    call(L.ne_k_gemm, dt, 0, 7, T, 2 * H, D, ptr(xd), D, ptr(wd), D, ptr(h13), 2 * H, ptr(gate), H, 1.0, None)
+    h13_ref, gate_ref = zeros((T, 2 * H), tdt), zeros((T, H), tdt)
+    call(L.ne_k_gemm, dt, 0, 0, T, 2 * H, D, ptr(xd), D, ptr(wd), D, ptr(h13_ref), 2 * H, None, 0, 1.0, None)
+    call(L.ne_k_swiglu_fwd, dt, ptr(h13_ref), ptr(gate_ref), T, H, None)
+    np.testing.assert_array_equal(host(h13), host(h13_ref))
+    np.testing.assert_array_equal(host(gate), host(gate_ref))
+    h = x.astype(np.float64) @ w13.astype(np.float64).T
+    ref = om.silu(h[:, :H]) * h[:, H:]
+    assert rel_l2(host(gate), ref) < 3 * u
+
+
 # -------------------------------------------------------------------- RoPE / QK-norm
 
 @pytest.mark.parametrize("fmt", FMTS)
