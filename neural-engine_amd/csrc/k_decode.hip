@@ -38,7 +38,7 @@ struct Dec {
   int Bmax;               // decode_batch
   int Bp;                 // MFMA path: batch padded to 16 or 32
   int ctx;                // max positions
-  float *kc, *vc;         // [L][Bmax][NKV][ctx][HD]
+  float *kc, *vc;         // [L][Bmax][NKV] of V [ctx][HD] and K [ctx][HD] (batch <= 4: [HD/4][ctx] float4 pieces)
   float *x, *xn, *qkv, *att, *logits;  // [Bp, *]
   float *ws;              // MFMA split-K partials
   long ws_elems;
@@ -532,7 +532,10 @@ __global__ void dec_token_kernel(const int32_t *__restrict__ prompt, int ctx, co
   }
 }
 
-template <int HD, int RATIO>
+// KCOL (batch <= 4, one block per KV head): the K cache holds float4 d4 of position t at
+// K4[d4 * ctx + t], so that the score loop's lanes (one position each) read consecutive 16-byte
+// pieces; else row-major like V ([ctx][HD]), which measured faster at batch 32.
+template <int HD, int RATIO, bool KCOL>
 __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv, int QKV,
                                                        const float *__restrict__ gq, const float *__restrict__ gk,
                                                        const float *__restrict__ cosb, const float *__restrict__ sinb,
@@ -542,7 +545,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   extern __shared__ float sc[];  // [RATIO][ctx]
   constexpr int C4 = HD / 4, NG = 256 / C4, HALF = HD / 2;
   __shared__ float4 qs[RATIO][C4];
-  __shared__ float4 kn[C4], vn[C4];
+  __shared__ float4 vn[C4];
   __shared__ float4 part[NG][RATIO][C4];
   __shared__ float red[RATIO][8];
   const int b = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   // slots 0..RATIO-1: q heads kvh*RATIO + slot; RATIO: k head kvh; RATIO+1: v head kvh
   for (int i = tid; i < (RATIO + 2) * HALF; i += 256) {
     const int slot = i / HALF, p = i % HALF;
-    float *q2 = (float *)qs, *k2 = (float *)kn, *v2 = (float *)vn;
+    float *q2 = (float *)qs, *v2 = (float *)vn;
     if (slot == RATIO + 1) {
       const int c0 = (NH + NKV) * HD + kvh * HD;
       const float y0 = qval(c0 + 2 * p), y1 = qval(c0 + 2 * p + 1);
@@ -587,23 +590,27 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
       q2[slot * HD + 2 * p] = y0;
       q2[slot * HD + 2 * p + 1] = y1;
     } else {
-      k2[2 * p] = y0; k2[2 * p + 1] = y1;
-      K[(long)pos * HD + 2 * p] = y0;
-      K[(long)pos * HD + 2 * p + 1] = y1;
+      if (KCOL) {
+        *(float2 *)(K + ((long)(p >> 1) * ctx + pos) * 4 + 2 * (p & 1)) = make_float2(y0, y1);
+      } else {
+        K[(long)pos * HD + 2 * p] = y0;
+        K[(long)pos * HD + 2 * p + 1] = y1;
+      }
     }
   }
   __syncthreads();
   float mx[RATIO];
 #pragma unroll
   for (int r = 0; r < RATIO; r++) mx[r] = -INFINITY;
+  const float4 *K4 = (const float4 *)K;
   for (int t = tid; t < npos; t += 256) {
-    const float4 *kr = t == pos ? kn : (const float4 *)(K + (long)t * HD);
+    // position pos was written by this block above; the barrier made it visible
     float s[RATIO];
 #pragma unroll
     for (int r = 0; r < RATIO; r++) s[r] = 0.f;
 #pragma unroll 8
     for (int d4 = 0; d4 < C4; d4++) {
-      const float4 kv = kr[d4];
+      const float4 kv = KCOL ? K4[(long)d4 * ctx + t] : K4[(long)t * C4 + d4];
 #pragma unroll
       for (int r = 0; r < RATIO; r++) {
         const float4 qv = qs[r][d4];
@@ -1078,7 +1085,7 @@ int gemv_bf3_resid(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *
 }
 
 // qkv: the q|k|v rows [Bp, QKV], or (qnz > 1) qnz split-K partial slices of them.
-int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const float *qkv, int qnz) {
+int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const float *qkv, int qnz, bool kcol) {
   Dec *d = (Dec *)c->dec;
   const int ratio = c->NH / c->NKV;
   const size_t sh = (size_t)ratio * d->ctx * sizeof(float);
@@ -1086,8 +1093,14 @@ int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const
   const float *gq = c->c.qk_norm ? c->P + o.gq : nullptr, *gk = c->c.qk_norm ? c->P + o.gk : nullptr;
   const dim3 grid(B, c->NKV);
 #define NE_DEC_ATTN(HDV, R)                                                                                     \
-  hipLaunchKernelGGL((dec_attn_kernel<HDV, R>), grid, dim3(256), sh, c->st, qkv, c->QKV, gq, gk, d->cosb,      \
-                     d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale, qkv, qnz, d->Bp)
+  if (kcol)                                                                                                     \
+    hipLaunchKernelGGL((dec_attn_kernel<HDV, R, true>), grid, dim3(256), sh, c->st, qkv, c->QKV, gq, gk,        \
+                       d->cosb, d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale,   \
+                       qkv, qnz, d->Bp);                                                                        \
+  else                                                                                                          \
+    hipLaunchKernelGGL((dec_attn_kernel<HDV, R, false>), grid, dim3(256), sh, c->st, qkv, c->QKV, gq, gk,       \
+                       d->cosb, d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale,   \
+                       qkv, qnz, d->Bp)
   if (c->HD == 128) {
     if (ratio == 1) NE_DEC_ATTN(128, 1);
     else if (ratio == 2) NE_DEC_ATTN(128, 2);
@@ -1128,13 +1141,13 @@ int enqueue_position(ne_ctx *c, int B, bool gen, bool greedy) {
     const size_t kvl = (size_t)l * d->Bmax * NKV * d->ctx * HD;
     if (small) {
       NE_CHECK(gemv_small(c, B, PRO_RMSNORM, false, Pb + o.wqkv, QKV, D, d->x, D, Pf + o.g_att, d->qkv, QKV, nullptr, 1.f));
-      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->qkv, 1));
+      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->qkv, 1, true));
     } else {
       int qnz = 0;
       int rc = gemv_bf3(c, B, Pb + o.wqkv, QKV, D, d->xn, D, BF3_WS, nullptr, 0, &qnz);
       if (rc < 0) return rc;
       if (!rc) NE_CHECK(gemv_big(c, B, Pb + o.wqkv, QKV, D, d->xn, D, d->ws, cap, nullptr, 0, nullptr, 1.f, &qnz));
-      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->ws, qnz));
+      NE_CHECK(launch_attn(c, B, o, d->kc + kvl, d->vc + kvl, d->ws, qnz, false));
     }
     if (small) {
       NE_CHECK(gemv_small(c, B, PRO_NONE, false, Pb + o.wo, D, Q, d->att, Q, nullptr, d->x, D, d->x, alpha));
