@@ -548,7 +548,10 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   __shared__ float4 vn[C4];
   __shared__ float4 part[NG][RATIO][C4];
   __shared__ float red[RATIO][8];
-  const int b = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+  // block y: query heads qh0 .. qh0 + RATIO - 1 of KV head kvh (RATIO may be a part of the
+  // model's NH / NKV query heads per KV head: the blocks of one KV head then append the same
+  // K and V values)
+  const int b = blockIdx.x, qh0 = blockIdx.y * RATIO, kvh = qh0 / (NH / NKV), tid = threadIdx.x;
   const int pos = st->pos, npos = pos + 1;
   float *K = kc + ((long)b * NKV + kvh) * ctx * HD;
   float *V = vc + ((long)b * NKV + kvh) * ctx * HD;
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     for (int z = 0; z < qnz; z++) s += qws[((long)z * Bp + b) * QKV + col];
     return s;
   };
-  // slots 0..RATIO-1: q heads kvh*RATIO + slot; RATIO: k head kvh; RATIO+1: v head kvh
+  // slots 0..RATIO-1: q heads qh0 + slot; RATIO: k head kvh; RATIO+1: v head kvh
   for (int i = tid; i < (RATIO + 2) * HALF; i += 256) {
     const int slot = i / HALF, p = i % HALF;
     float *q2 = (float *)qs, *v2 = (float *)vn;
@@ -574,7 +577,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
       continue;
     }
     const bool isq = slot < RATIO;
-    const int c0 = isq ? (kvh * RATIO + slot) * HD : NH * HD + kvh * HD;
+    const int c0 = isq ? (qh0 + slot) * HD : NH * HD + kvh * HD;
     float x0 = qval(c0 + 2 * p), x1 = qval(c0 + 2 * p + 1);
     const float *gg = isq ? gq : gk;
     if (gg) {  // uniform per block: every lane of the slot's (half-)wave takes part
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
       o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
     }
     o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
-    *(float4 *)(att + (long)b * NH * HD + (long)(kvh * RATIO + r) * HD + c * 4) = o;
+    *(float4 *)(att + (long)b * NH * HD + (long)(qh0 + r) * HD + c * 4) = o;
   }
 }
 
@@ -1088,10 +1091,13 @@ int gemv_bf3_resid(ne_ctx *c, int B, const h16_t *W, int N, int K, const float *
 int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const float *qkv, int qnz, bool kcol) {
   Dec *d = (Dec *)c->dec;
   const int ratio = c->NH / c->NKV;
-  const size_t sh = (size_t)ratio * d->ctx * sizeof(float);
+  // query heads per block: at batch <= 4 one (the blocks of a KV head share its K/V reads
+  // through L2, and twice the blocks run), else all of the KV head's
+  const int qpb = kcol ? 1 : ratio;
+  const size_t sh = (size_t)qpb * d->ctx * sizeof(float);
   const double scale = 1.0 / sqrt((double)c->HD);
   const float *gq = c->c.qk_norm ? c->P + o.gq : nullptr, *gk = c->c.qk_norm ? c->P + o.gk : nullptr;
-  const dim3 grid(B, c->NKV);
+  const dim3 grid(B, c->NH / qpb);
 #define NE_DEC_ATTN(HDV, R)                                                                                     \
   if (kcol)                                                                                                     \
     hipLaunchKernelGGL((dec_attn_kernel<HDV, R, true>), grid, dim3(256), sh, c->st, qkv, c->QKV, gq, gk,        \
@@ -1102,12 +1108,12 @@ int launch_attn(ne_ctx *c, int B, const LayerOff &o, float *kc, float *vc, const
                        d->cosb, d->sinb, kc, vc, d->att, c->NH, c->NKV, d->ctx, d->st, c->c.norm_eps, scale,   \
                        qkv, qnz, d->Bp)
   if (c->HD == 128) {
-    if (ratio == 1) NE_DEC_ATTN(128, 1);
-    else if (ratio == 2) NE_DEC_ATTN(128, 2);
+    if (qpb == 1) NE_DEC_ATTN(128, 1);
+    else if (qpb == 2) NE_DEC_ATTN(128, 2);
     else NE_DEC_ATTN(128, 4);
   } else {
-    if (ratio == 1) NE_DEC_ATTN(64, 1);
-    else if (ratio == 2) NE_DEC_ATTN(64, 2);
+    if (qpb == 1) NE_DEC_ATTN(64, 1);
+    else if (qpb == 2) NE_DEC_ATTN(64, 2);
     else NE_DEC_ATTN(64, 4);
   }
 #undef NE_DEC_ATTN
@@ -1221,7 +1227,8 @@ int decode_alloc(ne_ctx *c) {
   Dec *d = new Dec();
   c->dec = d;
   if (c->c.decode_batch > 32) return ne_fail(NE_ERR_ARG, "decode_batch %d > 32", c->c.decode_batch);
-  if (c->NH / c->NKV > 4) return ne_fail(NE_ERR_ARG, "decode: more than 4 query heads per KV head");
+  if (c->NH / c->NKV != 1 && c->NH / c->NKV != 2 && c->NH / c->NKV != 4)
+    return ne_fail(NE_ERR_ARG, "decode: %d query heads per KV head (1, 2 or 4)", c->NH / c->NKV);
   if (c->D % 128 || c->H % 128 || c->Q % 128)
     return ne_fail(NE_ERR_ARG, "decode: dim, hidden and q_dim must be multiples of 128");
   d->Bmax = c->c.decode_batch;
