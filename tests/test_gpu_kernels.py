@@ -223,7 +223,7 @@ def test_swiglu_fwd(fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,H,D", [(256, 3072, 1024), (256, 2048, 768), (2048, 3072, 1024), (4096, 3072, 1024),
-                                   (128, 192, 256)])
+                                   (1024, 3072, 1024), (128, 192, 256), (128, 256, 192)])
 def test_gemm_swiglu_fwd_epilogue(fmt, T, H, D):
     """The W1|W3 GEMM with the SwiGLU forward in its epilogue (B rows gathered so that h1 and h3
     of a column share a work-group) writes the same h13 and gate, bit for bit, as the plain
