@@ -497,7 +497,8 @@ def main():
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
     roofline = {"bound": "hbm",
                 "kernel": "adam_kernel (fused AdamW; one pass over all parameters per step, in "
-                          f"{adam_launches:.0f} launches: embedding + gains, then one per layer)",
+                          f"{adam_launches:.0f} launches: embedding + gains, then one per layer, the layer "
+                          "launches capped at 384 work-groups while they run beside the next forward)",
                 "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                 "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
                 "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,

@@ -174,7 +174,8 @@ int launch_clip_finalize(const double *partials, int nparts, float grad_scale, f
 int launch_adam(int dt, const AdamArgs &a, hipStream_t s) {
   if (a.n % 4 || a.n_decay % 4) return ne_fail(NE_ERR_ARG, "adam: sizes must be multiples of 4");
   // 64K work-groups: measured at the streaming ceiling of the device for this read/write mix
-  const int grid = (int)std::max<long>(1, std::min<long>((a.n / 4 + 511) / 512, 65536));
+  const long cap = a.max_groups > 0 ? a.max_groups : 65536;
+  const int grid = (int)std::max<long>(1, std::min<long>((a.n / 4 + 511) / 512, cap));
   return DISPATCH_H16(dt, [&] {
     if (a.pb) hipLaunchKernelGGL((adam_kernel<HT, true>), dim3(grid), dim3(256), 0, s, a);
     else hipLaunchKernelGGL((adam_kernel<HT, false>), dim3(grid), dim3(256), 0, s, a);

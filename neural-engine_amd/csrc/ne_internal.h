@@ -205,6 +205,7 @@ struct AdamArgs {
   const float *gscale;  // device scalar: grad_scale * clip factor
   const int *skip;      // device flag: when set, leave p/m/v untouched (overflowed step)
   int zero_grad;        // write g = 0 after the update
+  int max_groups;       // work-group cap of the launch (0: the streaming default)
 };
 int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s);
 // Sums of squares of two ranges in one launch: g1 into partials[0, nparts_each), g2 into
