@@ -127,6 +127,43 @@ def test_grads_accumulate_and_zero():
     m.close()
 
 
+@pytest.mark.parametrize("overlap", [True, False])
+def test_overflowed_window_skips_the_update(overlap):
+    """A 16-bit overflow in the accumulation window (a final-norm gain of 1e6 takes the 16-bit
+    final hidden state past the fp16 range) skips the update: the optimizer reports a NaN norm,
+    parameters and moments stay as they were bit for bit, Adam's step count does not advance, the
+    internal gradient scale halves and an overflow site is named; the next clean window updates
+    as usual."""
+    cfg = om.tiny(qk_norm=True)
+    sh = shapes(cfg)
+    P = om.init_params(cfg, seed=3, std=0.02)
+    tok = om.tokens_for_step(cfg, 1, cfg.seq, seed=4)
+    m = ne.Model.from_oracle(cfg, batch=1)
+    m.overlap_weight_grads(overlap)
+    m.set_params(P)
+    m.train_step(tok, 256.0)
+    assert np.isfinite(m.optimizer_step(3e-4, grad_scale=1 / 256, clip=1.0))
+    m.set("rms_final", m.get("rms_final") * np.float32(1e6))
+    before = {k: m.get_all(sh, k) for k in (ne.NE_PARAM, ne.NE_ADAM_M, ne.NE_ADAM_V)}
+    t0, (scale0, skipped0, _) = m.state().adam_t, m.grad_scale_info()
+    m.train_step(tok, 256.0)
+    assert np.isnan(m.optimizer_step(3e-4, grad_scale=1 / 256, clip=1.0))
+    scale, skipped, sites = m.grad_scale_info()
+    assert skipped == skipped0 + 1 and sites and scale == scale0 / 2, (skipped, sites, scale)
+    assert m.state().adam_t == t0
+    for k, want in before.items():
+        got = m.get_all(sh, k)
+        for n in want:
+            np.testing.assert_array_equal(got[n], want[n], err_msg=f"kind {k} {n}")
+    m.set("rms_final", before[ne.NE_PARAM]["rms_final"] / np.float32(1e6))
+    m.train_step(tok, 256.0)
+    assert np.isfinite(m.optimizer_step(3e-4, grad_scale=1 / 256, clip=1.0))
+    assert m.state().adam_t == t0 + 1 and m.grad_scale_info()[1] == skipped
+    after = m.get_all(sh, ne.NE_PARAM)
+    assert any(not np.array_equal(after[n], before[ne.NE_PARAM][n]) for n in after if n != "rms_final")
+    m.close()
+
+
 @pytest.mark.parametrize("clip", [1.0, 1e-3])
 def test_optimizer_step_matches_oracle(clip):
     """Same grads in -> AdamW out within 1e-5 (isolates the update from bf16 gradients)."""
