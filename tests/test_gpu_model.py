@@ -263,6 +263,34 @@ def test_decode_greedy_matches_oracle(case, dtype):
     m.close()
 
 
+def test_four_query_heads_per_kv_head():
+    """GQA with four query heads per KV head (the other tests run two and one): the training
+    step's gradients against the oracle, and greedy decoding token-identical to it on the
+    small-batch path (one query head per attention block) and the batched bf16 path (all four
+    query heads of a KV head per block)."""
+    cfg = om.tiny(**CASES["qwen3"], n_heads=8, kv_heads=2, vocab=1024)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = om.tokens_for_step(cfg, 2, cfg.seq, seed=1)
+    m, loss, G = run_step(cfg, P, tok)
+    Pm = as_multiplied(P, ne.NE_FP16)
+    lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0)
+    Go = om.backward(cfg, Pm, cache)
+    m.close()
+    assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
+    for n in P:
+        assert rel_l2(G[n], Go[n]) <= grad_tol(n, ne.NE_FP16), (n, rel_l2(G[n], Go[n]))
+    Pd = _held_params(cfg, ne.NE_BF16, std=0.05)
+    for B in (1, 6):
+        prompt = np.random.default_rng(B).integers(0, cfg.vocab, (B, 8)).astype(np.int32)
+        md = ne.Model.from_oracle(cfg, decode_batch=B, decode_ctx=64, dtype=ne.NE_BF16)
+        md.set_params(Pd)
+        got = md.decode(prompt, 24)
+        md.close()
+        want = om.decode(cfg, Pd, prompt, 24)
+        want = want[0] if isinstance(want, tuple) else want
+        np.testing.assert_array_equal(got, want, err_msg=f"B={B}")
+
+
 @pytest.mark.parametrize("B", [3, 6])
 def test_decode_long_cache_splits_match_oracle(B):
     """A cache of 4200 positions (scores of every position in LDS) with a 150-token prompt:
