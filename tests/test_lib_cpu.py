@@ -55,6 +55,17 @@ def test_kernel_entry_points_validate_shapes_before_launch():
     assert rc == -1
 
 
+def test_swiglu_forward_epilogue_arguments_checked_on_host():
+    """The W1|W3 GEMM's SwiGLU-forward epilogue (epi 7) needs both outputs and layout 0; the
+    checks run before any launch."""
+    L = ne.lib()
+    rc = L.ne_k_gemm(ne.NE_FP16, 0, 7, 64, 128, 64, None, 64, None, 64, None, 128, None, 64, 1.0, None)
+    assert rc == -1 and b"SwiGLU forward" in L.ne_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the layout is refused before a launch
+    rc = L.ne_k_gemm(ne.NE_FP16, 2, 7, 64, 128, 64, fake, 64, fake, 128, fake, 128, fake, 64, 1.0, None)
+    assert rc == -1 and b"layout 0" in L.ne_last_error()
+
+
 def test_wgrad_group_refuses_shapes_off_its_path():
     """The grouped weight-gradient GEMM takes only the long-step shapes (M, N multiples of 256,
     K >= 8192, at least 192 tiles); anything else is refused on the host, before a launch."""
