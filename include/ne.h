@@ -210,6 +210,26 @@ int ne_prof_reset(ne_ctx *ctx);
 /* Total milliseconds and launch count of one family since the last reset (synchronises). */
 int ne_prof_get(ne_ctx *ctx, int family, double *ms, int64_t *count);
 
+/* Phase timeline of the training step (off by default).  While on, ne_train_step and
+ * ne_optimizer_step record HIP timing events at their phase boundaries without changing
+ * the schedule (the two-stream step stays two-stream; the single-stream step launches
+ * eagerly instead of from its graph).  ne_step_timeline (synchronises) returns the last
+ * step's phases in milliseconds of GPU time on the step stream: out[NE_TL_WAIT] the wait for
+ * the previous update before the embedding lookup, NE_TL_FWD the forward through the final
+ * RMSNorm, NE_TL_CLS the classifier and cross-entropy forward and backward through the
+ * final RMSNorm's backward, NE_TL_BWD the layers' backward chain, NE_TL_DWAIT the wait for
+ * the weight-gradient stream, NE_TL_TAIL the gain sums and embedding scatter, NE_TL_STEP
+ * first to last event; for the last optimizer call NE_TL_OPT the norm and clip on the step
+ * stream and NE_TL_UPDATE the AdamW pass, first launch to last (NaN if none was recorded).
+ * layer_fwd / layer_bwd (may be NULL) receive n_layers times each.  Replaces the per-phase
+ * timers of the step line (TD/train.m:763-767). */
+enum {
+  NE_TL_WAIT = 0, NE_TL_FWD, NE_TL_CLS, NE_TL_BWD, NE_TL_DWAIT, NE_TL_TAIL, NE_TL_STEP, NE_TL_OPT,
+  NE_TL_UPDATE, NE_TL_COUNT
+};
+int ne_timeline(ne_ctx *ctx, int on);
+int ne_step_timeline(ne_ctx *ctx, float out[NE_TL_COUNT], float *layer_fwd, float *layer_bwd);
+
 /* ------------------------------------------------------ kernel-level entry points ---- */
 /* Device-pointer entry points of the individual kernels, for testing and for callers
  * composing their own step.  16-bit buffers hold NE_FP16 or NE_BF16 bit patterns as

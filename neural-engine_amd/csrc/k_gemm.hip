@@ -141,17 +141,42 @@ __device__ __forceinline__ void sched_kstep() {
 }
 
 
-// Final store of one output element v (alpha already applied) for every non-CE epilogue.
+// Epilogues whose fp32 output is a gradient: the tile also reports the sum of squares of
+// the values it stores (GemmArgs::sq), for the global gradient norm.
+template <int EPI>
+constexpr bool epi_sq() { return EPI == EPI_F32 || EPI == EPI_F32_ACC; }
+
+// Block sum of each thread's s (fixed order: waves, then wave 0..NW-1) into *out.
+template <int NW>
+__device__ __forceinline__ void block_sumsq_store(float s, double *out) {
+  __shared__ float red[NW];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) t += red[w];
+    *out = t;
+  }
+}
+
+// Final store of one output element v (alpha already applied) for every non-CE epilogue;
+// returns the fp32 value stored (EPI_F32, EPI_F32_ACC; else 0).
 template <typename HT, int EPI>
-__device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, float v, bool &bad) {
+__device__ __forceinline__ float store_out(const GemmArgs &g, int row, int col, float v, bool &bad) {
   if constexpr (EPI == EPI_H16) {
     const h16_t o = HT::h(v);
     bad |= HT::bad(o);
     ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
   } else if constexpr (EPI == EPI_F32) {
     ((float *)g.C)[(long)row * g.ldc + col] = v;
+    return v;
   } else if constexpr (EPI == EPI_F32_ACC) {
-    ((float *)g.C)[(long)row * g.ldc + col] += v;
+    float *c = (float *)g.C + (long)row * g.ldc + col;
+    const float o = *c + v;
+    *c = o;
+    return o;
   } else if constexpr (EPI == EPI_RESID) {
     ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
@@ -165,6 +190,7 @@ __device__ __forceinline__ void store_out(const GemmArgs &g, int row, int col, f
     d[col] = o1;
     d[g.N + col] = o3;
   }
+  return 0.f;
 }
 
 // How a split's K steps are run: the software pipeline takes two steps per iteration.
@@ -470,7 +496,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
     return;
   }
 
+  // The sum of squares of the stored values (epi_sq): summed as they are stored, except on
+  // the 256x256 tile (128 accumulators per lane), where keeping each stored value live for it
+  // pushed the registers past 256 (scratch spills); there each thread reads back the values it
+  // has just stored (L2 hits), after a compiler barrier that keeps the reads from being folded
+  // into the stores.  That tile runs long reductions (K >= 8192), where the read-back is
+  // negligible; at 256 tokens it cost the 128x128 weight-gradient tiles ~25 us per layer.
+  constexpr bool SQ_INLINE = FM * FN * 16 <= 64;
   bool bad = false;
+  float sq = 0.f;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
 #pragma unroll
@@ -479,11 +513,31 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        store_out<HT, EPI>(g, row, col, acc[i][j][e] * alpha, bad);
+        const float o = store_out<HT, EPI>(g, row, col, acc[i][j][e] * alpha, bad);
+        if constexpr (epi_sq<EPI>() && SQ_INLINE) sq += o * o;
       }
     }
   }
   flag_overflow(g.ovf, bad);
+  if constexpr (epi_sq<EPI>())
+    if (g.sq) {
+      if constexpr (!SQ_INLINE) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            const int col = n0 + wn * TN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+              const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+              const float o = ((const float *)g.C)[(long)row * g.ldc + col];
+              sq += o * o;
+            }
+          }
+      }
+      block_sumsq_store<WM * WN>(sq, g.sq + (long)mt * (g.N / BN) + nt);
+    }
 }
 
 // Tile order.  Work-groups go to the 8 XCDs round-robin (work-group w to XCD w % 8), and
@@ -544,6 +598,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
   const long n4 = (long)g.M * g.N / 4;
   const long slice = (long)g.M * g.N;
   bool bad = false;
+  float sq = 0.f;
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
     const long e = i * 4;
     float4 p[KS];
@@ -563,17 +618,23 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
       }
     }
     const int row = (int)(e / g.N), col = (int)(e % g.N);
-    store_out<HT, EPI>(g, row, col, s.x * g.alpha, bad);
-    store_out<HT, EPI>(g, row, col + 1, s.y * g.alpha, bad);
-    store_out<HT, EPI>(g, row, col + 2, s.z * g.alpha, bad);
-    store_out<HT, EPI>(g, row, col + 3, s.w * g.alpha, bad);
+    const float o0 = store_out<HT, EPI>(g, row, col, s.x * g.alpha, bad);
+    const float o1 = store_out<HT, EPI>(g, row, col + 1, s.y * g.alpha, bad);
+    const float o2 = store_out<HT, EPI>(g, row, col + 2, s.z * g.alpha, bad);
+    const float o3 = store_out<HT, EPI>(g, row, col + 3, s.w * g.alpha, bad);
+    if constexpr (epi_sq<EPI>()) sq += o0 * o0 + o1 * o1 + o2 * o2 + o3 * o3;
   }
   flag_overflow(g.ovf, bad);
+  if constexpr (epi_sq<EPI>())
+    if (g.sq) block_sumsq_store<4>(sq, g.sq + blockIdx.x);
 }
 
 }  // namespace
 
 namespace {
+
+// Work-groups of the ordered split-K reduction of an M x N output.
+int reduce_blocks(int M, int N) { return (int)std::min<long>(((long)M * N / 4 + 255) / 256, 2048); }
 
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI>
 int launch_t(GemmArgs g, hipStream_t s) {
@@ -590,8 +651,7 @@ int launch_t(GemmArgs g, hipStream_t s) {
   NE_HIP(hipGetLastError());
   if (g.split > 1 && !g.defer_reduce) {
     if constexpr (EPI != EPI_CE_FWD && EPI != EPI_CE_BWD && EPI != EPI_SWIGLU_FWD) {
-      const long n4 = (long)g.M * g.N / 4;
-      const int blocks = (int)std::min<long>((n4 + 255) / 256, 2048);
+      const int blocks = reduce_blocks(g.M, g.N);
       if (g.split == 2) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 2>), dim3(blocks), dim3(256), 0, s, g);
       else if (g.split == 4) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 4>), dim3(blocks), dim3(256), 0, s, g);
       else if (g.split % 8 == 0) hipLaunchKernelGGL((splitk_reduce_kernel<HT, EPI, 8>), dim3(blocks), dim3(256), 0, s, g);
@@ -755,6 +815,18 @@ int gemm_splits(int epi, int M, int N, int K, long ws_elems) {
   return split;
 }
 
+long gemm_sq_parts(int epi, int M, int N, int K, long ws_elems) {
+  // the same ragged splits as gemm_launch (EPI_F32 / EPI_F32_ACC take both)
+  if (const int nm = ragged_main(M, N, K))
+    return gemm_sq_parts(epi, M, nm, K, ws_elems) + gemm_sq_parts(epi, M, N - nm, K, ws_elems);
+  if (const int mm = ragged_main(N, M, K))
+    return gemm_sq_parts(epi, mm, N, K, ws_elems) + gemm_sq_parts(epi, M - mm, N, K, ws_elems);
+  int tile, split;
+  plan(epi, M, N, K, ws_elems, tile, split);
+  if (split > 1) return reduce_blocks(M, N);
+  return (long)(M / tile_bm(tile)) * (N / tile_bn(tile));
+}
+
 int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *split_out) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || g.M % 64 || g.N % 64 || g.K % 64)
     return ne_fail(NE_ERR_ARG, "gemm: M=%d N=%d K=%d must be positive multiples of 64", g.M, g.N, g.K);
@@ -777,6 +849,7 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
       b.B = (const h16_t *)g.B + ((layout & 2) ? (long)nm : (long)nm * g.ldb);
       if (g.C) b.C = (char *)g.C + nm * ce;
       if (g.R) b.R = (const float *)g.R + nm;
+      if (g.sq) b.sq = g.sq + gemm_sq_parts(epi, a.M, a.N, a.K, g.ws ? g.ws_elems : -1);
       b.col0 = g.col0 + nm;
       if (epi == EPI_CE_FWD) {
         a.part_ld = b.part_ld = g.part_ld > 0 ? g.part_ld : gemm_ce_tiles(g.M, g.N, g.K);
@@ -793,6 +866,7 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
         b.A = (const h16_t *)g.A + ((layout & 1) ? (long)mm : (long)mm * g.lda);
         if (g.C) b.C = (char *)g.C + (size_t)mm * g.ldc * ce;
         if (g.R) b.R = (const float *)g.R + (long)mm * g.ldr;
+        if (g.sq) b.sq = g.sq + gemm_sq_parts(epi, a.M, a.N, a.K, g.ws ? g.ws_elems : -1);
         NE_CHECK(gemm_launch(dt, layout, epi, a, s, split_out));
         return gemm_launch(dt, layout, epi, b, s, nullptr);
       }

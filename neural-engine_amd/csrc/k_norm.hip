@@ -17,6 +17,27 @@ __global__ void embed_fwd_kernel(const float *__restrict__ E, const int32_t *__r
   for (int i = lane; i < D / 4; i += 64) dst[i] = src[i];
 }
 
+// The lookup of a step whose preceding AdamW update of E has not run yet: x[t] = the row
+// E[tok[t]] as the update will leave it, computed from E, G, M, V with the update's element
+// arithmetic (adam_elem, weight decay on) and nothing written back; the update itself runs
+// later, beside the forward, and gives the same values bit for bit.
+__global__ void embed_fwd_adam_kernel(const float *__restrict__ E, const float *__restrict__ G,
+                                      const float *__restrict__ M, const float *__restrict__ V,
+                                      const int32_t *__restrict__ tok, float *__restrict__ x, int T, int D,
+                                      AdamArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= T) return;
+  const AdamConst k(a.gscale, a.b1, a.b2, a.bc1, a.bc2, a.lr, a.eps);
+  const long off = (long)tok[row] * D;
+  float *dst = x + (long)row * D;
+  for (int i = lane; i < D; i += 64) {
+    float p = E[off + i], m = M[off + i], v = V[off + i];
+    adam_elem(k, p, G[off + i], m, v, a.wd);
+    dst[i] = p;
+  }
+}
+
 // gE[tok[t], :] += scale * dx[t, :]   (TD/cpu_ops.h:441-447 embed_backward)
 __global__ void embed_bwd_kernel(float *__restrict__ gE, const int32_t *__restrict__ tok,
                                  const float *__restrict__ dx, float scale, int T, int D) {
@@ -627,6 +648,12 @@ int launch_embed_fwd(const float *E, const int32_t *tok, float *x, int T, int D,
   if (D % 4) return ne_fail(NE_ERR_ARG, "embed: D %% 4 != 0");
   hipLaunchKernelGGL(embed_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, E, tok, x, T, D);
   return ne_hip_status(hipGetLastError(), "embed_fwd");
+}
+
+int launch_embed_fwd_adam(const float *E, const float *G, const float *M, const float *V, const int32_t *tok,
+                          float *x, int T, int D, const AdamArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(embed_fwd_adam_kernel, dim3((T + 3) / 4), dim3(256), 0, s, E, G, M, V, tok, x, T, D, a);
+  return ne_hip_status(hipGetLastError(), "embed_fwd_adam");
 }
 
 int launch_embed_bwd(float *gE, const int32_t *tok, const float *dx, float scale, int T, int D, hipStream_t s) {

@@ -35,29 +35,31 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float *__restrict__ g,
   sumsq_block(g, n, blockIdx.x, gridDim.x, partials);
 }
 
-// Two ranges in one launch: the first half of the blocks sums g1 into partials[0, half), the
-// second g2 into partials[half, 2 half).
-__global__ __launch_bounds__(256) void sumsq2_kernel(const float *__restrict__ g1, long n1, const float *__restrict__ g2,
-                                                     long n2, double *__restrict__ partials) {
-  const int half = gridDim.x / 2;
-  if ((int)blockIdx.x < half) sumsq_block(g1, n1, blockIdx.x, half, partials);
-  else sumsq_block(g2, n2, blockIdx.x - half, half, partials + half);
-}
-
 // norm = grad_scale * sqrt(sum partials); factor = grad_scale * (clip / norm if norm > clip).
-// One block of 256 threads: strided sums, then the 4 wave sums in order (it sits between the
-// backward and the update, so its latency is on the step's critical path).
-__global__ __launch_bounds__(256) void clip_finalize_kernel(const double *__restrict__ partials, int nparts,
-                                                            float grad_scale, float clip, float *__restrict__ gscale,
-                                                            float *__restrict__ gnorm) {
-  __shared__ double red[4];
+// One block of 1024 threads (it sits between the backward and the update, so its latency is
+// on the step's critical path; the partials are the weight-gradient GEMMs' per-tile sums, tens
+// of thousands): each thread sums a strided subset, CL loads issued before the adds, then
+// the 16 wave sums in order.  Fixed order throughout (deterministic).
+__global__ __launch_bounds__(1024) void clip_finalize_kernel(const double *__restrict__ partials, int nparts,
+                                                             float grad_scale, float clip, float *__restrict__ gscale,
+                                                             float *__restrict__ gnorm) {
+  constexpr int NT = 1024, CL = 8;
+  __shared__ double red[NT / 64];
   double s = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += 256) s += partials[i];
+  for (int i0 = threadIdx.x; i0 < nparts; i0 += CL * NT) {
+    double v[CL];
+#pragma unroll
+    for (int u = 0; u < CL; u++) v[u] = i0 + u * NT < nparts ? partials[i0 + u * NT] : 0.0;
+#pragma unroll
+    for (int u = 0; u < CL; u++) s += v[u];
+  }
   s = wave_sum_d(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
-    s = red[0] + red[1] + red[2] + red[3];
+    s = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) s += red[w];
     // the partials may include signed row changes (embedding scatter): never below 0
     const float norm = (float)(sqrt(fmax(s, 0.0)) * (double)grad_scale);
     float f = grad_scale;
@@ -158,15 +160,9 @@ int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream
   return ne_hip_status(hipGetLastError(), "sumsq");
 }
 
-int launch_sumsq2(const float *g1, long n1, const float *g2, long n2, double *partials, int nparts_each,
-                  hipStream_t s) {
-  hipLaunchKernelGGL(sumsq2_kernel, dim3(2 * nparts_each), dim3(256), 0, s, g1, n1, g2, n2, partials);
-  return ne_hip_status(hipGetLastError(), "sumsq2");
-}
-
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
                          float *gscale_out, float *gnorm_out, hipStream_t s) {
-  hipLaunchKernelGGL(clip_finalize_kernel, dim3(1), dim3(256), 0, s, partials, nparts, grad_scale, clip,
+  hipLaunchKernelGGL(clip_finalize_kernel, dim3(1), dim3(1024), 0, s, partials, nparts, grad_scale, clip,
                      gscale_out, gnorm_out);
   return ne_hip_status(hipGetLastError(), "clip_finalize");
 }

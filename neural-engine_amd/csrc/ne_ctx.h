@@ -34,6 +34,18 @@ enum {
 
 constexpr int NE_STATS_BLOCKS = 256;
 
+// Phase timeline (ne_timeline): timing events recorded at the phase boundaries of the step on
+// st and around the optimizer's update, without changing the schedule (the two-stream step
+// stays two-stream; only the captured single-stream graph is replaced by eager launches).
+struct Timeline {
+  bool on = false;
+  bool step_ok = false, opt_ok = false;  // the last step / optimizer call recorded its events
+  hipEvent_t start = nullptr, lookup = nullptr, fwd = nullptr, cls = nullptr, bwd = nullptr, join = nullptr,
+             end = nullptr;
+  hipEvent_t opt0 = nullptr, opt1 = nullptr, upd0 = nullptr, upd1 = nullptr;
+  std::vector<hipEvent_t> fwd_l, bwd_l;  // end of layer l's forward / backward on st
+};
+
 struct LayerAct {
   float *x_in, *r1, *x2, *r2, *rq, *rk, *lse;
   h16_t *xn, *qkv, *qr, *kr, *attn, *x2n, *h13, *gate;
@@ -55,10 +67,17 @@ struct ne_ctx {
   // produces each dY, joined once before the end of the backward
   hipStream_t st2 = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-  // The optimizer's update also runs on st2, in chunks (0: embedding + gains, 1 + l: layer l)
-  // each marked by ev_adam[k]; the next step's forward waits for chunk k just before it reads
-  // what the chunk writes.  adam_pending: an update was enqueued that st has not waited for.
+  // Two-stream schedule: ne_optimizer_step leaves its AdamW pass (upd, after the norm and
+  // clip on st) to the next training step, which enqueues it on st2 in chunks, each marked by
+  // ev_adam[k] (0: the gains, 1 + l: layer l, L + 1: the last piece of the embedding), and
+  // waits for chunk k just before it reads what the chunk writes; its lookup computes the
+  // updated rows itself, and the embedding's pieces start after it (ev_lookup).
+  // upd_deferred: such a pass has not been enqueued yet (any other entry point that touches
+  // the parameters runs it on st first); adam_pending: enqueued, not yet waited for by st.
   std::vector<hipEvent_t> ev_adam;
+  hipEvent_t ev_lookup = nullptr;
+  AdamArgs upd = {};
+  bool upd_deferred = false;
   bool adam_pending = false;
   long n_params = 0, n_decay = 0;
   float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
@@ -83,6 +102,15 @@ struct ne_ctx {
   // The step fills them as each part of G becomes final (see gn_layer etc. in ne_host.hip);
   // gn_ready: they describe G as it is now (else the optimizer sums G itself)
   double *gn_part;
+  // slots per layer of its Wqkv, Wo, W13, W2 weight-gradient GEMMs (one per tile, the tiling
+  // the launches take, fixed by the shapes) and of the embedding gradient's GEMM
+  long gn_n[4] = {0, 0, 0, 0};
+  long gn_lay = 0, gn_emb = 0;
+  // the embedding gradient's GEMM in de_pieces row blocks (de_rows[p], p <= de_pieces), piece
+  // p queued with the weight gradients of the (p+1)-th layer the backward reaches
+  int de_pieces = 1;
+  std::vector<int> de_rows;
+  bool gn_grouped = false;  // a layer's weight gradients run as one grouped launch
   bool gn_ready = false;
   // the last non-skipped optimizer step summed gn_part over G as it then was, at grad_scale
   // gn_gsc (ne_grad_norm_parts reads the groups back until the next step or gradient write)
@@ -116,6 +144,7 @@ struct ne_ctx {
   int *h_ovf = nullptr;      // pinned [32]
   ne_train_state state = {};
   Prof prof;
+  Timeline tl;
   // vocabulary compaction: the classifier covers cv embedding rows (cvp = cv rounded up to
   // 64, the padding columns masked out of the softmax)
   int cv = 0, cvp = 0;

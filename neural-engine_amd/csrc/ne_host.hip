@@ -88,12 +88,29 @@ struct ProfScope {
   ~ProfScope() { prof_end(c, fam, e0, s); }
 };
 
-// Make st wait for an optimizer update still running on st2 (every entry point that reads
-// or writes parameters, moments or gradients, other than the next training step).
+// Make st follow the last optimizer update (every entry point that reads or writes
+// parameters, moments or gradients, other than the next training step): a deferred pass is
+// run on st now, in one launch; one still running on st2 is waited for.
 int adam_join(ne_ctx *c) {
+  if (c->upd_deferred) {
+    c->upd_deferred = false;
+    AdamArgs a = c->upd;
+    a.max_groups = 0;
+    hipEvent_t e0 = nullptr;
+    prof_begin(c, NE_PROF_ADAM, &e0, c->st);
+    NE_CHECK(launch_adam(c->dt, a, c->st));
+    prof_end(c, NE_PROF_ADAM, e0, c->st);
+  }
   if (!c->adam_pending) return 0;
-  NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[c->L], 0));
+  NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[c->L + 1], 0));
   c->adam_pending = false;
+  return 0;
+}
+
+// Timeline event e on stream s (default st), when the timeline is on.
+int tl_mark(ne_ctx *c, hipEvent_t e, hipStream_t s = nullptr) {
+  if (!c->tl.on) return 0;
+  NE_HIP(hipEventRecord(e, s ? s : c->st));
   return 0;
 }
 
@@ -130,8 +147,9 @@ int gemm(ne_ctx *c, int fam, int site, int layout, int epi, int M, int N, int K,
 // forks (see Fork), else in order on st.
 // Its split-K partials (if any) go to ws2 either way, so they never meet the dX partials
 // that a consumer has yet to read from ws.
+// sq (nullable): the sum-of-squares slots of C (GemmArgs::sq).
 int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X,
-            long ldx, float *C, float u) {
+            long ldx, float *C, float u, double *sq) {
   ProfScope ps(c, fam);
   GemmArgs g = {};
   g.M = M; g.N = N; g.K = K;
@@ -139,6 +157,7 @@ int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h
   g.alpha = u;
   g.ws = c->ws2;
   g.ws_elems = c->ws_elems;
+  g.sq = sq;
   return gemm_launch(c->dt, GEMM_TN, epi, g, side ? c->st2 : c->st);
 }
 
@@ -147,32 +166,36 @@ int gemm_dw(ne_ctx *c, bool side, int fam, int epi, int M, int N, int K, const h
 // stream capture, a graph edge) and enqueues the batch there; join() makes st wait for st2.
 // Without, a batch runs in order on st where flush() is called (per-kernel-family event
 // timing records on st).
-// Also queued: the sum of squares of a finished part of G into its partial slots (sumsq()).
+// A GEMM job with sq writes the sum of squares of each tile of G it finishes into its nsq
+// slots (the global gradient norm's partials); also queued: the sum of squares of a part of
+// G into its slots (sumsq(): the compact embedding gradient after its scatter).
 struct WgradQueue {
   struct Job {
     int fam, epi, M, N, K;
     const h16_t *dY; long ldy; const h16_t *X; long ldx; float *C; float u;
+    double *sq; long nsq;              // GEMM: its tiles' sum-of-squares slots (nullable)
     long n; int nparts; double *part;  // M == 0: sum of squares of C[0, n) into part[0, nparts)
-    const float *C2; long n2;          // and, if C2, of C2[0, n2) into part[nparts, 2 nparts)
   };
   ne_ctx *c;
   bool on;
   std::vector<Job> jobs;
   int run(const Job &j, bool side) {
-    if (j.M == 0 && j.C2) return launch_sumsq2(j.C, j.n, j.C2, j.n2, j.part, j.nparts, side ? c->st2 : c->st);
     if (j.M == 0) return launch_sumsq(j.C, j.n, j.part, j.nparts, side ? c->st2 : c->st);
-    return gemm_dw(c, side, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u);
+    if (j.sq && gemm_sq_parts(j.epi, j.M, j.N, j.K, c->ws_elems) != j.nsq)
+      return ne_fail(NE_ERR_STATE, "weight gradient %dx%d: %ld norm slots planned, the launch writes %ld", j.M, j.N,
+                     j.nsq, gemm_sq_parts(j.epi, j.M, j.N, j.K, c->ws_elems));
+    return gemm_dw(c, side, j.fam, j.epi, j.M, j.N, j.K, j.dY, j.ldy, j.X, j.ldx, j.C, j.u, j.sq);
   }
   int push(const Job &j) {
     jobs.push_back(j);
     return 0;
   }
   int add(int fam, int epi, int M, int N, int K, const h16_t *dY, long ldy, const h16_t *X, long ldx, float *C,
-          float u) {
-    return push({fam, epi, M, N, K, dY, ldy, X, ldx, C, u, 0, 0, nullptr, nullptr, 0});
+          float u, double *sq = nullptr, long nsq = 0) {
+    return push({fam, epi, M, N, K, dY, ldy, X, ldx, C, u, sq, nsq, 0, 0, nullptr});
   }
-  int sumsq(const float *g, long n, long slot, int nparts, const float *g2 = nullptr, long n2 = 0) {
-    return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, n, nparts, c->gn_part + slot, g2, n2});
+  int sumsq(const float *g, long n, long slot, int nparts) {
+    return push({0, 0, 0, 0, 0, nullptr, 0, nullptr, 0, (float *)g, 0.f, nullptr, 0, n, nparts, c->gn_part + slot});
   }
   // Consecutive GEMM jobs with one epilogue, K and scale that gemm_group_fits (a long step's
   // weight gradients of a layer) run as one launch without split-K, in both schedules, so the
@@ -189,9 +212,14 @@ struct WgradQueue {
         g.M = j.M; g.N = j.N; g.K = j.K;
         g.A = j.dY; g.lda = j.ldy; g.B = j.X; g.ldb = j.ldx; g.C = j.C; g.ldc = j.N;
         g.alpha = j.u;
+        g.sq = j.sq;
         e++;
       }
       if (e - i >= 2 && gemm_group_fits(ga, (int)(e - i))) {
+        for (size_t k = i; k < e; k++)
+          if (jobs[k].sq && jobs[k].nsq != (long)(jobs[k].M / 256) * (jobs[k].N / 256))
+            return ne_fail(NE_ERR_STATE, "grouped weight gradient %dx%d: %ld norm slots planned", jobs[k].M,
+                           jobs[k].N, jobs[k].nsq);
         ProfScope ps(c, jobs[i].fam);
         NE_CHECK(gemm_group_launch(c->dt, jobs[i].epi, ga, (int)(e - i), side ? c->st2 : c->st));
         i = e;
@@ -275,29 +303,70 @@ int gemm_split(ne_ctx *c, int fam, int layout, int epi, int M, int N, int K, con
 float *norm_part(ne_ctx *c, int site) { return c->gpart + (long)site * c->rms_slab; }
 float *qk_part(ne_ctx *c, int l) { return c->gpart + (long)(2 * c->L + 1) * c->rms_slab + (long)l * c->qk_slab; }
 
-// Sum-of-squares partials of G, reduced in slot order by the optimizer: layer l's matrix
-// gradients (its attention block Wqkv, Wo from lo[l].wqkv, then its FFN block W13, W2 from
-// lo[l].w13: GN_LAYER / 2 slots each), the embedding, the gains, then one slot per token row
+// Sum-of-squares partials of G, reduced in slot order by the optimizer: per layer the slots
+// of its Wqkv, Wo (the attention block, G from lo[l].wqkv), W13 and W2 (the FFN block, from
+// lo[l].w13) weight gradients, one per tile of each GEMM, written by the GEMM as it stores
+// the tile; the embedding gradient's GEMM (its tiles); the gains; then one slot per token row
 // for the change the embedding scatter makes to the row it updates.
-constexpr int GN_LAYER = 256, GN_EMBED = 512, GN_GAINS = 16;
-long gn_layer(const ne_ctx *c, int l) { (void)c; return (long)l * GN_LAYER; }
-long gn_embed(const ne_ctx *c) { return (long)c->L * GN_LAYER; }
-long gn_gains(const ne_ctx *c) { return gn_embed(c) + GN_EMBED; }
+constexpr int GN_GAINS = 16;
+enum { GN_WQKV = 0, GN_WO, GN_W13, GN_W2 };
+long gn_layer(const ne_ctx *c, int l) { return (long)l * c->gn_lay; }
+long gn_job(const ne_ctx *c, int l, int j) {
+  long o = gn_layer(c, l);
+  for (int i = 0; i < j; i++) o += c->gn_n[i];
+  return o;
+}
+long gn_attn_n(const ne_ctx *c) { return c->gn_n[GN_WQKV] + c->gn_n[GN_WO]; }
+long gn_embed(const ne_ctx *c) { return (long)c->L * c->gn_lay; }
+long gn_gains(const ne_ctx *c) { return gn_embed(c) + c->gn_emb; }
 long gn_rows(const ne_ctx *c) { return gn_gains(c) + GN_GAINS; }
 long gn_slots(const ne_ctx *c) { return gn_rows(c) + c->T; }
 long layer_params(const ne_ctx *c) { return (long)(c->QKV + c->Q + 3L * c->H) * c->D; }
 long layer_attn_params(const ne_ctx *c) { return (long)(c->QKV + c->Q) * c->D; }
 
-// Sum of squares of all of G into the slots the step fills (the per-row change slots of the
+// The slot counts: a layer's four weight gradients are queued as one batch (W2, W13, Wo,
+// Wqkv), which runs as one grouped launch of 256x256 tiles when gemm_group_fits, else as four
+// GEMMs tiled by gemm_launch's plan; the embedding gradient's GEMM runs alone.
+void plan_gn(ne_ctx *c) {
+  const int T = c->T, D = c->D, H = c->H;
+  const int M[4] = {c->QKV, D, 2 * H, D}, N[4] = {D, c->Q, D, H};  // GN_WQKV .. GN_W2
+  GemmArgs ga[4] = {};
+  for (int j = 0; j < 4; j++) {
+    ga[j].M = M[j];
+    ga[j].N = N[j];
+    ga[j].K = T;
+  }
+  c->gn_grouped = gemm_group_fits(ga, 4);
+  c->gn_lay = 0;
+  for (int j = 0; j < 4; j++) {
+    c->gn_n[j] = c->gn_grouped ? (long)(M[j] / 256) * (N[j] / 256) : gemm_sq_parts(EPI_F32, M[j], N[j], T, c->ws_elems);
+    c->gn_lay += c->gn_n[j];
+  }
+  // On short steps the embedding gradient's GEMM (V x D, K = T: at 256 tokens 622 MB of fp32
+  // written by a GEMM with little to compute) runs in row blocks, one beside each layer's
+  // backward: in one launch it slowed the two layers of the chain beside it by ~150 us.
+  // Block boundaries on the coarsest of 256, 128, 64 rows that divides the vocabulary.
+  const int gran = c->V % 256 == 0 ? 256 : c->V % 128 == 0 ? 128 : 64;
+  c->de_pieces = T <= 4096 ? std::min(c->L, c->V / gran) : 1;
+  c->de_rows.resize(c->de_pieces + 1);
+  c->gn_emb = 0;
+  for (int p = 0; p <= c->de_pieces; p++) c->de_rows[p] = (int)((long)(c->V / gran) * p / c->de_pieces) * gran;
+  for (int p = 0; p < c->de_pieces; p++)
+    c->gn_emb += gemm_sq_parts(EPI_F32, c->de_rows[p + 1] - c->de_rows[p], D, T, c->ws_elems);
+}
+
+// Sum of squares of all of G into the step's slots (the per-row change slots of the
 // embedding scatter read 0), on st: for an optimizer step that follows a direct gradient
 // write or no micro-step at all.
 int gn_sum_all(ne_ctx *c) {
   for (int l = 0; l < c->L; l++) {
     const LayerOff &o = c->lo[l];
-    NE_CHECK(launch_sumsq2(c->G + o.wqkv, layer_attn_params(c), c->G + o.w13, layer_params(c) - layer_attn_params(c),
-                           c->gn_part + gn_layer(c, l), GN_LAYER / 2, c->st));
+    const long na = gn_attn_n(c), nf = c->gn_lay - na;
+    NE_CHECK(launch_sumsq(c->G + o.wqkv, layer_attn_params(c), c->gn_part + gn_layer(c, l), (int)na, c->st));
+    NE_CHECK(launch_sumsq(c->G + o.w13, layer_params(c) - layer_attn_params(c), c->gn_part + gn_layer(c, l) + na,
+                          (int)nf, c->st));
   }
-  NE_CHECK(launch_sumsq(c->G + c->off_E, (long)c->V * c->D, c->gn_part + gn_embed(c), GN_EMBED, c->st));
+  NE_CHECK(launch_sumsq(c->G + c->off_E, (long)c->V * c->D, c->gn_part + gn_embed(c), (int)c->gn_emb, c->st));
   NE_CHECK(launch_sumsq(c->G + c->n_decay, c->n_params - c->n_decay, c->gn_part + gn_gains(c), GN_GAINS, c->st));
   return launch_fill_f32((float *)(c->gn_part + gn_rows(c)), 0.f, 2L * c->T, c->st);
 }
@@ -421,12 +490,14 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ce_tgt, T); pl.add(&c->ce_lse, T); pl.add(&c->ce_rows, T); pl.add(&c->loss, 4);
   pl.add(&c->tok_in, 4 * T);  // inputs, targets, id chains: filled by one copy
   pl.add(&c->cosb, (size_t)c->S * c->HD / 2); pl.add(&c->sinb, (size_t)c->S * c->HD / 2);
-  pl.add(&c->gn_part, (size_t)gn_slots(c)); pl.add(&c->gscale, 4);
+  pl.add(&c->gscale, 4);
   pl.add(&c->stats_part, 4 * NE_STATS_BLOCKS); pl.add(&c->gnorm, 4); pl.add(&c->ovf, 32);
   // split-K partials: up to 32 splits of a [T, D] result (the LM-head dX of a short step)
   c->ws_elems = std::min<long>(32L << 20, std::max<long>(8L << 20, (long)T * D * 32));
   pl.add(&c->ws, (size_t)c->ws_elems);
   pl.add(&c->ws2, (size_t)c->ws_elems);
+  plan_gn(c);
+  pl.add(&c->gn_part, (size_t)gn_slots(c));
   // gain-gradient partials of every norm site (2L+1 RMSNorms, L QK-norm pairs), summed by one
   // ordered launch at the end of the backward
   c->rms_slab = rmsnorm_bwd_part_elems(c->T, c->D);
@@ -440,9 +511,12 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st2, hipStreamNonBlocking), "stream"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event"))) goto fail;
-  c->ev_adam.assign(c->L + 1, nullptr);
+  c->ev_adam.assign(c->L + 2, nullptr);
+  c->tl.fwd_l.assign(c->L, nullptr);  // the step names them whether or not the timeline is on
+  c->tl.bwd_l.assign(c->L, nullptr);
   for (auto &e : c->ev_adam)
     if ((rc = ne_hip_status(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event"))) goto fail;
+  if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_lookup, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipMalloc(&c->arena, pl.total), "hipMalloc(arena)"))) goto fail;
   pl.assign((char *)c->arena);
   c->tok_tgt = c->tok_in + T;
@@ -514,6 +588,7 @@ extern "C" void ne_destroy(ne_ctx *c) {
   if (c->ev_join) hipEventDestroy(c->ev_join);
   for (auto e : c->ev_adam)
     if (e) hipEventDestroy(e);
+  if (c->ev_lookup) hipEventDestroy(c->ev_lookup);
   for (int i = 0; i < 2; i++)
     if (c->tok_ev[i]) hipEventDestroy(c->tok_ev[i]);
   decode_free(c);
@@ -522,6 +597,13 @@ extern "C" void ne_destroy(ne_ctx *c) {
     hipEventDestroy(r.b);
   }
   for (auto e : c->prof.pool) hipEventDestroy(e);
+  for (hipEvent_t e : {c->tl.start, c->tl.lookup, c->tl.fwd, c->tl.cls, c->tl.bwd, c->tl.join, c->tl.end, c->tl.opt0,
+                       c->tl.opt1, c->tl.upd0, c->tl.upd1})
+    if (e) hipEventDestroy(e);
+  for (auto e : c->tl.fwd_l)
+    if (e) hipEventDestroy(e);
+  for (auto e : c->tl.bwd_l)
+    if (e) hipEventDestroy(e);
   if (c->arena) hipFree(c->arena);
   if (c->cids) hipFree(c->cids);
   if (c->cE) hipFree(c->cE);
@@ -598,9 +680,64 @@ extern "C" int ne_set_state(ne_ctx *c, const ne_train_state *st) {
 
 // ------------------------------------------------------------------- training step ----
 
+// The deferred AdamW pass of the last optimizer step, enqueued on st2 by the training step
+// that follows it, forked from st at the step's start.  Chunks in order: the gains
+// (ev_adam[0]), layer l's matrices (ev_adam[1 + l]), then the embedding (ev_adam[L + 1]) after
+// ev_lookup (the step's lookup, which computes the updated rows itself, has read them).  The
+// forward waits for each chunk just before it reads what the chunk writes, the classifier for
+// the embedding's.  The step enqueues the chunks as its forward goes, UPD_AHEAD layers ahead
+// of the layer it enqueues: all of them up front kept the GPU's forward waiting 0.2-0.3 ms for
+// the host.  Qwen3-0.6B, 256 tokens, one box, ms per step: the embedding last 7.94, its rows
+// in pieces after each of the last 14 layers 7.95, after every layer 8.06; the embedding
+// first with the lookup waiting for it (the former order) 8.02-8.03.  The forward runs at the
+// pace of the pass beside it (~140-150 us per layer against ~60 alone); over the forward the
+// two move ~19.4 GB in ~4 ms, about 90% of what a plain device copy streams.
+constexpr int UPD_AHEAD = 2;
+// The chunks beside the forward run at most this many work-groups: the update streams more
+// slowly and the forward's small GEMMs, which wait on HBM behind it, less so (same step, ms:
+// 256 work-groups 8.16, 384 7.94-8.06, 512 8.02; the former order: uncapped 8.24, 768 8.39,
+// 512 8.08-8.19, 384 7.97, 256 8.18).  Four float4 of each stream per thread instead of two
+// measured the same (8.02).
+constexpr int UPD_MAX_GROUPS = 384;
+struct UpdateQueue {
+  ne_ctx *c;
+  int next = -1;  // next chunk: -1 the gains, l < L the layer l, L the embedding
+  int chunk(long off, long n, long n_decay) {
+    AdamArgs ch = c->upd;
+    ch.p = c->P + off; ch.g = c->G + off; ch.m = c->M + off; ch.v = c->Vm + off; ch.pb = c->Pb + off;
+    ch.n = n; ch.n_decay = n_decay;
+    ch.max_groups = UPD_MAX_GROUPS;
+    ProfScope ps(c, NE_PROF_ADAM, c->st2);  // per launch: the family time is the sum of durations
+    return launch_adam(c->dt, ch, c->st2);
+  }
+  // enqueue the chunks up to and including chunk l (l = L: everything)
+  int upto(int l) {
+    const int L = c->L;
+    for (; next <= std::min(l, L); next++) {
+      if (next == -1) {
+        c->adam_pending = true;
+        NE_CHECK(tl_mark(c, c->tl.upd0, c->st2));
+        NE_CHECK(chunk(c->n_decay, c->n_params - c->n_decay, 0));
+        NE_HIP(hipEventRecord(c->ev_adam[0], c->st2));
+      } else if (next < L) {
+        NE_CHECK(chunk(c->lo[next].wqkv, layer_params(c), layer_params(c)));
+        NE_HIP(hipEventRecord(c->ev_adam[1 + next], c->st2));
+      } else {
+        NE_HIP(hipStreamWaitEvent(c->st2, c->ev_lookup, 0));
+        const long ne = (long)c->V * c->D;
+        NE_CHECK(chunk(c->off_E, ne, ne));
+        NE_HIP(hipEventRecord(c->ev_adam[L + 1], c->st2));
+        NE_CHECK(tl_mark(c, c->tl.upd1, c->st2));
+        c->tl.opt_ok = c->tl.on;
+      }
+    }
+    return 0;
+  }
+};
+
 // Enqueue one forward+backward on c->st with token ids already in c->tok_in/tok_tgt.
 // Free of host synchronisation and memsets, so it can be captured into a HIP graph.
-static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two, bool adam_ov = false) {
+static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two, bool upd = false) {
   const int T = c->T, S = c->S, D = c->D, H = c->H, Q = c->Q, KV = c->KV, QKV = c->QKV, V = c->V;
   const float alpha = c->c.res_alpha, eps = c->c.norm_eps;
   const h16_t *Pb = c->Pb;
@@ -621,21 +758,35 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
   // gradients instead of accumulating (no zeroing pass, no read of G); only the gains,
   // which accumulate through atomics, are cleared.
   const int EPI_DW = fresh ? EPI_F32 : EPI_F32_ACC;
-  // The optimizer update of the previous step may still run on st2 (adam_ov): chunk 0 (the
-  // embedding and the gains, read and written below first), then chunk 1 + l before layer l.
-  // The last wait comes before the backward, the first writer of G.
+  // With upd, the deferred optimizer update (UpdateQueue) runs on st2 beside the forward:
+  // the lookup applies it to the rows it reads, then the step waits for chunk 0 (the gains,
+  // whose gradients the fresh fill below clears), chunk 1 + l before layer l and the last
+  // embedding piece before the classifier, all before the backward, the first writer of G.
   auto wait_update = [&](int k) -> int {
-    if (adam_ov) NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[k], 0));
+    if (upd) NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[k], 0));
     return 0;
   };
-  NE_CHECK(wait_update(0));
-  if (fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
-
+  UpdateQueue uq{c};
+  NE_CHECK(tl_mark(c, c->tl.start));
   // ---------------- forward ----------------
   {
     ProfScope ps(c, NE_PROF_EMBED);
-    NE_CHECK(launch_embed_fwd(P + c->off_E, c->tok_in, c->act[0].x_in, T, D, c->st));
+    if (upd) {
+      NE_HIP(hipEventRecord(c->ev_fork, c->st));
+      NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
+      NE_CHECK(uq.upto(-1));  // the gains
+      NE_CHECK(launch_embed_fwd_adam(P + c->off_E, G + c->off_E, c->M + c->off_E, c->Vm + c->off_E, c->tok_in,
+                                     c->act[0].x_in, T, D, c->upd, c->st));
+      NE_HIP(hipEventRecord(c->ev_lookup, c->st));
+      NE_CHECK(uq.upto(UPD_AHEAD - 1));
+    } else {
+      NE_CHECK(launch_embed_fwd(P + c->off_E, c->tok_in, c->act[0].x_in, T, D, c->st));
+    }
   }
+  NE_CHECK(wait_update(0));
+  NE_CHECK(tl_mark(c, c->tl.lookup));
+  if (fresh) NE_CHECK(launch_fill_f32(G + c->n_decay, 0.f, c->n_params - c->n_decay, c->st));
+
   // The residual-producing GEMMs (Wo, W2) leave their split-K partials to the RMSNorm that
   // reads their output; sp_x describes the pending partials of the next norm's input.
   SplitIn sp_x;
@@ -643,6 +794,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
     float *x_next = (l + 1 < c->L) ? c->act[l + 1].x_in : c->xL;
+    if (upd) NE_CHECK(uq.upto(l + UPD_AHEAD));
     NE_CHECK(wait_update(1 + l));
     {
       ProfScope ps(c, NE_PROF_NORM);
@@ -678,12 +830,16 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     }
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_FWD, GEMM_NT, EPI_RESID, T, D, H, a.gate, H, Pb + o.w2, H, x_next, &sp_x,
                         a.x2, alpha));
+    NE_CHECK(tl_mark(c, c->tl.fwd_l[l]));
   }
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_rmsnorm_fwd(dt, c->xL, P + c->off_gfinal, c->xf, c->rf, T, D, eps, ovf + OVF_NORM_FWD, c->st,
                                 sp_x));
   }
+  NE_CHECK(tl_mark(c, c->tl.fwd));
+  if (upd) NE_CHECK(uq.upto(c->L));
+  NE_CHECK(wait_update(c->L + 1));
   // classifier: the tied embedding, or its compact rows (vocabulary compaction; padding
   // columns cv..cvp are masked out of the softmax)
   const bool compact = c->cv > 0;
@@ -715,12 +871,24 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     hipStream_t sd = wq.on ? c->st2 : c->st;
     if (fresh) NE_CHECK(launch_fill_f32(G + c->off_E, 0.f, (long)V * D, sd));
     NE_CHECK(launch_scatter_add_rows(G + c->off_E, c->gcE, c->cids, c->cv, D, sd));
-  } else {
-    NE_CHECK(wq.add(NE_PROF_CE, EPI_DW, V, D, T, c->dlogits, V, c->xf, D, G + c->off_E, u));
+    // the embedding gradient as it stands before the input-embedding scatter (which reports
+    // its change per row)
+    NE_CHECK(wq.sumsq(G + c->off_E, (long)V * D, gn_embed(c), (int)c->gn_emb));
   }
-  // the embedding gradient as it stands before the input-embedding scatter (which reports
-  // its change per row)
-  NE_CHECK(wq.sumsq(G + c->off_E, (long)V * D, gn_embed(c), GN_EMBED));
+  // The embedding gradient's GEMM (row block p of de_pieces; compaction: none), whose tiles
+  // leave the embedding gradient's sum of squares as it stands before the input-embedding
+  // scatter (which reports its change per row).
+  long de_slot = gn_embed(c);
+  auto add_de = [&](int p) -> int {
+    if (compact || p >= c->de_pieces) return 0;
+    const int r0 = c->de_rows[p], r1 = c->de_rows[p + 1];
+    const long ns = gemm_sq_parts(EPI_F32, r1 - r0, D, T, c->ws_elems);
+    NE_CHECK(wq.add(NE_PROF_CE, EPI_DW, r1 - r0, D, T, c->dlogits + r0, V, c->xf, D, G + c->off_E + (long)r0 * D, u,
+                    c->gn_part + de_slot, ns));
+    de_slot += ns;
+    return 0;
+  };
+  if (c->de_pieces == 1) NE_CHECK(add_de(0));
   NE_CHECK(wq.flush());
   NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, Vc, c->dlogits, Vc, Ecls, D, c->dtmp, &sp_d));
   {
@@ -729,6 +897,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
                                 c->dbf + 2 * (size_t)(c->L - 1) * TD, alpha, G + c->off_gfinal, u, T, D,
                                 ovf + OVF_NORM_BWD, norm_part(c, 0), c->st, sp_d, true, c->rms_bwd_ref));
   }
+  NE_CHECK(tl_mark(c, c->tl.cls));
   for (int l = c->L - 1; l >= 0; l--) {
     LayerAct &a = c->act[l];
     const LayerOff &o = c->lo[l];
@@ -737,8 +906,10 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     // FFN: dbf_ffn = alpha * dx
     NE_CHECK(gemm(c, NE_PROF_GEMM_BWD, OVF_DH13, GEMM_NN, EPI_SWIGLU_BWD, T, H, D, dbf_ffn, D, Pb + o.w2, H, dh13,
                   2 * H, a.h13, 2 * H));
-    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, H, T, dbf_ffn, D, a.gate, H, G + o.w2, u));
-    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, 2 * H, D, T, dh13, 2 * H, a.x2n, D, G + o.w13, u));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, H, T, dbf_ffn, D, a.gate, H, G + o.w2, u,
+                    c->gn_part + gn_job(c, l, GN_W2), c->gn_n[GN_W2]));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, 2 * H, D, T, dh13, 2 * H, a.x2n, D, G + o.w13, u,
+                    c->gn_part + gn_job(c, l, GN_W13), c->gn_n[GN_W13]));
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, 2 * H, dh13, 2 * H, Pb + o.w13, D, c->dtmp,
                         &sp_d));
     {
@@ -768,10 +939,11 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
                                   c->NH, c->NKV, c->HD, ovf + OVF_DQKV, c->c.qk_norm ? qk_part(c, l) : nullptr,
                                   c->st, true, at.part, ovf + OVF_DV));
     }
-    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u));
-    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u));
-    NE_CHECK(wq.sumsq(G + o.wqkv, layer_attn_params(c), gn_layer(c, l), GN_LAYER / 2, G + o.w13,
-                      layer_params(c) - layer_attn_params(c)));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, D, Q, T, dbf_att, D, a.attn, Q, G + o.wo, u,
+                    c->gn_part + gn_job(c, l, GN_WO), c->gn_n[GN_WO]));
+    NE_CHECK(wq.add(NE_PROF_GEMM_BWD, EPI_DW, QKV, D, T, dqkv, QKV, a.xn, D, G + o.wqkv, u,
+                    c->gn_part + gn_job(c, l, GN_WQKV), c->gn_n[GN_WQKV]));
+    if (c->de_pieces > 1) NE_CHECK(add_de(c->L - 1 - l));
     NE_CHECK(wq.flush());  // one hand-over per layer
     NE_CHECK(gemm_split(c, NE_PROF_GEMM_BWD, GEMM_NN, EPI_F32, T, D, QKV, dqkv, QKV, Pb + o.wqkv, D, c->dtmp, &sp_d));
     {
@@ -781,8 +953,11 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
                                   l > 0 ? c->dbf + 2 * (size_t)(l - 1) * TD : nullptr, alpha, G + o.g_att, u, T, D,
                                   ovf + OVF_NORM_BWD, norm_part(c, 2 + 2 * l), c->st, sp_d, true, c->rms_bwd_ref));
     }
+    NE_CHECK(tl_mark(c, c->tl.bwd_l[l]));
   }
+  NE_CHECK(tl_mark(c, c->tl.bwd));
   NE_CHECK(wq.join());
+  NE_CHECK(tl_mark(c, c->tl.join));
   {
     ProfScope ps(c, NE_PROF_NORM);
     NE_CHECK(launch_colsum_batch(c->cs_jobs, c->cs_njobs, std::max(c->D, c->HD), c->st));
@@ -793,6 +968,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
     NE_CHECK(launch_embed_bwd_chain(G + c->off_E, c->tok_in, c->tok_nxt, c->tok_first, c->dx, u, T, D, c->st,
                                     c->gn_part + gn_rows(c)));
   }
+  NE_CHECK(tl_mark(c, c->tl.end));
   return 0;
 }
 
@@ -862,13 +1038,16 @@ extern "C" int ne_train_step(ne_ctx *c, const int32_t *tokens, float loss_scale,
   // launched eagerly: replaying it from a graph measured slower than in order on one stream
   // (the branches' hand-overs cost more in a graph than between eager launches).
   const bool two = c->overlap_wgrad && !profiled;
-  // an update still running on st2: the two-stream step waits for it chunk by chunk
-  const bool adam_ov = c->adam_pending && two;
-  if (!adam_ov) NE_CHECK(adam_join(c));
+  // a deferred update: the two-stream step runs it beside its forward (UpdateQueue)
+  const bool upd = c->upd_deferred && two;
+  if (upd) c->upd_deferred = false;
+  else NE_CHECK(adam_join(c));
   c->gn_ready = c->gn_parts_ok = false;
   c->last_u = loss_scale / (float)T / c->gs;  // the factor train_step_enqueue gives the fp32 sinks
-  if (c->use_graphs && !profiled && !two) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
-  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two, adam_ov));
+  // the timeline's events need eager launches too
+  if (c->use_graphs && !profiled && !two && !c->tl.on) NE_CHECK(train_step_graph(c, loss_scale, fresh, false));
+  else NE_CHECK(train_step_enqueue(c, loss_scale, fresh, two, upd));
+  c->tl.step_ok = c->tl.on;
   c->adam_pending = false;  // the forward waited for the last chunk before the backward
   c->gn_ready = true;  // the step refreshed every sum-of-squares partial of G
   c->stats_ok = true;
@@ -977,6 +1156,7 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
     if (gnorm_out) *gnorm_out = NAN;
     return 1;
   }
+  NE_CHECK(tl_mark(c, c->tl.opt0));
   {
     ProfScope ps(c, NE_PROF_GNORM);
     // the last micro-step left the partials of G as it is now; otherwise (G written through
@@ -989,6 +1169,7 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
       NE_CHECK(launch_clip_finalize(c->gn_part, (int)gn_slots(c), grad_scale, clip, c->gscale, c->gnorm, c->st));
     }
   }
+  NE_CHECK(tl_mark(c, c->tl.opt1));
   c->gn_parts_ok = true;
   c->gn_gsc = grad_scale;
   c->state.adam_t += 1;
@@ -1001,36 +1182,17 @@ extern "C" int ne_optimizer_step(ne_ctx *c, float lr, float b1, float b2, float 
   a.bc2 = 1.f - powf(b2, (float)t);
   a.gscale = c->gscale; a.zero_grad = 0;
   if (c->overlap_wgrad) {
-    // on st2 in chunks, so that the next step's forward can start on the embedding and layer
-    // 0 while the later layers are still being updated (ne_train_step waits per chunk)
-    NE_HIP(hipEventRecord(c->ev_fork, c->st));
-    NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
-    auto chunk = [&](long off, long n, long n_decay, hipEvent_t done) -> int {
-      AdamArgs ch = a;
-      ch.p = c->P + off; ch.g = c->G + off; ch.m = c->M + off; ch.v = c->Vm + off; ch.pb = c->Pb + off;
-      ch.n = n; ch.n_decay = n_decay;
-      {
-        ProfScope ps(c, NE_PROF_ADAM, c->st2);  // per launch: the family time is the sum of durations
-        NE_CHECK(launch_adam(c->dt, ch, c->st2));
-      }
-      NE_HIP(hipEventRecord(done, c->st2));
-      return 0;
-    };
-    NE_CHECK(chunk(c->off_E, c->n_params - c->off_E, c->n_decay - c->off_E, c->ev_adam[0]));
-    // The layer launches run beside the next forward, whose small GEMMs wait on HBM behind
-    // them: at 384 work-groups (1.5 per CU) the update streams slower and the forward less
-    // so.  Qwen3-0.6B, 256 tokens, one box: uncapped 8.24 ms per step, 768: 8.39, 512:
-    // 8.08-8.19, 384: 7.97, 256: 8.18.  The embedding's launch, which the lookup waits for
-    // with nothing beside it, keeps the full grid.
-    a.max_groups = 384;
-    for (int l = 0; l < c->L; l++) {
-      const long n = layer_params(c);
-      NE_CHECK(chunk(c->lo[l].wqkv, n, n, c->ev_adam[1 + l]));
-    }
-    c->adam_pending = true;
+    // left to the next training step, which runs it beside its forward (UpdateQueue)
+    c->upd = a;
+    c->upd_deferred = true;
   } else {
-    ProfScope ps(c, NE_PROF_ADAM);
-    NE_CHECK(launch_adam(c->dt, a, c->st));
+    NE_CHECK(tl_mark(c, c->tl.upd0));
+    {
+      ProfScope ps(c, NE_PROF_ADAM);
+      NE_CHECK(launch_adam(c->dt, a, c->st));
+    }
+    NE_CHECK(tl_mark(c, c->tl.upd1));
+    c->tl.opt_ok = c->tl.on;
   }
   c->grads_fresh = true;
   c->state.lr = lr;
@@ -1063,7 +1225,7 @@ extern "C" int ne_grad_norm_parts(ne_ctx *c, float *out) {
   NE_HIP(hipStreamSynchronize(c->st));
   double attn = 0, ffn = 0, embed = 0, total = 0;
   for (int l = 0; l < c->L; l++)
-    for (int k = 0; k < GN_LAYER; k++) (k < GN_LAYER / 2 ? attn : ffn) += h[gn_layer(c, l) + k];
+    for (long k = 0; k < c->gn_lay; k++) (k < gn_attn_n(c) ? attn : ffn) += h[gn_layer(c, l) + k];
   for (long k = gn_embed(c); k < gn_gains(c); k++) embed += h[k];
   for (long k = gn_rows(c); k < gn_slots(c); k++) embed += h[k];
   for (double v : h) total += v;
@@ -1099,6 +1261,50 @@ extern "C" int ne_step_stats(ne_ctx *c, float *out) {
 }
 
 // ------------------------------------------------------------------------ profiling ----
+
+extern "C" int ne_timeline(ne_ctx *c, int on) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  Timeline &t = c->tl;
+  if (on && !t.start) {
+    std::vector<hipEvent_t *> evs = {&t.start, &t.lookup, &t.fwd, &t.cls, &t.bwd, &t.join, &t.end,
+                                     &t.opt0,  &t.opt1,   &t.upd0, &t.upd1};
+    for (auto &e : t.fwd_l) evs.push_back(&e);
+    for (auto &e : t.bwd_l) evs.push_back(&e);
+    for (hipEvent_t *e : evs) NE_HIP(hipEventCreate(e));
+  }
+  t.on = on != 0;
+  t.step_ok = t.opt_ok = false;
+  return 0;
+}
+
+extern "C" int ne_step_timeline(ne_ctx *c, float *out, float *layer_fwd, float *layer_bwd) {
+  if (!c || !out) return ne_fail(NE_ERR_ARG, "null argument");
+  const Timeline &t = c->tl;
+  if (!t.step_ok) return ne_fail(NE_ERR_STATE, "step timeline: no training step has run with the timeline on");
+  NE_HIP(hipEventSynchronize(t.end));
+  auto ms = [](hipEvent_t a, hipEvent_t b) -> float {
+    float v = 0.f;
+    return hipEventElapsedTime(&v, a, b) == hipSuccess ? v : NAN;
+  };
+  for (int i = 0; i < NE_TL_COUNT; i++) out[i] = NAN;
+  out[NE_TL_WAIT] = ms(t.start, t.lookup);
+  out[NE_TL_FWD] = ms(t.lookup, t.fwd);
+  out[NE_TL_CLS] = ms(t.fwd, t.cls);
+  out[NE_TL_BWD] = ms(t.cls, t.bwd);
+  out[NE_TL_DWAIT] = ms(t.bwd, t.join);
+  out[NE_TL_TAIL] = ms(t.join, t.end);
+  out[NE_TL_STEP] = ms(t.start, t.end);
+  if (t.opt_ok) {
+    NE_HIP(hipEventSynchronize(t.upd1));
+    out[NE_TL_OPT] = ms(t.opt0, t.opt1);
+    out[NE_TL_UPDATE] = ms(t.upd0, t.upd1);
+  }
+  for (int l = 0; l < c->L; l++) {
+    if (layer_fwd) layer_fwd[l] = ms(l ? t.fwd_l[l - 1] : t.lookup, t.fwd_l[l]);
+    if (layer_bwd) layer_bwd[l] = ms(l + 1 < c->L ? t.bwd_l[l + 1] : t.cls, t.bwd_l[l]);
+  }
+  return 0;
+}
 
 extern "C" int ne_prof_enable(ne_ctx *c, int mask) {
   const int on = mask;

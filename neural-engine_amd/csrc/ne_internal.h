@@ -68,6 +68,9 @@ struct GemmArgs {
   int col0;                  // CE epilogues: the full output's column of this launch's column 0
   int tile0;                 // EPI_CE_FWD: the partial slot of this launch's first N tile
   int part_ld;               // EPI_CE_FWD: partial slots per row (0: N / BN)
+  double *sq;                // EPI_F32 / EPI_F32_ACC (nullable): sums of squares of C as stored,
+                             // one slot per output tile (mt * N/BN + nt) or, with split-K, per
+                             // block of the ordered reduction; gemm_sq_parts slots in all
 };
 
 // Up to GEMM_GROUP_MAX GEMMs run as one launch (gemm_group_launch): problem p's tiles are
@@ -96,6 +99,10 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *spl
 int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per row it writes
 // K splits gemm_launch would use for this shape with a workspace of ws_elems floats (1: none).
 int gemm_splits(int epi, int M, int N, int K, long ws_elems);
+// Sum-of-squares slots (GemmArgs::sq) gemm_launch writes for this shape (EPI_F32 /
+// EPI_F32_ACC, no deferred reduction), ws_elems as for gemm_splits; with gemm_group_launch
+// a problem writes (M / 256) * (N / 256).
+long gemm_sq_parts(int epi, int M, int N, int K, long ws_elems);
 // Weight-gradient GEMMs (layout TN, fp32 out: EPI_F32 or EPI_F32_ACC, one epilogue for all)
 // of n <= GEMM_GROUP_MAX problems as one launch of 256x256 tiles, each over its whole K range
 // (no split-K, no workspace).  gemm_group_fits: whether a set of shapes takes this path (every
@@ -208,10 +215,10 @@ struct AdamArgs {
   int max_groups;       // work-group cap of the launch (0: the streaming default)
 };
 int launch_sumsq(const float *g, long n, double *partials, int nparts, hipStream_t s);
-// Sums of squares of two ranges in one launch: g1 into partials[0, nparts_each), g2 into
-// partials[nparts_each, 2 nparts_each).
-int launch_sumsq2(const float *g1, long n1, const float *g2, long n2, double *partials, int nparts_each,
-                  hipStream_t s);
+// Embedding lookup x[t] = E[tok[t]] with the AdamW update a (weight decay on; its gscale on
+// the device) applied to the rows read, as adam_kernel would leave them; writes only x.
+int launch_embed_fwd_adam(const float *E, const float *G, const float *M, const float *V, const int32_t *tok,
+                          float *x, int T, int D, const AdamArgs &a, hipStream_t s);
 int launch_clip_finalize(const double *partials, int nparts, float grad_scale, float clip,
                          float *gscale_out, float *gnorm_out, hipStream_t s);
 int launch_adam(int dt, const AdamArgs &a, hipStream_t s);

@@ -21,6 +21,7 @@ NE_BF16, NE_FP16 = 0, 1
 PROF_FAMILIES = ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "norm", "ce", "adam", "gnorm",
                  "embed", "decode")
 LAYER_TENSORS = ("Wq", "Wk", "Wv", "Wo", "W1", "W2", "W3", "rms_att", "rms_ffn")
+TIMELINE_PHASES = ("wait", "fwd", "cls", "bwd", "dwait", "tail", "step", "opt", "update")
 OVF_SITES = ("norm_fwd", "qkv", "h13", "swiglu", "dlogits", "norm_bwd", "dh13", "dattn", "dv", "dqkv")
 
 # every symbol include/ne.h declares
@@ -30,7 +31,7 @@ EXPORTS = (
     "ne_rmsnorm_bwd_formula", "ne_zero_grads",
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_set_vocab_map",
-    "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
+    "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_timeline", "ne_step_timeline", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_gemm_wgrad_group", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
     "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
@@ -123,6 +124,8 @@ def lib():
         "ne_prof_enable": (I, [P, I]),
         "ne_prof_reset": (I, [P]),
         "ne_prof_get": (I, [P, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
+        "ne_timeline": (I, [P, I]),
+        "ne_step_timeline": (I, [P, P, P, P]),
         "ne_k_rmsnorm_fwd": (I, [I, P, P, P, P, I, I, F, P]),
         "ne_k_rmsnorm_bwd": (I, [I, P, P, P, P, P, P, P, F, P, F, I, I, P]),
         "ne_k_gemm": (I, [I, I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
@@ -322,6 +325,20 @@ class Model:
 
     def prof_reset(self):
         check(lib().ne_prof_reset(self._h), "prof_reset")
+
+    def timeline(self, on=True):
+        """Record the step's phase boundaries with HIP events (ne_timeline)."""
+        check(lib().ne_timeline(self._h, int(bool(on))), "timeline")
+
+    def step_timeline(self, layers=False):
+        """Phases of the last step in ms (TIMELINE_PHASES), and with layers=True the per-layer
+        forward and backward times."""
+        out = np.zeros(len(TIMELINE_PHASES), np.float32)
+        lf = np.zeros(self.cfg.n_layers, np.float32)
+        lb = np.zeros(self.cfg.n_layers, np.float32)
+        check(lib().ne_step_timeline(self._h, _ptr(out), _ptr(lf), _ptr(lb)), "step_timeline")
+        ph = {k: float(v) for k, v in zip(TIMELINE_PHASES, out)}
+        return (ph, lf, lb) if layers else ph
 
     def prof(self):
         out = {}

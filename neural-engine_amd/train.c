@@ -225,7 +225,18 @@ int main(int argc, char *argv[]) {
     }
     printf("Vocab compaction: %d \u2192 %d active tokens (%.1fx reduction)\n", VOCAB, cv, (float)VOCAB / cv);
   }
-  printf("Context created in %.0fms\n\n", create_ms);
+  /* TD/train.m:302 (read by TR/dashboard.py's RE_COMPILED): nothing is compiled at run time
+   * here, the gfx950 code objects are prebuilt into the library; the time is context creation */
+  printf("Compiled 0 kernels in %.0fms (gfx950 code prebuilt; context created)\n\n", create_ms);
+  /* phase timing of the printed steps (HIP events; the schedule is unchanged) */
+  int rc = 0;
+  if ((rc = ne_timeline(ctx, 1))) {
+    fail("ne_timeline", rc);
+    munmap(data, data_len);
+    close(fd);
+    ne_destroy(ctx);
+    return 1;
+  }
 
   int32_t tok[SEQ + 1];
   float last_loss = 999.0f;
@@ -233,7 +244,6 @@ int main(int argc, char *argv[]) {
   double total_train_ms = 0;
   int total_steps_done = 0;
   const double t_wall_start = now_ms();
-  int rc = 0;
   srand48(42 + start_step);
 
   for (int step = start_step; step < total_steps; step++) {
@@ -263,7 +273,24 @@ int main(int argc, char *argv[]) {
         fail("ne_step_stats", rc);
         break;
       }
-      printf("  timing: step=%.1f (fwd+bwd on GPU)\n", step_ms);
+      /* TD/train.m:764-767.  GPU time of the step's phases on its stream: ane_fwd the forward
+       * chain, io_fwd the wait for the previous update's share that the forward reads first
+       * (the device counterpart of restaging weights), ane_bwd the backward chain, cls the
+       * classifier and cross-entropy, dwait the wait for the weight-gradient stream; RMSNorm,
+       * residual, GQA and RoPE run inside those chains (fused kernels, no separate phase) and
+       * nothing is copied for the weight gradients, so rms, io_bwd, rms_bwd, resid, gqa, rope
+       * and dw read 0; gap is the rest of the step's wall time (gain sums, embedding scatter,
+       * host). */
+      float ph[NE_TL_COUNT];
+      if ((rc = ne_step_timeline(ctx, ph, NULL, NULL))) {
+        fail("ne_step_timeline", rc);
+        break;
+      }
+      const double timed = ph[NE_TL_FWD] + ph[NE_TL_WAIT] + ph[NE_TL_BWD] + ph[NE_TL_CLS] + ph[NE_TL_DWAIT];
+      printf("  timing: ane_fwd=%.1f io_fwd=%.1f rms=%.1f ane_bwd=%.1f io_bwd=%.1f rms_bwd=%.1f cls=%.1f dw=%.1f "
+             "dwait=%.1f resid=%.1f gqa=%.1f rope=%.1f [gap=%.1f]\n",
+             ph[NE_TL_FWD], ph[NE_TL_WAIT], 0.0, ph[NE_TL_BWD], 0.0, 0.0, ph[NE_TL_CLS], 0.0, ph[NE_TL_DWAIT], 0.0, 0.0,
+             0.0, step_ms - timed);
       printf("step %-4d loss=%.4f  lr=%.2e  %.1fms/step  x[%.2f,%.2f] dy[%.3e,%.3e]\n", step, loss, lr, step_ms,
              xs[0], xs[1], xs[2], xs[3]);
     }

@@ -155,6 +155,15 @@ def test_scratch_init_and_dashboard_lines(tmp_path):
     for f in full:
         xmn, xmx, dmn, dmx = map(float, f[1:])
         assert xmn < 0 < xmx and dmn < 0 < dmx
+    # TD/train.m:302 (TR/dashboard.py RE_COMPILED) and the per-phase timing line of
+    # TD/train.m:766, printed with each step line: phases in ms, non-negative, within the step
+    assert re.search(r"Compiled (\d+) kernels in (\d+)ms", out)
+    tl = re.findall(r"timing: ane_fwd=(\S+) io_fwd=(\S+) rms=(\S+) ane_bwd=(\S+) io_bwd=(\S+) rms_bwd=(\S+) "
+                    r"cls=(\S+) dw=(\S+) dwait=(\S+) resid=(\S+) gqa=(\S+) rope=(\S+) \[gap=(\S+)\]", out)
+    assert len(tl) == len(steps)
+    for t in tl:
+        v = list(map(float, t))
+        assert min(v[:12]) >= 0 and v[0] > 0 and v[3] > 0, t   # %.1f ms: the tiny classifier can read 0.0
     gl = re.findall(r"grad_norm=(\S+)\s+attn=(\S+) ffn=(\S+) embed=(\S+)", out)
     assert len(gl) == 1
     tot, att, ffn, emb = map(float, gl[0])

@@ -471,6 +471,41 @@ def test_step_identical_across_launch_modes(compact):
                 np.testing.assert_array_equal(a[n], b[n], err_msg=n)
 
 
+def test_step_timeline():
+    """ne_step_timeline: the phases of the last step (HIP events at its phase boundaries on
+    the step stream) are non-negative and add up to no more than the step, each layer's
+    forward and backward time is positive and their sums stay inside their phases; the
+    timeline changes no result (the losses of the same steps with it off are identical)."""
+    cfg = om.tiny(**CASES["qwen3"], n_layers=3)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2, 3)]
+    runs = []
+    for on in (False, True):
+        m = ne.Model.from_oracle(cfg, batch=2)
+        m.set_params(P)
+        m.timeline(on)
+        if on:
+            with pytest.raises(ne.NEError):
+                m.step_timeline()      # no step with the timeline on yet
+        losses = []
+        for t in toks:
+            losses.append(m.train_step(t, 256.0))
+            m.optimizer_step(3e-4, 0.9, 0.95, 1e-8, 0.1, grad_scale=1 / 256, clip=1.0)
+        losses.append(m.train_step(toks[0], 256.0))
+        if on:
+            ph, lf, lb = m.step_timeline(layers=True)
+            print("\n[timeline]", ph, lf, lb, flush=True)
+            parts = ("wait", "fwd", "cls", "bwd", "dwait", "tail")
+            assert all(ph[k] >= 0 for k in parts + ("opt", "update")), ph
+            assert sum(ph[k] for k in parts) <= ph["step"] * (1 + 1e-3) + 1e-3
+            assert ph["fwd"] > 0 and ph["bwd"] > 0 and ph["update"] > 0
+            assert (lf > 0).all() and (lb > 0).all()
+            assert lf.sum() <= ph["fwd"] * (1 + 1e-3) + 1e-3 and lb.sum() <= ph["bwd"] * (1 + 1e-3) + 1e-3
+        runs.append(losses)
+        m.close()
+    assert runs[0] == runs[1]
+
+
 def _compact_case(vocab=1024, seed=5):
     cfg = om.tiny(qk_norm=True, rope_theta=1e6, res_alpha=om.train_alpha(2), vocab=vocab)
     rng = np.random.default_rng(seed)
