@@ -24,7 +24,13 @@ import platform
 import sys
 import time
 
-import numpy as np
+# The CPU baseline's BLAS threads, fixed before numpy loads: OMP_NUM_THREADS where the
+# environment sets it (a GPU box's harness fixes a process's CPU share that way), else every
+# core of the host; OpenBLAS follows it.
+os.environ.setdefault("OMP_NUM_THREADS", str(os.cpu_count() or 1))
+os.environ.setdefault("OPENBLAS_NUM_THREADS", os.environ["OMP_NUM_THREADS"])
+
+import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "neural-engine_amd"))
@@ -231,7 +237,7 @@ def cpu_baseline(wname, w, n_runs=5, legs=True):
     Pd = {k: om.round_bf16(v) for k, v in P.items()} if legs and wname.startswith("qwen3") else None
     step_s = _train_leg(w, n_runs, P=P)
     del P
-    threads, blas = os.cpu_count() or 1, "unknown"
+    threads, blas = int(os.environ["OPENBLAS_NUM_THREADS"]), "unknown"
     try:
         from threadpoolctl import threadpool_info
         info = [d for d in threadpool_info() if d.get("user_api") == "blas"]
@@ -240,9 +246,13 @@ def cpu_baseline(wname, w, n_runs=5, legs=True):
     except Exception:
         pass
     out = {"value": w["batch"] * w["seq"] / step_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "host_cpus": os.cpu_count(), "blas_threads": threads,
+           "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
            "sample": f"median of {n_runs} full steps (fwd+bwd+AdamW, after 1 warm-up) of {wname} on the numpy "
-                     f"oracle: {step_s:.2f} s/step; numpy BLAS {blas}, {threads} threads; "
-                     f"host CPU {platform.processor() or platform.machine()}"}
+                     f"oracle: {step_s:.2f} s/step; numpy BLAS {blas} on {threads} threads (OMP_NUM_THREADS and "
+                     f"OPENBLAS_NUM_THREADS = {os.environ.get('OMP_NUM_THREADS')}: the environment's value where it "
+                     f"sets one, as the GPU box's harness does for a process's CPU share, else all "
+                     f"{os.cpu_count()} host CPUs); host CPU {platform.processor() or platform.machine()}"}
     if not legs:
         return out
     res = []
@@ -272,6 +282,18 @@ def cpu_baseline(wname, w, n_runs=5, legs=True):
     return out
 
 
+def roofline_step(w, ms):
+    """The step against its floor on one MI355X: the algorithmic FLOPs of fwd + bwd (3 x forward,
+    causal attention counted once) at the dense 16-bit MFMA peak plus the AdamW pass's algorithmic
+    bytes (30 B per parameter: p, g, m, v read, p, m, v and the 16-bit copy written) at the HBM
+    peak, as if nothing else moved a byte and the two did not overlap."""
+    fl = flops(w)["total"]
+    mfma_ms = fl / PEAK_MFMA_16 * 1e3
+    adam_ms = 30 * n_params(w) / PEAK_HBM * 1e3
+    return {"floor_ms": mfma_ms + adam_ms, "mfma_floor_ms": mfma_ms, "adam_floor_ms": adam_ms,
+            "frac": (mfma_ms + adam_ms) / ms}
+
+
 def train_summary(w, r, ceiling=None):
     """Throughput, per-family kernel time and MFMA utilisation of one run_train result (against
     the datasheet peak and, when given, the measured 32x32x16 issue ceiling in TFLOP/s)."""
@@ -280,6 +302,7 @@ def train_summary(w, r, ceiling=None):
     mm_ms = sum(fam_ms.get(k, 0.0) for k in ("gemm_fwd", "gemm_bwd", "attn_fwd", "attn_bwd", "ce"))
     T = w["batch"] * w["seq"]
     return {"tokens_per_s": T / (r["ms"] / 1e3), "ms_per_step": r["ms"],
+            "roofline_step": roofline_step(w, r["ms"]),
             "kernel_ms_per_step": {k: round(v, 4) for k, v in fam_ms.items()},
             "mfma_util": {"flops_per_step": fl["total"], "gemm_attn_ms_per_step": mm_ms,
                           "achieved_tflops": fl["total"] / (mm_ms / 1e3) / 1e12 if mm_ms else None,
@@ -307,7 +330,7 @@ def _short(name):
 def counters_run(child_args, outdir, timeout_s=900):
     """The per-kernel counter report of one benchmark invocation, for the training step of its
     workload: this process never touches the GPU; it runs the benchmark as child processes under
-    rocprofv3, eager launches, no decode, no CPU leg: a kernel trace with statistics, one pass
+    rocprofv3, eager launches on one stream, no decode, no CPU leg: a kernel trace with statistics, one pass
     each of the FETCH_SIZE and WRITE_SIZE counters (their bytes scaled by three plain 1 GiB
     device copies run first in the same process) and one of MfmaUtil with the fp16/bf16 MFMA
     op count.  Returns the trace run's JSON result with a `counters` object added."""
@@ -315,7 +338,9 @@ def counters_run(child_args, outdir, timeout_s=900):
     import subprocess
     me = [sys.executable, os.path.abspath(__file__)]
     os.makedirs(outdir, exist_ok=True)
-    run = me + child_args + ["--no-graphs", "--no-cpu", "--no-decode", "--no-scale"]
+    # one stream, eager: every kernel runs alone, so a row's duration, counters and rates belong
+    # to that kernel (with the second stream, overlapping kernels stretch each other's durations)
+    run = me + child_args + ["--no-graphs", "--no-overlap", "--no-cpu", "--no-decode", "--no-scale"]
     pmc_run = run + ["--steps", "3", "--warmup", "1"]
 
     def prof(key, what):
@@ -386,6 +411,10 @@ def counters_collect(outdir, result, commands):
             if "SQ_INSTS_VALU_MFMA_MOPS_F16" in mfma[k]:
                 v, n = mfma[k]["SQ_INSTS_VALU_MFMA_MOPS_F16"]
                 row["mfma_tflops"] = v / n * 512 / (avg_us[k] * 1e-6) / 1e12
+        if "read_MB_per_launch" in row and "write_MB_per_launch" in row:
+            gbs = (row["read_MB_per_launch"] + row["write_MB_per_launch"]) * 1e6 / (d["avg_us"] * 1e-6) / 1e9
+            row["hbm_GBps"] = gbs
+            row["hbm_frac"] = gbs * 1e9 / PEAK_HBM
         rows.append(row)
     result["counters"] = {"kernels": rows[:40],
                           "calibration": {"fetch_bytes_per_unit": fs, "write_bytes_per_unit": wsc,
@@ -409,21 +438,24 @@ def counters_markdown(res, made_by):
     cal = c["calibration"]
     out = [f"# rocprofv3 per-kernel report: training step of {res['config']['workload']}", "",
            f"Made by `{made_by}` (one run: its child processes below).", "",
-           f"Traced run (eager launches, kernels serialised by the tracer where counters are read): "
-           f"{res['ms_per_step']:.3f} ms per step.", "",
+           f"Traced run (eager launches on one stream: each kernel runs alone, so its duration, counters and "
+           f"rates are its own): {res['ms_per_step']:.3f} ms per step.", "",
            "Commands of the child processes:", ""]
     out += [f"    {v}" for v in c["commands"].values()]
     out += ["", "Durations from the kernel trace; HBM bytes per launch from FETCH_SIZE and WRITE_SIZE scaled by "
             f"{cal['fetch_bytes_per_unit']:.0f} and {cal['write_bytes_per_unit']:.0f} bytes per counter unit (the "
             "factors that make three 1 GiB device copies read and write 1 GiB each); MfmaUtil as rocprofv3 derives "
-            "it; MFMA TFLOP/s = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 / average duration.", "",
-            "| kernel | calls | avg µs | total ms | % | read MB | write MB | MfmaUtil % | MFMA TFLOP/s |",
-            "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+            "it; MFMA TFLOP/s = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 / average duration; HBM GB/s = (read + write) / "
+            "average duration, and its fraction of the 8 TB/s peak.", "",
+            "| kernel | calls | avg µs | total ms | % | read MB | write MB | HBM GB/s | of peak | MfmaUtil % | "
+            "MFMA TFLOP/s |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
 
     def f(d, k, fmt):
         return format(d[k], fmt) if k in d else "–"
     out += [f"| `{d['kernel']}` | {d['calls']} | {d['avg_us']:.2f} | {d['total_ms']:.2f} | {d['pct']:.2f} | "
             f"{f(d, 'read_MB_per_launch', '.2f')} | {f(d, 'write_MB_per_launch', '.2f')} | "
+            f"{f(d, 'hbm_GBps', '.0f')} | {f(d, 'hbm_frac', '.2f')} | "
             f"{f(d, 'mfma_util_pct', '.1f')} | {f(d, 'mfma_tflops', '.0f')} |" for d in c["kernels"]]
     r = res["roofline"]
     out += ["", f"Roofline kernel `{r['kernel'].split(' ')[0]}`: {r['achieved']:.0f} GB/s of {r['peak']:.0f} "
@@ -490,15 +522,20 @@ def main():
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
-    # one AdamW pass per step: 1 + L launches (embedding + gains, then one per layer) on the
-    # second stream, each between its own event pair; the pass time is the sum of their durations
-    adam_launches = max(r["adam"][1], 1) / a.steps
-    adam_ms = r["adam"][0] / a.steps
+    # One AdamW pass per step, run by the next step beside its forward in L + 2 launches on the
+    # second stream (the gains, one per layer, the embedding; capped at 384 work-groups each),
+    # between one event pair (a pair per launch cost the step 0.22 ms); the last pass of the
+    # timed steps runs after them in one launch.  Pass time: the pair's span, gaps included.
+    passes = max(r["adam"][1], 1)
+    adam_launches = 1 if a.no_overlap else w["n_layers"] + 2   # one stream: the pass in one launch
+    adam_ms = r["adam"][0] / passes
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
     roofline = {"bound": "hbm",
-                "kernel": "adam_kernel (fused AdamW; one pass over all parameters per step, in "
-                          f"{adam_launches:.0f} launches: embedding + gains, then one per layer, the layer "
-                          "launches capped at 384 work-groups while they run beside the next forward)",
+                "kernel": ("adam_kernel (fused AdamW; one pass over all parameters per step, in one launch after "
+                           "the step on one stream)" if a.no_overlap else
+                           "adam_kernel (fused AdamW; one pass over all parameters per step, run beside the next "
+                           f"step's forward in {adam_launches} launches: the gains, one per layer, the embedding, "
+                           "each capped at 384 work-groups; timed by one event pair around the pass)"),
                 "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                 "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
                 "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
@@ -533,6 +570,7 @@ def main():
         "grad_scale": r["scale"], "skipped_steps": r["skipped"], "overflow_sites": r["sites"],
         "loss_last": r["loss"],
     }
+    out["roofline_step"] = summ["roofline_step"]
     if not a.no_scale and a.workload == "qwen3-0.6b-s256-b1":
         ws = WORKLOADS["qwen3-0.6b-s2048-b8"]
         rs = run_train(ws, 3, 1, graphs=not a.no_graphs, overlap=not a.no_overlap)
