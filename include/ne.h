@@ -311,6 +311,15 @@ int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_t *targets,
 /* Backward: dlogits 16-bit [T,V] = (softmax - onehot) * scale, recomputing the logits. */
 int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_t *targets,
                 const float *lse, int T, int D, int V, float scale, void *dlogits, void *stream);
+/* Forward and backward in one call, as the reference's cross_entropy_loss computes the loss
+ * and dlogits together (TD/cpu_ops.h:348-382): ne_k_ce_fwd's outputs, and dlogits as
+ * ne_k_ce_bwd defines it, without a second logits GEMM: the GEMM's epilogue stores each
+ * logit as the 16-bit exp(logit - its 256-column tile's max) into dlogits, which one
+ * streaming pass turns into (softmax - onehot) * scale once the rows' log-sum-exp is known
+ * (the target's probability from its fp32 logit).  dlogits: 16-byte aligned [T, V]. */
+int ne_k_ce_fwd_grad(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D,
+                     int V, float *part, float *tgt_logit, float *lse, float *loss_rows,
+                     float *loss, float scale, void *dlogits, void *stream);
 /* In-place AdamW over n fp32 elements; elements [0, n_decay) get weight decay.  The grad is
  * multiplied by *gscale (device scalar).  pb (may be NULL) receives the 16-bit weights; the
  * grad is zeroed when zero_grad.  TD/cpu_ops.h:266-303. */

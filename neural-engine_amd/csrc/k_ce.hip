@@ -67,7 +67,54 @@ __global__ void scatter_add_rows_kernel(float *__restrict__ G, const float *__re
   }
 }
 
+// The cross-entropy gradient in place over e = exp(logit - tile max), the 16-bit values the
+// LM-head GEMM's forward epilogue stored: dl = (softmax - onehot) * scale with softmax =
+// e * exp(tile max - lse) (TD/cpu_ops.h:373-378: p - 1 at the target, times the loss
+// scale); at the target the probability is formed from its fp32 logit, exp(tgt - lse), as
+// the loss is; padding columns (>= n_valid) are 0.  Eight consecutive columns per thread,
+// which never straddle a tile (tile widths are multiples of 64).
+template <typename HT>
+__global__ __launch_bounds__(256) void ce_grad_kernel(h16_t *__restrict__ dl, int V, int n_valid,
+                                                      const float *__restrict__ part, int n_tiles, int main_cols,
+                                                      int w_main, int w_rest, const float *__restrict__ lse,
+                                                      const float *__restrict__ tgt_logit,
+                                                      const int32_t *__restrict__ targets, float scale,
+                                                      int *__restrict__ ovf) {
+  const long row = blockIdx.y;
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c0 >= V) return;
+  const int slot = c0 < main_cols ? c0 / w_main : main_cols / w_main + (c0 - main_cols) / w_rest;
+  const float l = lse[row];
+  const float f = __expf(part[(row * n_tiles + slot) * 2] - l) * scale;
+  const int tc = targets[row] - c0;
+  u16x8 *p8 = (u16x8 *)(dl + row * V + c0);
+  const u16x8 ev = *p8;
+  u16x8 o;
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    float v = c0 + k < n_valid ? HT::f(ev[k]) * f : 0.f;
+    if (k == tc) v = (__expf(tgt_logit[row] - l) - 1.f) * scale;
+    o[k] = HT::h(v);
+    bad |= HT::bad(o[k]);
+  }
+  *p8 = o;
+  flag_overflow(ovf, bad);
+}
+
 }  // namespace
+
+int launch_ce_grad(int dt, h16_t *dl, int T, int V, int n_valid, const float *part, int n_tiles, int main_cols,
+                   int w_main, int w_rest, const float *lse, const float *tgt_logit, const int32_t *targets,
+                   float scale, int *ovf, hipStream_t s) {
+  if (V % 64 || (((uintptr_t)dl) & 15)) return ne_fail(NE_ERR_ARG, "ce_grad: V %% 64 and 16-byte aligned rows");
+  const dim3 grid((V / 8 + 255) / 256, T);
+  return DISPATCH_H16(dt, [&] {
+    hipLaunchKernelGGL(ce_grad_kernel<HT>, grid, dim3(256), 0, s, dl, V, n_valid, part, n_tiles, main_cols, w_main,
+                       w_rest, lse, tgt_logit, targets, scale, ovf);
+    return ne_hip_status(hipGetLastError(), "ce_grad");
+  }());
+}
 
 int launch_gather_rows16(const h16_t *src, const int32_t *ids, h16_t *dst, int n, int D, hipStream_t s) {
   if (D % 8) return ne_fail(NE_ERR_ARG, "gather_rows16: D=%d must be a multiple of 8", D);

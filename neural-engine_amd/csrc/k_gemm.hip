@@ -303,8 +303,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
   // ---- epilogue: lane owns column (lane & 31) and rows 8*(e/4) + 4*(lane/32) + e%4 ----
   const float alpha = g.alpha;
   if constexpr (EPI == EPI_CE_FWD) {
-    // Per row of this N-tile: max and sum of exp over the tile's columns, plus the
-    // target logit when the target column falls in the tile.
+    // Per row of this N-tile: the max over the tile's columns and the sum of exp relative to
+    // it, plus the target logit when the target column falls in the tile.  With C, each
+    // logit v is also stored as the 16-bit e = exp(v - tile max) in [0, 1], from which the
+    // gradient pass (launch_ce_grad) forms softmax - onehot once the row's log-sum-exp is
+    // known, instead of a second logits GEMM.  Padding columns (>= n_valid) take no part
+    // (e = 0).
     __shared__ float red_m[WN][BM], red_s[WN][BM];
 #pragma unroll
     for (int i = 0; i < FM; i++) {
@@ -317,7 +321,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
 #pragma unroll
         for (int j = 0; j < FN; j++) {
           const int col = g.col0 + n0 + wn * TN + j * 32 + (lane & 31);  // of the full vocabulary
-          // padding columns (>= n_valid) take no part in the softmax
           const float v = col < g.n_valid ? acc[i][j][e] * alpha : -INFINITY;
           mx = fmaxf(mx, v);
           if (col == tgt) g.tgt_logit[row] = v;
@@ -325,31 +328,42 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
         // reduce over the 32 lanes sharing this row (lanes with equal lane>>5)
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if ((lane & 31) == 0) red_m[wn][rl] = mx;
+      }
+    }
+    __syncthreads();
+    h16_t *ce = (h16_t *)g.C;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int rl = wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        float mx = red_m[0][rl];
+#pragma unroll
+        for (int w = 1; w < WN; w++) mx = fmaxf(mx, red_m[w][rl]);
         // a row with no valid column in this tile has mx = -inf and sum 0
         const float mxs = mx > -INFINITY ? mx : 0.f;
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-          const int col = g.col0 + n0 + wn * TN + j * 32 + (lane & 31);
-          s += col < g.n_valid ? __expf(acc[i][j][e] * alpha - mxs) : 0.f;
+          const int cl = n0 + wn * TN + j * 32 + (lane & 31);  // of this launch
+          const float ev = g.col0 + cl < g.n_valid ? __expf(acc[i][j][e] * alpha - mxs) : 0.f;
+          s += ev;
+          if (ce) ce[(long)(m0 + rl) * g.ldc + cl] = HT::h(ev);
         }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-        if ((lane & 31) == 0) {
-          red_m[wn][rl] = mx;
-          red_s[wn][rl] = s;
-        }
+        if ((lane & 31) == 0) red_s[wn][rl] = s;
       }
     }
     __syncthreads();
     for (int r = tid; r < BM; r += NTHREADS) {
-      float mx = red_m[0][r];
+      float mx = red_m[0][r], s = red_s[0][r];
 #pragma unroll
-      for (int w = 1; w < WN; w++) mx = fmaxf(mx, red_m[w][r]);
-      float s = 0.f;
-#pragma unroll
-      for (int w = 0; w < WN; w++)
-        if (red_m[w][r] > -INFINITY) s += red_s[w][r] * __expf(red_m[w][r] - mx);
+      for (int w = 1; w < WN; w++) {
+        mx = fmaxf(mx, red_m[w][r]);
+        s += red_s[w][r];
+      }
       float *p = g.part + ((long)(m0 + r) * g.n_tiles + g.tile0 + nt) * 2;
       p[0] = mx;
       p[1] = s;
@@ -741,6 +755,13 @@ int gemm_ce_tiles(int M, int N, int K) {
   return nm / 256 + (N - nm) / tile_bn(gemm_tile(M, N - nm, K));
 }
 
+void gemm_ce_layout(int M, int N, int K, int *main_cols, int *w_main, int *w_rest) {
+  const int nm = ragged_main(M, N, K);
+  *main_cols = nm ? nm : N;
+  *w_main = nm ? 256 : tile_bn(gemm_tile(M, N, K));
+  *w_rest = nm ? tile_bn(gemm_tile(M, N - nm, K)) : *w_main;
+}
+
 bool gemm_group_fits(const GemmArgs *g, int n) {
   if (n < 1 || n > GEMM_GROUP_MAX) return false;
   long tiles = 0;
@@ -841,7 +862,7 @@ int gemm_launch(int dt, int layout, int epi, GemmArgs g, hipStream_t s, int *spl
     return ne_fail(NE_ERR_ARG, "gemm: the SwiGLU forward needs h13 [M,N] and gate [M,N/2] outputs, N %% 128 == 0");
   // ragged shapes: the main part of whole 256-wide tiles, then the rest (see ragged_main)
   if (epi != EPI_SWIGLU_BWD && epi != EPI_SWIGLU_FWD && !g.defer_reduce) {
-    const size_t ce = epi == EPI_H16 || epi == EPI_CE_BWD ? 2 : 4;  // C element size
+    const size_t ce = epi == EPI_H16 || epi == EPI_CE_BWD || epi == EPI_CE_FWD ? 2 : 4;  // C element size
     if (const int nm = ragged_main(g.M, g.N, g.K)) {  // split the columns
       GemmArgs a = g, b = g;
       a.N = nm;

@@ -202,6 +202,27 @@ int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, co
   return gemm_launch(dt, GEMM_NT, EPI_CE_BWD, g, s);
 }
 
+int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, int n_valid,
+                    float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale,
+                    void *dlogits, int *ovf, hipStream_t s) {
+  if (n_valid <= 0 || n_valid > V) return ne_fail(NE_ERR_ARG, "ce: %d valid columns of %d", n_valid, V);
+  if (!dlogits || ((uintptr_t)dlogits & 15)) return ne_fail(NE_ERR_ARG, "ce: dlogits must be 16-byte aligned");
+  GemmArgs g = {};
+  g.M = T; g.N = V; g.K = D;
+  g.A = x; g.lda = D; g.B = E; g.ldb = D;
+  g.C = dlogits; g.ldc = V;
+  g.alpha = 1.f;
+  g.targets = targets; g.part = part; g.tgt_logit = tgt_logit;
+  g.n_valid = n_valid;
+  NE_CHECK(gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s));
+  const int n_tiles = gemm_ce_tiles(T, V, D);
+  NE_CHECK(launch_ce_reduce(part, n_tiles, tgt_logit, lse, loss_rows, loss, T, s));
+  int mc, wm, wr;
+  gemm_ce_layout(T, V, D, &mc, &wm, &wr);
+  return launch_ce_grad(dt, (h16_t *)dlogits, T, V, n_valid, part, n_tiles, mc, wm, wr, lse, tgt_logit, targets,
+                        scale, ovf, s);
+}
+
 extern "C" int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
                            float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                            void *stream) {
@@ -213,6 +234,14 @@ extern "C" int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_
                            int T, int D, int V, float scale, void *dlogits, void *stream) {
   CHECK_DT(dtype);
   return ce_backward(dtype, x, E, targets, lse, T, D, V, V, scale, dlogits, nullptr, S(stream));
+}
+
+extern "C" int ne_k_ce_fwd_grad(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D,
+                                int V, float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+                                float scale, void *dlogits, void *stream) {
+  CHECK_DT(dtype);
+  return ce_forward_grad(dtype, x, E, targets, T, D, V, V, part, tgt_logit, lse, loss_rows, loss, scale, dlogits,
+                         nullptr, S(stream));
 }
 
 extern "C" int ne_k_adam(int dtype, float *p, float *g, float *m, float *v, void *pb, int64_t n,

@@ -852,10 +852,8 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
   {
     ProfScope ps(c, NE_PROF_CE);
     if (compact) NE_CHECK(launch_gather_rows16(Pb + c->off_E, c->cids, c->cE, c->cvp, D, c->st));
-    NE_CHECK(ce_forward(dt, c->xf, Ecls, c->tok_tgt, T, D, Vc, Vvalid, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows,
-                        c->loss, c->st));
-    NE_CHECK(ce_backward(dt, c->xf, Ecls, c->tok_tgt, c->ce_lse, T, D, Vc, Vvalid, c->gs, c->dlogits,
-                         ovf + OVF_DLOGITS, c->st));
+    NE_CHECK(ce_forward_grad(dt, c->xf, Ecls, c->tok_tgt, T, D, Vc, Vvalid, c->ce_part, c->ce_tgt, c->ce_lse,
+                             c->ce_rows, c->loss, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
   }
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------

@@ -97,6 +97,10 @@ struct SplitIn {
 // split, C is not written and the partials stay in a.ws (M*N floats per split).
 int gemm_launch(int dt, int layout, int epi, GemmArgs a, hipStream_t s, int *split_out = nullptr);
 int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per row it writes
+// EPI_CE_FWD's column tiling: columns [0, main_cols) in tiles of w_main, the rest in tiles of
+// w_rest; partial slot of column c: c < main_cols ? c / w_main : main_cols / w_main +
+// (c - main_cols) / w_rest.
+void gemm_ce_layout(int M, int N, int K, int *main_cols, int *w_main, int *w_rest);
 // K splits gemm_launch would use for this shape with a workspace of ws_elems floats (1: none).
 int gemm_splits(int epi, int M, int N, int K, long ws_elems);
 // Sum-of-squares slots (GemmArgs::sq) gemm_launch writes for this shape (EPI_F32 /
@@ -198,6 +202,15 @@ int ce_forward(int dt, const void *x, const void *E, const int32_t *targets, int
                hipStream_t s);
 int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, const float *lse,
                 int T, int D, int V, int n_valid, float scale, void *dlogits, int *ovf, hipStream_t s);
+// The forward with its gradient: the logits GEMM also stores e = exp(logit - tile max) in
+// dlogits (16-bit [T, V]), and after the row reduction one streaming pass turns it in place
+// into (softmax - onehot) * scale (no second logits GEMM).  ovf: the gradient's overflow flag.
+int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
+                    int n_valid, float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
+                    float scale, void *dlogits, int *ovf, hipStream_t s);
+int launch_ce_grad(int dt, h16_t *dl, int T, int V, int n_valid, const float *part, int n_tiles, int main_cols,
+                   int w_main, int w_rest, const float *lse, const float *tgt_logit, const int32_t *targets,
+                   float scale, int *ovf, hipStream_t s);
 // Vocabulary compaction: dst[r] = src[ids[r]] (16-bit rows of D); G[ids[r]] += src[r] for
 // r < n (fp32 rows of D; the ids are distinct).
 int launch_gather_rows16(const h16_t *src, const int32_t *ids, h16_t *dst, int n, int D, hipStream_t s);

@@ -33,7 +33,7 @@ EXPORTS = (
     "ne_decode", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_timeline", "ne_step_timeline", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_gemm_wgrad_group", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
-    "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
+    "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_ce_fwd_grad", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
     "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
 )
 
@@ -137,6 +137,7 @@ def lib():
         "ne_k_attn_bwd_noalloc": (I, [I, P, L, P, L, P, L, P, L, P, P, L, P, L, P, L, P, L, I, I, I, I, I, F, P]),
         "ne_k_ce_fwd": (I, [I, P, P, P, I, I, I, P, P, P, P, P, P]),
         "ne_k_ce_bwd": (I, [I, P, P, P, P, I, I, I, F, P, P]),
+        "ne_k_ce_fwd_grad": (I, [I, P, P, P, I, I, I, P, P, P, P, P, F, P, P]),
         "ne_k_adam": (I, [I, P, P, P, P, P, L, L, F, F, F, F, F, I, P, I, P]),
         "ne_k_grad_norm": (I, [P, L, F, F, P, P, P, P]),
         "ne_k_embed_fwd": (I, [P, P, P, I, I, P]),

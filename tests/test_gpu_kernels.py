@@ -448,6 +448,53 @@ def test_fused_ce_fwd_bwd(fmt, T, D, V):
     assert np.abs(got[T]).max() == 0
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,D,V,estd", [(64, 128, 512, 0.05), (256, 768, 32000, 0.05), (2048, 1024, 32896, 0.05),
+                                        (256, 128, 65664, 0.05), (256, 1024, 4096, 0.5)])
+def test_fused_ce_fwd_grad(fmt, T, D, V, estd):
+    """The forward with its gradient in one call (ne_k_ce_fwd_grad): loss and log-sum-exp as
+    ne_k_ce_fwd's, and dlogits against float64 within two roundings of the format (the stored
+    exp(logit - tile max), then the gradient), whichever tiling the vocabulary takes (ragged
+    256.5 and 128.5 tiles as in test_fused_ce_fwd_bwd).  estd 0.5 makes logits of std ~16, a
+    peaked softmax like a trained model's, where the target's gradient p - 1 is small.  The
+    guard row after dlogits stays zero."""
+    dt, tdt, rnd, u = FMT[fmt]
+    rng = np.random.default_rng(V + 1)
+    x = rnd(rng.standard_normal((T, D)).astype(np.float32))
+    E = rnd(rng.standard_normal((V, D)).astype(np.float32) * estd)
+    tgt = rng.integers(0, V, T).astype(np.int32)
+    logits = x.astype(np.float64) @ E.T.astype(np.float64)
+    if estd > 0.1:  # targets at each row's most likely token: p_tgt near 1
+        tgt = logits.argmax(1).astype(np.int32)
+    xd, Ed, td = dev(x, tdt), dev(E, tdt), dev(tgt)
+    part = zeros((T * (V // 64) * 2,))
+    tl, lse, rows, loss = zeros((T,)), zeros((T,)), zeros((T,)), zeros((4,))
+    dlg = zeros((T + 1, V), tdt)  # + a guard row
+    scale = 1024.0
+    call(L.ne_k_ce_fwd_grad, dt, ptr(xd), ptr(Ed), ptr(td), T, D, V, ptr(part), ptr(tl), ptr(lse), ptr(rows),
+         ptr(loss), scale, ptr(dlg), None)
+    m = logits.max(1, keepdims=True)
+    lse_r = (m + np.log(np.exp(logits - m).sum(1, keepdims=True)))[:, 0]
+    p_t = np.exp(logits[np.arange(T), tgt] - lse_r)
+    loss_r = np.mean(-np.log(p_t + 1e-10))
+    np.testing.assert_allclose(host(lse), lse_r, rtol=1e-5)
+    assert abs(host(loss)[0] - loss_r) < 1e-4 * abs(loss_r) + 1e-6
+    ref = np.exp(logits - lse_r[:, None])
+    ref[np.arange(T), tgt] -= 1
+    ref *= scale
+    got = host(dlg)
+    err = rel_l2(got[:T], ref)
+    print(f"\n  {fmt} T={T} V={V} estd={estd}: dlogits rel-L2 {err:.2e} (u {u:.1e})", flush=True)
+    assert err < 2 * u
+    assert np.abs(got[T]).max() == 0
+    # the loss outputs equal the forward alone
+    lse2, loss2 = zeros((T,)), zeros((4,))
+    call(L.ne_k_ce_fwd, dt, ptr(xd), ptr(Ed), ptr(td), T, D, V, ptr(part), ptr(tl), ptr(lse2), ptr(rows),
+         ptr(loss2), None)
+    np.testing.assert_array_equal(host(lse2), host(lse))
+    assert host(loss2)[0] == host(loss)[0]
+
+
 # ------------------------------------------------------------------------ optimizer
 
 @pytest.mark.parametrize("fmt", FMTS)
