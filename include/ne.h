@@ -195,6 +195,17 @@ int ne_set_vocab_map(ne_ctx *ctx, const int32_t *ids, int cv);
  * B <= decode_batch and P + n_new <= decode_ctx. */
 int ne_decode(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temperature,
               float top_p, const double *uniforms, int32_t *out_tokens);
+/* ne_decode with the sampling draws taken from a seed, as generate.py's --seed makes them
+ * (np.random.seed(seed), then one np.random.choice per sampled token: generate.py:198-215,
+ * 248-249): MT19937 seeded by the 32-bit integer seed (seed >= 2^32 is rejected, as numpy
+ * rejects it), each draw the 53-bit double numpy's RandomState.random_sample returns.  With
+ * B > 1 the draws go position by position, the sequences of a position in order.
+ * temperature < 1e-6 is greedy and draws nothing. */
+int ne_decode_seeded(ne_ctx *ctx, const int32_t *prompt, int B, int P, int n_new, float temperature,
+                     float top_p, uint64_t seed, int32_t *out_tokens);
+/* The first n draws of that generator: out[k] = RandomState(seed).random_sample() in order.
+ * Host only (no device work). */
+int ne_mt19937_uniforms(uint64_t seed, int64_t n, double *out);
 
 /* ------------------------------------------------------------- profiling ---- */
 

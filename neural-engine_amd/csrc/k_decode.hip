@@ -1304,6 +1304,9 @@ int decode_run(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float 
   if (!greedy && !uniforms) return ne_fail(NE_ERR_ARG, "decode: sampling needs uniforms");
   for (long i = 0; i < (long)B * P; i++)
     if (prompt[i] < 0 || prompt[i] >= c->V) return ne_fail(NE_ERR_ARG, "decode: prompt id out of range");
+  // Every call runs its prompt from position 0 and rebuilds the KV cache, so the cache layout
+  // may follow this call's batch size (K column-major at B <= 4, row-major above,
+  // dec_attn_kernel); a cache kept across calls would have to keep one layout for both.
   // per-call inputs: prompt rows, uniforms, state (outside the captured graphs)
   std::vector<int32_t> pr((size_t)d->Bp * d->ctx, 0);
   for (int b = 0; b < B; b++)

@@ -127,27 +127,35 @@ __global__ void fill_f32_kernel(float *__restrict__ dst, float v, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) dst[i] = v;
 }
 
+// A block that meets a NaN writes NaN for both (fminf / fmaxf alone would skip it and report
+// a finite range for a diverged run).
 __global__ __launch_bounds__(256) void minmax_kernel(const float *__restrict__ a, long n, float *__restrict__ out) {
   __shared__ float rmn[4], rmx[4];
+  __shared__ int rnan[4];
   float mn = INFINITY, mx = -INFINITY;
+  int nan = 0;
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
     const float v = a[i];
     mn = fminf(mn, v);
     mx = fmaxf(mx, v);
+    nan |= v != v;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     mn = fminf(mn, __shfl_xor(mn, o, 64));
     mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    nan |= __shfl_xor(nan, o, 64);
   }
   if ((threadIdx.x & 63) == 0) {
     rmn[threadIdx.x >> 6] = mn;
     rmx[threadIdx.x >> 6] = mx;
+    rnan[threadIdx.x >> 6] = nan;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    out[2 * blockIdx.x] = fminf(fminf(rmn[0], rmn[1]), fminf(rmn[2], rmn[3]));
-    out[2 * blockIdx.x + 1] = fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
+    const bool any = rnan[0] | rnan[1] | rnan[2] | rnan[3];
+    out[2 * blockIdx.x] = any ? NAN : fminf(fminf(rmn[0], rmn[1]), fminf(rmn[2], rmn[3]));
+    out[2 * blockIdx.x + 1] = any ? NAN : fmaxf(fmaxf(rmx[0], rmx[1]), fmaxf(rmx[2], rmx[3]));
   }
 }
 

@@ -1248,11 +1248,17 @@ extern "C" int ne_step_stats(ne_ctx *c, float *out) {
   std::vector<float> h(4 * NE_STATS_BLOCKS);
   NE_HIP(hipMemcpyAsync(h.data(), c->stats_part, h.size() * sizeof(float), hipMemcpyDeviceToHost, c->st));
   NE_HIP(hipStreamSynchronize(c->st));
+  // a NaN anywhere (a block's NaN partials) makes both ends of that range NaN
   float v[4] = {INFINITY, -INFINITY, INFINITY, -INFINITY};
   for (int k = 0; k < 2; k++)
     for (int b = 0; b < NE_STATS_BLOCKS; b++) {
-      v[2 * k] = fminf(v[2 * k], h[(size_t)(k * NE_STATS_BLOCKS + b) * 2]);
-      v[2 * k + 1] = fmaxf(v[2 * k + 1], h[(size_t)(k * NE_STATS_BLOCKS + b) * 2 + 1]);
+      const float lo = h[(size_t)(k * NE_STATS_BLOCKS + b) * 2], hi = h[(size_t)(k * NE_STATS_BLOCKS + b) * 2 + 1];
+      if (lo != lo || hi != hi || v[2 * k] != v[2 * k]) {
+        v[2 * k] = v[2 * k + 1] = NAN;
+        continue;
+      }
+      v[2 * k] = fminf(v[2 * k], lo);
+      v[2 * k + 1] = fmaxf(v[2 * k + 1], hi);
     }
   // dx holds the gradient at the internal scale; u > 0 maps it to the reference's scale
   out[0] = v[0];
@@ -1445,6 +1451,65 @@ extern "C" int ne_save_ckpt_v4(ne_ctx *c, const char *path, const ne_train_state
   if (!rc) rc = io_body(c, f, false, c->c.qk_norm != 0);
   if (fclose(f) != 0 && !rc) rc = ne_fail(NE_ERR_IO, "%s: close failed", path);
   return rc;
+}
+
+namespace {
+
+// MT19937 (Matsumoto & Nishimura 1998, "Mersenne Twister: a 623-dimensionally equidistributed
+// uniform pseudo-random number generator"): 624-word state, initialised from a 32-bit seed by
+// the published recurrence x[i] = 1812433253 * (x[i-1] ^ (x[i-1] >> 30)) + i, and the 53-bit
+// double of two draws, (a >> 5) * 2^26 + (b >> 6) over 2^53 -- what numpy's legacy
+// RandomState(seed).random_sample() returns for an integer seed, and so the draw of
+// np.random.choice in TD/tools/generate.py:215 after np.random.seed(seed) (generate.py:248-249).
+struct MT19937 {
+  uint32_t x[624];
+  int i = 624;
+  explicit MT19937(uint32_t seed) {
+    x[0] = seed;
+    for (int k = 1; k < 624; k++) x[k] = 1812433253u * (x[k - 1] ^ (x[k - 1] >> 30)) + (uint32_t)k;
+  }
+  uint32_t next() {
+    if (i >= 624) {
+      for (int k = 0; k < 624; k++) {
+        const uint32_t y = (x[k] & 0x80000000u) | (x[(k + 1) % 624] & 0x7fffffffu);
+        x[k] = x[(k + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+      }
+      i = 0;
+    }
+    uint32_t y = x[i++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+  }
+  double uniform() {
+    const uint32_t a = next() >> 5, b = next() >> 6;
+    return (a * 67108864.0 + b) / 9007199254740992.0;
+  }
+};
+
+}  // namespace
+
+extern "C" int ne_mt19937_uniforms(uint64_t seed, int64_t n, double *out) {
+  if (!out || n < 0) return ne_fail(NE_ERR_ARG, "mt19937: null output or negative count");
+  if (seed > 0xffffffffull) return ne_fail(NE_ERR_ARG, "mt19937: seed must be in [0, 2^32)");
+  MT19937 mt((uint32_t)seed);
+  for (int64_t k = 0; k < n; k++) out[k] = mt.uniform();
+  return 0;
+}
+
+extern "C" int ne_decode_seeded(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float temperature,
+                                float top_p, uint64_t seed, int32_t *out_tokens) {
+  if (!c || !prompt || !out_tokens) return ne_fail(NE_ERR_ARG, "null argument");
+  if (B <= 0 || n_new <= 0) return ne_fail(NE_ERR_ARG, "decode: B=%d n_new=%d", B, n_new);
+  if (temperature < 1e-6f) return ne_decode(c, prompt, B, P, n_new, temperature, top_p, nullptr, out_tokens);
+  // one draw per sampled token, position by position, the sequences of a position in order
+  std::vector<double> s((size_t)B * n_new), u((size_t)B * n_new);
+  NE_CHECK(ne_mt19937_uniforms(seed, (int64_t)s.size(), s.data()));
+  for (int j = 0; j < n_new; j++)
+    for (int b = 0; b < B; b++) u[(size_t)b * n_new + j] = s[(size_t)j * B + b];
+  return ne_decode(c, prompt, B, P, n_new, temperature, top_p, u.data(), out_tokens);
 }
 
 extern "C" int ne_decode(ne_ctx *c, const int32_t *prompt, int B, int P, int n_new, float temperature, float top_p,

@@ -30,7 +30,7 @@ EXPORTS = (
     "ne_set_tensor", "ne_get_tensor", "ne_train_step", "ne_use_graphs", "ne_overlap_weight_grads", "ne_optimizer_step",
     "ne_rmsnorm_bwd_formula", "ne_zero_grads",
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
-    "ne_decode", "ne_set_vocab_map",
+    "ne_decode", "ne_decode_seeded", "ne_mt19937_uniforms", "ne_set_vocab_map",
     "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_timeline", "ne_step_timeline", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_gemm_wgrad_group", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_ce_fwd_grad", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
@@ -120,6 +120,8 @@ def lib():
         "ne_load_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
         "ne_save_ckpt_v4": (I, [P, C.c_char_p, C.POINTER(TrainState)]),
         "ne_decode": (I, [P, P, I, I, I, F, F, P, P]),
+        "ne_decode_seeded": (I, [P, P, I, I, I, F, F, C.c_uint64, P]),
+        "ne_mt19937_uniforms": (I, [C.c_uint64, L, P]),
         "ne_set_vocab_map": (I, [P, P, I]),
         "ne_prof_enable": (I, [P, I]),
         "ne_prof_reset": (I, [P]),
@@ -157,6 +159,13 @@ def check(rc: int, what: str = ""):
     if rc != 0:
         msg = lib().ne_last_error().decode(errors="replace")
         raise NEError(f"{what} failed ({rc}): {msg}")
+
+
+def mt19937_uniforms(seed: int, n: int) -> np.ndarray:
+    """ne_mt19937_uniforms: the draws numpy's RandomState(seed).random_sample(n) gives."""
+    out = np.zeros(n, np.float64)
+    check(lib().ne_mt19937_uniforms(seed, n, _ptr(out)), "mt19937_uniforms")
+    return out
 
 
 def tensor_names(n_layers: int, qk_norm: bool):
@@ -315,6 +324,15 @@ class Model:
             u = np.ascontiguousarray(uniforms, np.float64).reshape(B, n_new)
         check(lib().ne_decode(self._h, _ptr(p), B, P0, n_new, temperature, top_p,
                               _ptr(u) if u is not None else None, _ptr(out)), "decode")
+        return out
+
+    def decode_seeded(self, prompt: np.ndarray, n_new: int, temperature: float, top_p: float, seed: int):
+        """ne_decode_seeded: sampling draws from MT19937(seed), as generate.py --seed."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        B, P0 = p.shape
+        out = np.zeros((B, n_new), np.int32)
+        check(lib().ne_decode_seeded(self._h, _ptr(p), B, P0, n_new, temperature, top_p, seed, _ptr(out)),
+              "decode_seeded")
         return out
 
     def prof_enable(self, families=PROF_FAMILIES):

@@ -414,12 +414,14 @@ def test_flash_attention_at_scale(fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,D,V", [(64, 128, 512), (256, 768, 32000), (2048, 128, 32768), (256, 128, 65664),
-                                   (2048, 1024, 32896)])
+                                   (2048, 1024, 32896), (64, 192, 512), (64, 320, 512)])
 def test_fused_ce_fwd_bwd(fmt, T, D, V):
     """(256, 128, 65664): a vocabulary 256.5 tiles of 256 wide.  (2048, 1024, 32896): 128.5
     tiles, large enough that the classifier GEMMs run as whole 256-wide tiles plus the last 128
-    columns (partial slots and target columns offset in the second launch).  The guard row
-    after dlogits must stay zero (no store past the last column)."""
+    columns (partial slots and target columns offset in the second launch).  D = 192 and 320
+    on the 64-row tile: 3 and 5 K steps of 64, an odd count, which the cross-entropy epilogues
+    run as one more step over a zeroed A stage (the padded K loop).  The guard row after
+    dlogits must stay zero (no store past the last column)."""
     dt, tdt, rnd, u = FMT[fmt]
     rng = np.random.default_rng(V)
     x = rnd(rng.standard_normal((T, D)).astype(np.float32))
@@ -450,7 +452,7 @@ def test_fused_ce_fwd_bwd(fmt, T, D, V):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,D,V,estd", [(64, 128, 512, 0.05), (256, 768, 32000, 0.05), (2048, 1024, 32896, 0.05),
-                                        (256, 128, 65664, 0.05), (256, 1024, 4096, 0.5)])
+                                        (256, 128, 65664, 0.05), (256, 1024, 4096, 0.5), (64, 320, 512, 0.05)])
 def test_fused_ce_fwd_grad(fmt, T, D, V, estd):
     """The forward with its gradient in one call (ne_k_ce_fwd_grad): loss and log-sum-exp as
     ne_k_ce_fwd's, and dlogits against float64 within two roundings of the format (the stored

@@ -99,3 +99,24 @@ def test_attn_bwd_noalloc_rejects_oversized_inputs_without_device():
     rc = L.ne_k_attn_bwd_noalloc(ne.NE_FP16, None, 0, None, 0, None, 0, None, 0, None, None, 0, None, 0, None, 0,
                                  None, 0, 0, 2048, 16, 8, 128, 1.0, None)
     assert rc == -1 and b"must be positive" in L.ne_last_error()
+
+
+def test_mt19937_uniforms_match_numpy_random_state():
+    """ne_mt19937_uniforms (the draws of ne_decode_seeded) against numpy's legacy
+    RandomState(seed).random_sample, bit for bit, across the 624-word regeneration; seeds of
+    2^32 and above are rejected as numpy rejects them."""
+    import numpy as np
+    for seed in (0, 1, 42, 1234, 2**32 - 1):
+        want = np.random.RandomState(seed).random_sample(1500)
+        got = ne.mt19937_uniforms(seed, 1500)
+        np.testing.assert_array_equal(got, want, err_msg=str(seed))
+    with pytest.raises(ne.NEError):
+        ne.mt19937_uniforms(2**32, 4)
+    # generate.py draws through np.random.choice: one random_sample per call
+    rs = np.random.RandomState(7)
+    p = np.full(10, 0.1)
+    picks = [rs.choice(10, p=p) for _ in range(5)]
+    u = ne.mt19937_uniforms(7, 5)
+    cdf = np.cumsum(p)
+    cdf /= cdf[-1]
+    assert picks == [int(np.searchsorted(cdf, x, side="right")) for x in u]
