@@ -682,13 +682,16 @@ int launch_rmsnorm_fwd(int dt, const float *x, const float *g, h16_t *y, float *
 
 namespace {
 int rms_rows(int T) { return std::max(1, (T + 1023) / 1024); }  // rows per block: <= 1024 blocks
-int qk_tpb(int T) { return T <= 4096 ? 16 : 128; }   // tokens per block
+// Tokens per block of the QK-prep backward: on short steps one per thread group (HD/2 threads a
+// token), so a block runs one pass and there are 4x-8x more blocks (256 tokens: 10.3 us with
+// 16 tokens a block, four passes of dependent loads); 128 on long steps.
+int qk_tpb(int T, int HD) { return T <= 4096 ? 512 / HD : 128; }
 }  // namespace
 
 long rmsnorm_bwd_part_elems(int T, int D) { return (long)((T + rms_rows(T) - 1) / rms_rows(T)) * D; }
 int rmsnorm_bwd_part_rows(int T) { return (T + rms_rows(T) - 1) / rms_rows(T); }
-void qk_prep_bwd_part_rows(int T, int NH, int NKV, int *rows_q, int *rows_k) {
-  const int nbx = (T + qk_tpb(T) - 1) / qk_tpb(T);
+void qk_prep_bwd_part_rows(int T, int NH, int NKV, int HD, int *rows_q, int *rows_k) {
+  const int nbx = (T + qk_tpb(T, HD) - 1) / qk_tpb(T, HD);
   *rows_q = NH * nbx;
   *rows_k = NKV * nbx;
 }
@@ -700,7 +703,7 @@ int launch_colsum_batch(const ColsumJob *jobs_dev, int njobs, int max_n, hipStre
   return ne_hip_status(hipGetLastError(), "colsum_batch");
 }
 long qk_prep_bwd_part_elems(int T, int NH, int NKV, int HD) {
-  return (long)((T + qk_tpb(T) - 1) / qk_tpb(T)) * (NH + NKV) * HD;
+  return (long)((T + qk_tpb(T, HD) - 1) / qk_tpb(T, HD)) * (NH + NKV) * HD;
 }
 
 int launch_rmsnorm_bwd(int dt, const float *dy, const float *x, const float *g, const float *r,
@@ -769,7 +772,7 @@ int launch_qk_prep_bwd(int dt, const float *dq, const float *dk, const h16_t *qk
                        bool defer_colsum, const float *kvpart, int *ovf_v) {
   if (HD != 64 && HD != 128) return ne_fail(NE_ERR_ARG, "qk_prep: head_dim %d not in {64,128}", HD);
   if (kvpart && (ld % 2 || NH % NKV)) return ne_fail(NE_ERR_ARG, "qk_prep: bad layout for the dK/dV partials");
-  const int tpb = qk_tpb(T);
+  const int tpb = qk_tpb(T, HD);
   const int nbx = (T + tpb - 1) / tpb;
   dim3 grid(nbx, NH + NKV + (kvpart ? NKV : 0));
   NE_CHECK(DISPATCH_H16(dt, [&] {

@@ -533,7 +533,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
     }
     if (c->c.qk_norm) {
       int rq, rk;
-      qk_prep_bwd_part_rows(c->T, c->NH, c->NKV, &rq, &rk);
+      qk_prep_bwd_part_rows(c->T, c->NH, c->NKV, c->HD, &rq, &rk);
       for (int l = 0; l < c->L; l++) {
         jobs.push_back({qk_part(c, l), c->G + c->lo[l].gq, rq, c->HD});
         jobs.push_back({qk_part(c, l) + (long)rq * c->HD, c->G + c->lo[l].gk, rk, c->HD});

@@ -148,7 +148,7 @@ struct ColsumJob {
   int rows, n;
 };
 int rmsnorm_bwd_part_rows(int T);                              // partial rows of one rmsnorm_bwd
-void qk_prep_bwd_part_rows(int T, int NH, int NKV, int *rows_q, int *rows_k);
+void qk_prep_bwd_part_rows(int T, int NH, int NKV, int HD, int *rows_q, int *rows_k);
 int launch_colsum_batch(const ColsumJob *jobs_dev, int njobs, int max_n, hipStream_t s);
 // With sp.n > 0 the 16-bit input (h13 / qkv, the GEMM's output) is formed from split-K
 // partials and written before use; ovf_h13 / ovf_qkv take the GEMM's overflow flag.

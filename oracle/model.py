@@ -243,15 +243,31 @@ def vocab_map_build(data: np.ndarray, vocab: int) -> np.ndarray:
     return np.flatnonzero(used).astype(np.int32)
 
 
+# Sites of the device's 16-bit roundings (the operands its GEMMs and attention read in 16 bits),
+# for forward(rnd=...) / backward(rnd=...): rnd(site, array) returns the array as the device
+# holds it there (default: unchanged, the fp32 oracle).  Forward: xn, x2n, xf (RMSNorm outputs),
+# qkv (the QKV GEMM's output), qkr (q, k after QK-norm and RoPE), p_fwd (attention
+# probabilities in P.V), att (attention output), h13, gate, dlogits.  Backward: dbf (alpha * dx
+# into the FFN and attention blocks), dh13, datt (dO), p_bwd (P in dV), ds (dS), dv, dqk (dq,
+# dk after the RoPE / QK-norm backward).
+ROUND_SITES = ("xn", "qkv", "qkr", "p_fwd", "att", "x2n", "h13", "gate", "xf", "dlogits",
+               "dbf", "dh13", "datt", "p_bwd", "ds", "dv", "dqk")
+
+
+def _keep(site, t):
+    return t
+
+
 def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, want_grad_cache=True,
-            vocab_ids: np.ndarray | None = None):
+            vocab_ids: np.ndarray | None = None, rnd=None):
     """Batched forward + CE.  tokens [B, S+1] int: inputs [:, :S], targets [:, 1:].
 
     vocab_ids (optional, from vocab_map_build): the classifier and the softmax run over
     those embedding rows only and the targets are mapped to their compact ids
-    (TD/train.m:401, 497-503).  Returns (loss, cache).  cache carries everything the
-    backward needs.
+    (TD/train.m:401, 497-503).  rnd (optional): see ROUND_SITES.  Returns (loss, cache).
+    cache carries everything the backward needs.
     """
+    R = rnd or _keep
     B, S1 = tokens.shape
     S = S1 - 1
     inp, tgt = tokens[:, :S], tokens[:, 1:]
@@ -268,9 +284,10 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
         p = lambda t: P[f"layers.{l}.{t}"]
         c = {"x_in": x}
         xn, r1 = rmsnorm(x, p("rms_att"), cfg.eps)
-        q = (xn @ p("Wq").T).reshape(B, S, NH, HD)
-        k = (xn @ p("Wk").T).reshape(B, S, NKV, HD)
-        v = (xn @ p("Wv").T).reshape(B, S, NKV, HD)
+        xn = R("xn", xn)
+        q = R("qkv", (xn @ p("Wq").T).reshape(B, S, NH, HD))
+        k = R("qkv", (xn @ p("Wk").T).reshape(B, S, NKV, HD))
+        v = R("qkv", (xn @ p("Wv").T).reshape(B, S, NKV, HD))
         c.update(xn=xn, r1=r1, q_raw=q, k_raw=k, v=v)
         if cfg.qk_norm:
             qn, rq = rmsnorm(q, p("q_norm"), cfg.eps)
@@ -278,8 +295,8 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
             c.update(rq=rq, rk=rk, qn=qn, kn=kn)
         else:
             qn, kn = q, k
-        qr = rope_apply(qn, cos, sin)
-        kr = rope_apply(kn, cos, sin)
+        qr = R("qkr", rope_apply(qn, cos, sin))
+        kr = R("qkr", rope_apply(kn, cos, sin))
         att = np.empty((B, S, NH, HD), F32)
         probs = np.empty((B, NH, S, S), F32)
         for b in range(B):
@@ -288,14 +305,15 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
                 s = (qr[b, :, h, :] @ kr[b, :, kh, :].T) * scale + mask
                 pr = softmax_rows(s)
                 probs[b, h] = pr
-                att[b, :, h, :] = pr @ v[b, :, kh, :]
-        attf = att.reshape(B, S, NH * HD)
+                att[b, :, h, :] = R("p_fwd", pr) @ v[b, :, kh, :]
+        attf = R("att", att.reshape(B, S, NH * HD))
         o = attf @ p("Wo").T
         x2 = (x + a * o).astype(F32)
         x2n, r2 = rmsnorm(x2, p("rms_ffn"), cfg.eps)
-        h1 = x2n @ p("W1").T
-        h3 = x2n @ p("W3").T
-        gate = (silu(h1) * h3).astype(F32)
+        x2n = R("x2n", x2n)
+        h1 = R("h13", x2n @ p("W1").T)
+        h3 = R("h13", x2n @ p("W3").T)
+        gate = R("gate", (silu(h1) * h3).astype(F32))
         f = gate @ p("W2").T
         x = (x2 + a * f).astype(F32)
         c.update(qr=qr, kr=kr, probs=probs, att=attf, x2=x2, x2n=x2n, r2=r2, h1=h1, h3=h3,
@@ -303,6 +321,7 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
         layers.append(c)
     xL = x
     xf, rf = rmsnorm(xL, P["rms_final"], cfg.eps)
+    xf = R("xf", xf)
     E_cls = P["embed"] if vocab_ids is None else P["embed"][vocab_ids]
     logits = xf @ E_cls.T                                 # [B,S,V] (or [B,S,CV])
     T = B * S
@@ -324,16 +343,18 @@ def forward(cfg: Config, P: dict, tokens: np.ndarray, loss_scale: float = 1.0, w
     if want_grad_cache:
         dlog = probs_v * F32(loss_scale / T)
         dlog[np.arange(T), t_flat] -= F32(loss_scale / T)
-        cache = dict(inp=inp, tgt=tgt, layers=layers, xL=xL, xf=xf, rf=rf, dlogits=dlog.astype(F32),
+        cache = dict(inp=inp, tgt=tgt, layers=layers, xL=xL, xf=xf, rf=rf, dlogits=R("dlogits", dlog.astype(F32)),
                      cos=cos, sin=sin, B=B, S=S, vocab_ids=vocab_ids)
     return loss, cache
 
 
-def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> dict:
+def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False, rnd=None) -> dict:
     """Analytic fp32 backward of forward(); returns grads keyed like P (loss_scale included).
 
     norm_bwd_ref: the attention, FFN and final RMSNorms use the reference's backward formula
-    (rmsnorm_bwd(ref=True); TD/train.m:527, 603, 751); the QK-norms stay exact."""
+    (rmsnorm_bwd(ref=True); TD/train.m:527, 603, 751); the QK-norms stay exact.  rnd: see
+    ROUND_SITES."""
+    R = rnd or _keep
     B, S = cache["B"], cache["S"]
     D, NH, NKV, HD = cfg.dim, cfg.n_heads, cfg.kv_heads, cfg.head_dim
     r_gqa = cfg.gqa_ratio
@@ -360,13 +381,13 @@ def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> d
         p = lambda t: P[f"layers.{l}.{t}"]
         g = lambda t: f"layers.{l}.{t}"
         # FFN
-        dffn = a * dx                                      # grad of f
+        dffn = R("dbf", a * dx)                            # grad of f
         G[g("W2")] += (dffn.reshape(-1, D).T @ c["gate"].reshape(B * S, -1)).astype(F32)
         dgate = dffn @ p("W2")
         h1, h3 = c["h1"], c["h3"]
         sig = (F32(1.0) / (F32(1.0) + np.exp(-h1))).astype(F32)
-        dh3 = dgate * (h1 * sig)
-        dh1 = dgate * h3 * sig * (F32(1.0) + h1 * (F32(1.0) - sig))
+        dh3 = R("dh13", dgate * (h1 * sig))
+        dh1 = R("dh13", dgate * h3 * sig * (F32(1.0) + h1 * (F32(1.0) - sig)))
         x2n = c["x2n"].reshape(B * S, D)
         G[g("W1")] += (dh1.reshape(B * S, -1).T @ x2n).astype(F32)
         G[g("W3")] += (dh3.reshape(B * S, -1).T @ x2n).astype(F32)
@@ -375,9 +396,9 @@ def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> d
         G[g("rms_ffn")] += dg
         dx2 = (dx + dxr).astype(F32)
         # attention
-        do = a * dx2
+        do = R("dbf", a * dx2)
         G[g("Wo")] += (do.reshape(-1, D).T @ c["att"].reshape(B * S, -1)).astype(F32)
-        datt = (do @ p("Wo")).reshape(B, S, NH, HD)
+        datt = R("datt", (do @ p("Wo")).reshape(B, S, NH, HD))
         qr, kr, v, probs = c["qr"], c["kr"], c["v"], c["probs"]
         dqr = np.zeros_like(qr)
         dkr = np.zeros_like(kr)
@@ -387,11 +408,12 @@ def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> d
                 kh = h // r_gqa
                 pr = probs[b, h]
                 do_h = datt[b, :, h, :]
-                dv[b, :, kh, :] += pr.T @ do_h
+                dv[b, :, kh, :] += R("p_bwd", pr).T @ do_h
                 dp = do_h @ v[b, :, kh, :].T
-                ds = pr * (dp - np.sum(dp * pr, axis=1, keepdims=True, dtype=F32))
+                ds = R("ds", pr * (dp - np.sum(dp * pr, axis=1, keepdims=True, dtype=F32)))
                 dqr[b, :, h, :] = (ds @ kr[b, :, kh, :]) * scale
                 dkr[b, :, kh, :] += (ds.T @ qr[b, :, h, :]) * scale
+        dv = R("dv", dv)
         dqn = rope_bwd(dqr, cos, sin)
         dkn = rope_bwd(dkr, cos, sin)
         if cfg.qk_norm:
@@ -401,6 +423,7 @@ def backward(cfg: Config, P: dict, cache: dict, norm_bwd_ref: bool = False) -> d
             G[g("k_norm")] += dgk
         else:
             dq, dk = dqn, dkn
+        dq, dk = R("dqk", dq), R("dqk", dk)
         dq = dq.reshape(B * S, -1)
         dk = dk.reshape(B * S, -1)
         dvf = dv.reshape(B * S, -1)
