@@ -495,6 +495,54 @@ def test_step_identical_across_launch_modes(compact):
                 np.testing.assert_array_equal(a[n], b[n], err_msg=n)
 
 
+def test_update_sequences_identical_across_launch_modes():
+    """At Qwen3-0.6B's layer shapes and 256 tokens (the weight-gradient GEMMs of a short step),
+    sequences of accumulating micro-steps, optimizer updates (each deferred to the next step's
+    forward on two streams), zero_grads, a gradient read and a switch to one stream and back
+    leave the losses, gradient norms, gradients and weights bit-identical between in-order
+    launches on one stream and the two-stream schedule."""
+    cfg = om.tiny(**CASES["qwen3"], n_layers=2, dim=1024, hidden=3072, n_heads=16, kv_heads=8,
+                  head_dim=128, vocab=4096, seq=128)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    toks = [om.tokens_for_step(cfg, 2, cfg.seq, seed=s) for s in (1, 2, 3)]
+    opt = dict(lr=3e-4, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_scale=1 / 256, clip=1.0)
+    out = []
+    for mode in ("profiled", "two_streams"):
+        print(f"\nmode {mode}", flush=True)
+        m = ne.Model.from_oracle(cfg, batch=2)
+        m.overlap_weight_grads(mode == "two_streams")
+        if mode == "profiled":
+            m.prof_enable()
+        m.set_params(P)
+        rec = []
+        # two accumulating micro-steps, then an update over the accumulated sum
+        rec += [m.train_step(toks[0], 256.0), m.train_step(toks[1], 256.0)]
+        rec.append(m.optimizer_step(**opt))
+        # one micro-step (the update above beside its forward), an update of its fresh sum
+        rec.append(m.train_step(toks[2], 256.0))
+        rec.append(m.optimizer_step(**opt))
+        # a micro-step whose gradients are dropped, then one whose gradients are read
+        rec.append(m.train_step(toks[0], 256.0))
+        m.zero_grads()
+        rec.append(m.train_step(toks[1], 256.0))
+        g1 = m.get_all(shapes(cfg), ne.NE_GRAD)
+        rec.append(m.optimizer_step(**opt))
+        # a micro-step left pending across a switch to one stream and back
+        rec.append(m.train_step(toks[2], 256.0))
+        m.overlap_weight_grads(False)
+        m.overlap_weight_grads(mode == "two_streams")
+        rec.append(m.train_step(toks[0], 256.0))
+        rec.append(m.optimizer_step(**opt))
+        rec.append(m.train_step(toks[1], 256.0))
+        out.append((rec, g1, m.get_all(shapes(cfg), ne.NE_GRAD), m.get_all(shapes(cfg))))
+        m.close()
+    (r0, *t0), (r1, *t1) = out
+    assert r1 == r0
+    for a, b in zip(t1, t0):
+        for n in b:
+            np.testing.assert_array_equal(a[n], b[n], err_msg=n)
+
+
 def test_step_timeline():
     """ne_step_timeline: the phases of the last step (HIP events at its phase boundaries on
     the step stream) are non-negative and add up to no more than the step, each layer's
