@@ -762,6 +762,31 @@ void gemm_ce_layout(int M, int N, int K, int *main_cols, int *w_main, int *w_res
   *w_rest = nm ? tile_bn(gemm_tile(M, N - nm, K)) : *w_main;
 }
 
+bool gemm_ce_piece_ok(int M, int N, int K, int c0, int c1) {
+  if (c0 == 0 && c1 == N) return true;
+  if (ragged_main(M, N, K) || c0 < 0 || c1 > N || c0 >= c1) return false;
+  const int tile = gemm_tile(M, N, K), bn = tile_bn(tile), w = c1 - c0;
+  return c0 % bn == 0 && w % bn == 0 && gemm_tile(M, w, K) == tile && !ragged_main(M, w, K);
+}
+
+int gemm_ce_pieces(int M, int N, int K, int max_pieces, int *cut) {
+  cut[0] = 0;
+  cut[1] = N;
+  if (max_pieces < 2 || ragged_main(M, N, K)) return 1;
+  const int tile = gemm_tile(M, N, K), bn = tile_bn(tile);
+  const int per = tile == TILE_256 || tile == TILE_256x128 ? 256 : 512;  // 8-wave tiles: one per CU
+  const int np = std::min(max_pieces, N / bn / per);
+  if (np < 2) return 1;
+  for (int k = 0; k < np; k++) {
+    cut[k + 1] = k + 1 < np ? (k + 1) * per * bn : N;
+    if (!gemm_ce_piece_ok(M, N, K, cut[k], cut[k + 1])) {
+      cut[1] = N;
+      return 1;
+    }
+  }
+  return np;
+}
+
 bool gemm_group_fits(const GemmArgs *g, int n) {
   if (n < 1 || n > GEMM_GROUP_MAX) return false;
   long tiles = 0;

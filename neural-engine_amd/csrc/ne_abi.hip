@@ -202,9 +202,8 @@ int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, co
   return gemm_launch(dt, GEMM_NT, EPI_CE_BWD, g, s);
 }
 
-int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, int n_valid,
-                    float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale,
-                    void *dlogits, int *ovf, hipStream_t s) {
+int ce_forward_piece(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, int n_valid,
+                     int c0, int c1, float *part, float *tgt_logit, void *dlogits, hipStream_t s) {
   if (n_valid <= 0 || n_valid > V) return ne_fail(NE_ERR_ARG, "ce: %d valid columns of %d", n_valid, V);
   if (!dlogits || ((uintptr_t)dlogits & 15)) return ne_fail(NE_ERR_ARG, "ce: dlogits must be 16-byte aligned");
   GemmArgs g = {};
@@ -214,13 +213,38 @@ int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets
   g.alpha = 1.f;
   g.targets = targets; g.part = part; g.tgt_logit = tgt_logit;
   g.n_valid = n_valid;
-  NE_CHECK(gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s));
+  if (!gemm_ce_piece_ok(T, V, D, c0, c1))
+    return ne_fail(NE_ERR_ARG, "ce: columns [%d, %d) are not a piece of the %d x %d x %d classifier", c0, c1, T, V, D);
+  if (c0 != 0 || c1 != V) {  // a piece: its own tiles of the whole shape's tiling
+    int mc, wm, wr;
+    gemm_ce_layout(T, V, D, &mc, &wm, &wr);
+    g.N = c1 - c0;
+    g.B = (const h16_t *)E + (long)c0 * D;
+    g.C = (h16_t *)dlogits + c0;
+    g.col0 = c0;
+    g.part_ld = gemm_ce_tiles(T, V, D);
+    g.tile0 = c0 / wm;
+  }
+  return gemm_launch(dt, GEMM_NT, EPI_CE_FWD, g, s);
+}
+
+int ce_forward_finish(int dt, const int32_t *targets, int T, int D, int V, int n_valid, float *part,
+                      float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale, void *dlogits,
+                      int *ovf, hipStream_t s) {
   const int n_tiles = gemm_ce_tiles(T, V, D);
   NE_CHECK(launch_ce_reduce(part, n_tiles, tgt_logit, lse, loss_rows, loss, T, s));
   int mc, wm, wr;
   gemm_ce_layout(T, V, D, &mc, &wm, &wr);
   return launch_ce_grad(dt, (h16_t *)dlogits, T, V, n_valid, part, n_tiles, mc, wm, wr, lse, tgt_logit, targets,
                         scale, ovf, s);
+}
+
+int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V, int n_valid,
+                    float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale,
+                    void *dlogits, int *ovf, hipStream_t s) {
+  NE_CHECK(ce_forward_piece(dt, x, E, targets, T, D, V, n_valid, 0, V, part, tgt_logit, dlogits, s));
+  return ce_forward_finish(dt, targets, T, D, V, n_valid, part, tgt_logit, lse, loss_rows, loss, scale, dlogits, ovf,
+                           s);
 }
 
 extern "C" int ne_k_ce_fwd(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D, int V,

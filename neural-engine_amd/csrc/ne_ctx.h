@@ -69,12 +69,15 @@ struct ne_ctx {
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   // Two-stream schedule: ne_optimizer_step leaves its AdamW pass (upd, after the norm and
   // clip on st) to the next training step, which enqueues it on st2 in chunks, each marked by
-  // ev_adam[k] (0: the gains, 1 + l: layer l, L + 1: the last piece of the embedding), and
-  // waits for chunk k just before it reads what the chunk writes; its lookup computes the
-  // updated rows itself, and the embedding's pieces start after it (ev_lookup).
+  // ev_adam[k] (0: the gains, 1 + l: layer l, L + 1 + p: the embedding rows of classifier piece
+  // p), and waits for chunk k just before it reads what the chunk writes; its lookup computes
+  // the updated rows itself, and the embedding's pieces start after it (ev_lookup).
   // upd_deferred: such a pass has not been enqueued yet (any other entry point that touches
   // the parameters runs it on st first); adam_pending: enqueued, not yet waited for by st.
   std::vector<hipEvent_t> ev_adam;
+  // The classifier's vocabulary pieces (gemm_ce_pieces of the T x V x D logits GEMM): columns
+  // [ce_cut[p], ce_cut[p + 1]), each run after the AdamW chunk of its embedding rows.
+  std::vector<int> ce_cut;
   hipEvent_t ev_lookup = nullptr;
   AdamArgs upd = {};
   bool upd_deferred = false;

@@ -102,7 +102,7 @@ int adam_join(ne_ctx *c) {
     prof_end(c, NE_PROF_ADAM, e0, c->st);
   }
   if (!c->adam_pending) return 0;
-  NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam[c->L + 1], 0));
+  NE_HIP(hipStreamWaitEvent(c->st, c->ev_adam.back(), 0));
   c->adam_pending = false;
   return 0;
 }
@@ -452,6 +452,10 @@ float *kind_base(ne_ctx *c, int kind) {
 
 // ------------------------------------------------------------------------ lifetime ----
 
+// Vocabulary pieces of the classifier's logits GEMM at most (ce_cut): a 256-token Qwen3-0.6B
+// step has four (256, 256, 256 and 419 work-groups of 256 x 128 tiles).
+constexpr int CE_PIECES_MAX = 8;
+
 extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if (validate(cfg)) return nullptr;
   ne_ctx *c = new ne_ctx();
@@ -498,6 +502,8 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->ws2, (size_t)c->ws_elems);
   plan_gn(c);
   pl.add(&c->gn_part, (size_t)gn_slots(c));
+  c->ce_cut.assign(CE_PIECES_MAX + 1, 0);
+  c->ce_cut.resize(gemm_ce_pieces(T, c->V, D, CE_PIECES_MAX, c->ce_cut.data()) + 1);
   // gain-gradient partials of every norm site (2L+1 RMSNorms, L QK-norm pairs), summed by one
   // ordered launch at the end of the backward
   c->rms_slab = rmsnorm_bwd_part_elems(c->T, c->D);
@@ -511,7 +517,7 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   if ((rc = ne_hip_status(hipStreamCreateWithFlags(&c->st2, hipStreamNonBlocking), "stream"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event"))) goto fail;
   if ((rc = ne_hip_status(hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event"))) goto fail;
-  c->ev_adam.assign(c->L + 2, nullptr);
+  c->ev_adam.assign(c->L + c->ce_cut.size(), nullptr);
   c->tl.fwd_l.assign(c->L, nullptr);  // the step names them whether or not the timeline is on
   c->tl.bwd_l.assign(c->L, nullptr);
   for (auto &e : c->ev_adam)
@@ -727,10 +733,13 @@ struct UpdateQueue {
         NE_HIP(hipEventRecord(c->ev_adam[1 + next], c->st2));
       } else {
         NE_HIP(hipStreamWaitEvent(c->st2, c->ev_lookup, 0));
-        const long ne = (long)c->V * c->D;
-        NE_CHECK(chunk(c->off_E, ne, ne));
+        for (size_t p = 0; p + 1 < c->ce_cut.size(); p++) {
+          const long r0 = c->ce_cut[p], n = (long)(c->ce_cut[p + 1] - r0) * c->D;
+          NE_CHECK(chunk(c->off_E + r0 * c->D, n, n));
+          if (p + 2 < c->ce_cut.size()) NE_HIP(hipEventRecord(c->ev_adam[L + 1 + p], c->st2));
+        }
         prof_end(c, NE_PROF_ADAM, e0, c->st2);
-        NE_HIP(hipEventRecord(c->ev_adam[L + 1], c->st2));
+        NE_HIP(hipEventRecord(c->ev_adam.back(), c->st2));
         NE_CHECK(tl_mark(c, c->tl.upd1, c->st2));
         c->tl.opt_ok = c->tl.on;
       }
@@ -843,17 +852,29 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
   }
   NE_CHECK(tl_mark(c, c->tl.fwd));
   if (upd) NE_CHECK(uq.upto(c->L));
-  NE_CHECK(wait_update(c->L + 1));
   // classifier: the tied embedding, or its compact rows (vocabulary compaction; padding
-  // columns cv..cvp are masked out of the softmax)
+  // columns cv..cvp are masked out of the softmax).  The full vocabulary's logits GEMM runs in
+  // the pieces of ce_cut, each right after the update of its embedding rows: the last pieces
+  // of the update overlap the first pieces of the GEMM.
   const bool compact = c->cv > 0;
   const int Vc = compact ? c->cvp : V, Vvalid = compact ? c->cv : V;
   const h16_t *Ecls = compact ? c->cE : Pb + c->off_E;
   {
     ProfScope ps(c, NE_PROF_CE);
-    if (compact) NE_CHECK(launch_gather_rows16(Pb + c->off_E, c->cids, c->cE, c->cvp, D, c->st));
-    NE_CHECK(ce_forward_grad(dt, c->xf, Ecls, c->tok_tgt, T, D, Vc, Vvalid, c->ce_part, c->ce_tgt, c->ce_lse,
-                             c->ce_rows, c->loss, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
+    if (compact) {
+      NE_CHECK(wait_update((int)c->ev_adam.size() - 1));
+      NE_CHECK(launch_gather_rows16(Pb + c->off_E, c->cids, c->cE, c->cvp, D, c->st));
+      NE_CHECK(ce_forward_grad(dt, c->xf, Ecls, c->tok_tgt, T, D, Vc, Vvalid, c->ce_part, c->ce_tgt, c->ce_lse,
+                               c->ce_rows, c->loss, c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
+    } else {
+      for (size_t p = 0; p + 1 < c->ce_cut.size(); p++) {
+        NE_CHECK(wait_update(c->L + 1 + (int)p));
+        NE_CHECK(ce_forward_piece(dt, c->xf, Ecls, c->tok_tgt, T, D, V, V, c->ce_cut[p], c->ce_cut[p + 1],
+                                  c->ce_part, c->ce_tgt, c->dlogits, c->st));
+      }
+      NE_CHECK(ce_forward_finish(dt, c->tok_tgt, T, D, V, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows, c->loss,
+                                 c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
+    }
   }
 
   // ---------------- backward (gradients at scale gs until the fp32 sinks) ----------------

@@ -101,6 +101,13 @@ int gemm_ce_tiles(int M, int N, int K);  // EPI_CE_FWD: the partial slots per ro
 // w_rest; partial slot of column c: c < main_cols ? c / w_main : main_cols / w_main +
 // (c - main_cols) / w_rest.
 void gemm_ce_layout(int M, int N, int K, int *main_cols, int *w_main, int *w_rest);
+// Column pieces of EPI_CE_FWD's M x N x K GEMM that run with the whole shape's tiles: cut[0] = 0
+// < cut[1] < ... < cut[np] = N on its tile boundaries, each piece as many tiles as run at once
+// on the device (the last takes the remainder).  Returns np (<= max_pieces; 1 when the shape is
+// ragged or a piece would plan another tile).
+int gemm_ce_pieces(int M, int N, int K, int max_pieces, int *cut);
+// Whether columns [c0, c1) are such a piece (or the whole).
+bool gemm_ce_piece_ok(int M, int N, int K, int c0, int c1);
 // K splits gemm_launch would use for this shape with a workspace of ws_elems floats (1: none).
 int gemm_splits(int epi, int M, int N, int K, long ws_elems);
 // Sum-of-squares slots (GemmArgs::sq) gemm_launch writes for this shape (EPI_F32 /
@@ -208,6 +215,15 @@ int ce_backward(int dt, const void *x, const void *E, const int32_t *targets, co
 int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
                     int n_valid, float *part, float *tgt_logit, float *lse, float *loss_rows, float *loss,
                     float scale, void *dlogits, int *ovf, hipStream_t s);
+// The same in parts: ce_forward_piece runs the logits GEMM over vocabulary columns [c0, c1)
+// (boundaries from gemm_ce_pieces(T, V, D, ...)) against E rows [c0, c1); once every piece has
+// run, ce_forward_finish reduces the rows and forms the gradient.  The pieces give the same bits
+// as the whole.
+int ce_forward_piece(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
+                     int n_valid, int c0, int c1, float *part, float *tgt_logit, void *dlogits, hipStream_t s);
+int ce_forward_finish(int dt, const int32_t *targets, int T, int D, int V, int n_valid, float *part,
+                      float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale, void *dlogits,
+                      int *ovf, hipStream_t s);
 int launch_ce_grad(int dt, h16_t *dl, int T, int V, int n_valid, const float *part, int n_tiles, int main_cols,
                    int w_main, int w_rest, const float *lse, const float *tgt_logit, const int32_t *targets,
                    float scale, int *ovf, hipStream_t s);
