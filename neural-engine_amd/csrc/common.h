@@ -106,6 +106,35 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
+// Reductions over the 32 lanes of a half-wave (lanes sharing lane / 32) as an xor butterfly
+// of strides 1, 2, 4, 8, 16, every lane left with the same result: the first four strides as DPP
+// operands of the VALU (quad permutations for 1 and 2; then, the value being uniform over each
+// quad and then over each 8-lane half-row, the half-row and row mirrors pair the same groups as
+// xor 4 and xor 8), the last as one swizzle (xor 16 inside 32 lanes).  Cross-lane permutes
+// through LDS (ds_bpermute) for all five strides cost the cross-entropy forward epilogue
+// 160 permutes per lane per pass.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]: xor 1
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: xor 2
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v + swizzle_xor16(v);
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  return fmaxf(v, swizzle_xor16(v));
+}
+
 // Reductions over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
 __device__ __forceinline__ float quad16_sum(float v) {
   v += __shfl_xor(v, 16, 64);

@@ -325,9 +325,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
           mx = fmaxf(mx, v);
           if (col == tgt) g.tgt_logit[row] = v;
         }
-        // reduce over the 32 lanes sharing this row (lanes with equal lane>>5)
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        mx = half_wave_max(mx);  // over the 32 lanes sharing this row (equal lane>>5)
         if ((lane & 31) == 0) red_m[wn][rl] = mx;
       }
     }
@@ -351,8 +349,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
           s += ev;
           if (ce) ce[(long)(m0 + rl) * g.ldc + cl] = HT::h(ev);
         }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        s = half_wave_sum(s);
         if ((lane & 31) == 0) red_s[wn][rl] = s;
       }
     }
