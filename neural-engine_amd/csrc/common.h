@@ -135,6 +135,12 @@ __device__ __forceinline__ float half_wave_max(float v) {
   return fmaxf(v, swizzle_xor16(v));
 }
 
+// The same butterfly over all 64 lanes (one LDS permute for the last stride, 32).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = half_wave_sum(v);
+  return v + __shfl_xor(v, 32, 64);
+}
+
 // Reductions over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
 __device__ __forceinline__ float quad16_sum(float v) {
   v += __shfl_xor(v, 16, 64);

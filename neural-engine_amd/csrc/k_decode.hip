@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
           const float4 v = xa[b][i];
           ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-      ss[b] = wave_sum(ss[b]);
+      ss[b] = wave_sum_dpp(ss[b]);
     }
     if (lane == 0)
 #pragma unroll
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
 #pragma unroll
   for (int r = 0; r < RPW; r++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
+    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum_dpp(acc[r][b]);
   if (GATE) {
     if (lane < HALF * NB) {
       const int r = lane / NB, b = lane % NB;
