@@ -140,6 +140,10 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = half_wave_sum(v);
   return v + __shfl_xor(v, 32, 64);
 }
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = half_wave_max(v);
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
 
 // Reductions over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
 __device__ __forceinline__ float quad16_sum(float v) {

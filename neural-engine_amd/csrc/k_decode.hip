@@ -582,7 +582,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const float *gg = isq ? gq : gk;
     if (gg) {  // uniform per block: every lane of the slot's (half-)wave takes part
       float ss = x0 * x0 + x1 * x1;
-      for (int o = 1; o < HALF; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      ss = HALF == 64 ? wave_sum_dpp(ss) : half_wave_sum(ss);
       const float rms = sqrtf(ss / (float)HD + eps);
       x0 = x0 / rms * gg[2 * p];
       x1 = x1 / rms * gg[2 * p + 1];
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   }
 #pragma unroll
   for (int r = 0; r < RATIO; r++) {
-    mx[r] = wave_max(mx[r]);
+    mx[r] = wave_max_dpp(mx[r]);
     if ((tid & 63) == 0) red[r][tid >> 6] = mx[r];
   }
   __syncthreads();
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     }
 #pragma unroll
   for (int r = 0; r < RATIO; r++) {
-    sum[r] = wave_sum(sum[r]);
+    sum[r] = wave_sum_dpp(sum[r]);
     if ((tid & 63) == 0) red[r][4 + (tid >> 6)] = sum[r];
   }
   __syncthreads();
