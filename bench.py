@@ -128,8 +128,10 @@ def run_train(w, steps, warmup, graphs=True, overlap=True):
     m.prof_enable(())
     scale, skipped, sites = m.grad_scale_info()
     loss = m.train_step(toks[0], 256.0)
+    upd_launches = m.update_launches()
     m.close()
-    return dict(ms=ms, adam=(adam_ms, adam_n), fam=fam, skipped=skipped, scale=scale, loss=loss, sites=sites)
+    return dict(ms=ms, adam=(adam_ms, adam_n), fam=fam, skipped=skipped, scale=scale, loss=loss, sites=sites,
+                upd_launches=upd_launches)
 
 
 def run_decode(w, B, n_new=200, prompt_len=32, graphs=True):
@@ -522,20 +524,22 @@ def main():
     npar = n_params(w)
     fam_ms = summ["kernel_ms_per_step"]
     dom = max(fam_ms, key=fam_ms.get)
-    # One AdamW pass per step, run by the next step beside its forward in L + 2 launches on the
-    # second stream (the gains, one per layer, the embedding; capped at 384 work-groups each),
-    # between one event pair (a pair per launch cost the step 0.22 ms); the last pass of the
-    # timed steps runs after them in one launch.  Pass time: the pair's span, gaps included.
+    # One AdamW pass per step, run by the next step beside its forward on the second stream in
+    # ne_update_launches launches (the gains, one per layer, the embedding's rows in the
+    # classifier's vocabulary pieces; capped at 384 work-groups each), between one event pair (a
+    # pair per launch cost the step 0.22 ms); the last pass of the timed steps runs after them in
+    # one launch.  Pass time: the pair's span, gaps included.
     passes = max(r["adam"][1], 1)
-    adam_launches = 1 if a.no_overlap else w["n_layers"] + 2   # one stream: the pass in one launch
+    adam_launches = 1 if a.no_overlap else r["upd_launches"]   # one stream: the pass in one launch
     adam_ms = r["adam"][0] / passes
     adam_bytes = 30 * npar                                 # read p,g,m,v; write p,m,v + 16-bit shadow
     roofline = {"bound": "hbm",
                 "kernel": ("adam_kernel (fused AdamW; one pass over all parameters per step, in one launch after "
                            "the step on one stream)" if a.no_overlap else
                            "adam_kernel (fused AdamW; one pass over all parameters per step, run beside the next "
-                           f"step's forward in {adam_launches} launches: the gains, one per layer, the embedding, "
-                           "each capped at 384 work-groups; timed by one event pair around the pass)"),
+                           f"step's forward in {adam_launches} launches: the gains, one per layer, the embedding's "
+                           "rows in the classifier's vocabulary pieces, each capped at 384 work-groups; timed by "
+                           "one event pair around the pass)"),
                 "achieved": adam_bytes / (adam_ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                 "frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM,
                 "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,

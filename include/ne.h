@@ -240,6 +240,11 @@ enum {
 };
 int ne_timeline(ne_ctx *ctx, int on);
 int ne_step_timeline(ne_ctx *ctx, float out[NE_TL_COUNT], float *layer_fwd, float *layer_bwd);
+/* Launches of the AdamW pass that a training step runs beside its forward after an optimizer
+ * step on two streams: the gains, one per layer, then the embedding's rows in the classifier's
+ * vocabulary pieces (a measurement aid for the pass's per-launch roofline; the reference's
+ * update, TD/train.m:861-897, is one CPU loop over the tensors).  Negative for a NULL ctx. */
+int ne_update_launches(const ne_ctx *ctx);
 
 /* ------------------------------------------------------ kernel-level entry points ---- */
 /* Device-pointer entry points of the individual kernels, for testing and for callers

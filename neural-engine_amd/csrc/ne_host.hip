@@ -1306,6 +1306,11 @@ extern "C" int ne_timeline(ne_ctx *c, int on) {
   return 0;
 }
 
+extern "C" int ne_update_launches(const ne_ctx *c) {
+  if (!c) return ne_fail(NE_ERR_ARG, "null context");
+  return 1 + c->L + (int)c->ce_cut.size() - 1;
+}
+
 extern "C" int ne_step_timeline(ne_ctx *c, float *out, float *layer_fwd, float *layer_bwd) {
   if (!c || !out) return ne_fail(NE_ERR_ARG, "null argument");
   const Timeline &t = c->tl;

@@ -31,7 +31,7 @@ EXPORTS = (
     "ne_rmsnorm_bwd_formula", "ne_zero_grads",
     "ne_grad_scale_info", "ne_grad_norm_parts", "ne_step_stats", "ne_get_state", "ne_set_state", "ne_load_ckpt_v4", "ne_save_ckpt_v4",
     "ne_decode", "ne_decode_seeded", "ne_mt19937_uniforms", "ne_set_vocab_map",
-    "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_timeline", "ne_step_timeline", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
+    "ne_prof_enable", "ne_prof_reset", "ne_prof_get", "ne_timeline", "ne_step_timeline", "ne_update_launches", "ne_k_rmsnorm_fwd", "ne_k_rmsnorm_bwd",
     "ne_k_gemm", "ne_k_gemm_wgrad_group", "ne_k_qk_prep_fwd", "ne_k_qk_prep_bwd", "ne_k_attn_fwd", "ne_k_attn_bwd", "ne_k_attn_bwd_noalloc",
     "ne_k_ce_fwd", "ne_k_ce_bwd", "ne_k_ce_fwd_grad", "ne_k_adam", "ne_k_grad_norm", "ne_k_embed_fwd",
     "ne_k_embed_bwd", "ne_k_swiglu_fwd", "ne_k_mfma_ceiling",
@@ -128,6 +128,7 @@ def lib():
         "ne_prof_get": (I, [P, I, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "ne_timeline": (I, [P, I]),
         "ne_step_timeline": (I, [P, P, P, P]),
+        "ne_update_launches": (I, [P]),
         "ne_k_rmsnorm_fwd": (I, [I, P, P, P, P, I, I, F, P]),
         "ne_k_rmsnorm_bwd": (I, [I, P, P, P, P, P, P, P, F, P, F, I, I, P]),
         "ne_k_gemm": (I, [I, I, I, I, I, I, P, L, P, L, P, L, P, L, F, P]),
@@ -348,6 +349,13 @@ class Model:
     def timeline(self, on=True):
         """Record the step's phase boundaries with HIP events (ne_timeline)."""
         check(lib().ne_timeline(self._h, int(bool(on))), "timeline")
+
+    def update_launches(self):
+        """Launches of the AdamW pass a two-stream step runs beside its forward."""
+        n = lib().ne_update_launches(self._h)
+        if n < 0:
+            raise NEError(lib().ne_last_error().decode())
+        return n
 
     def step_timeline(self, layers=False):
         """Phases of the last step in ms (TIMELINE_PHASES), and with layers=True the per-layer

@@ -641,6 +641,9 @@ def test_classifier_pieces_match_whole():
     for mapped in (False, True):
         print(f"\nidentity map {mapped}", flush=True)
         m = ne.Model.from_oracle(cfg, batch=1)
+        # the pass beside the forward: the gains, the layer, the embedding in the 4 pieces of
+        # 256, 256, 256 and 419 work-groups of 256 x 128 logits tiles
+        assert m.update_launches() == 1 + cfg.n_layers + 4
         m.set_params(P)
         if mapped:
             m.set_vocab_map(np.arange(cfg.vocab, dtype=np.int32))
