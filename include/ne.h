@@ -330,7 +330,7 @@ int ne_k_ce_bwd(int dtype, const void *x, const void *E, const int32_t *targets,
 /* Forward and backward in one call, as the reference's cross_entropy_loss computes the loss
  * and dlogits together (TD/cpu_ops.h:348-382): ne_k_ce_fwd's outputs, and dlogits as
  * ne_k_ce_bwd defines it, without a second logits GEMM: the GEMM's epilogue stores each
- * logit as the 16-bit exp(logit - its 256-column tile's max) into dlogits, which one
+ * logit as the 16-bit exp(logit - the max of its column tile) into dlogits, which one
  * streaming pass turns into (softmax - onehot) * scale once the rows' log-sum-exp is known
  * (the target's probability from its fp32 logit).  dlogits: 16-byte aligned [T, V]. */
 int ne_k_ce_fwd_grad(int dtype, const void *x, const void *E, const int32_t *targets, int T, int D,

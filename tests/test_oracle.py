@@ -385,3 +385,36 @@ def test_ckpt_reference_sizes():
     """Byte counts of the reference checkpoints computed from TD/train.m:97-131."""
     assert ckpt.expected_size(om.stories110m()) == 1_314_358_368
     assert ckpt.expected_size(om.qwen3_06b(qk_norm=False)) == 7_152_513_120
+
+
+def test_rounding_hooks_pass_values_through_and_reach_every_site():
+    """The oracle's 16-bit rounding hooks (used only by the bf16 site study): an identity hook
+    leaves the loss and every gradient bit-identical to no hook, and the forward and backward
+    visit every site of ROUND_SITES; rounding one backward site (dlogits) to bf16 moves the
+    gradients, rounding the final norm's output moves the loss."""
+    cfg = om.tiny(qk_norm=True, n_layers=2)
+    P = om.init_params(cfg, seed=0, std=0.02)
+    tok = om.tokens_for_step(cfg, 2, cfg.seq, seed=1)
+    seen = set()
+
+    def ident(site, x):
+        seen.add(site)
+        return x
+
+    l0, c0 = om.forward(cfg, P, tok, loss_scale=256.0)
+    g0 = om.backward(cfg, P, c0)
+    l1, c1 = om.forward(cfg, P, tok, loss_scale=256.0, rnd=ident)
+    g1 = om.backward(cfg, P, c1, rnd=ident)
+    assert l1 == l0
+    for n in g0:
+        np.testing.assert_array_equal(g1[n], g0[n], err_msg=n)
+    assert seen == set(om.ROUND_SITES)
+
+    def only(name):
+        return lambda site, x: om.round_bf16(np.asarray(x, np.float32)) if site == name else x
+
+    _, c2 = om.forward(cfg, P, tok, loss_scale=256.0, rnd=only("dlogits"))
+    g2 = om.backward(cfg, P, c2, rnd=only("dlogits"))
+    assert any(not np.array_equal(g2[n], g0[n]) for n in g0)
+    l3, _ = om.forward(cfg, P, tok, loss_scale=256.0, rnd=only("xf"))
+    assert l3 != l0
