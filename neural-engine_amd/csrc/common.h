@@ -88,17 +88,6 @@ __device__ __forceinline__ void flag_overflow(int *ovf, bool bad) {
   if (ovf && bad) *ovf = 1;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
 
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -136,11 +125,11 @@ __device__ __forceinline__ float half_wave_max(float v) {
 }
 
 // The same butterfly over all 64 lanes (one LDS permute for the last stride, 32).
-__device__ __forceinline__ float wave_sum_dpp(float v) {
+__device__ __forceinline__ float wave_sum(float v) {
   v = half_wave_sum(v);
   return v + __shfl_xor(v, 32, 64);
 }
-__device__ __forceinline__ float wave_max_dpp(float v) {
+__device__ __forceinline__ float wave_max(float v) {
   v = half_wave_max(v);
   return fmaxf(v, __shfl_xor(v, 32, 64));
 }

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
           const float4 v = xa[b][i];
           ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-      ss[b] = wave_sum_dpp(ss[b]);
+      ss[b] = wave_sum(ss[b]);
     }
     if (lane == 0)
 #pragma unroll
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(const h16_t *__restrict_
 #pragma unroll
   for (int r = 0; r < RPW; r++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum_dpp(acc[r][b]);
+    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
   if (GATE) {
     if (lane < HALF * NB) {
       const int r = lane / NB, b = lane % NB;
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const float *gg = isq ? gq : gk;
     if (gg) {  // uniform per block: every lane of the slot's (half-)wave takes part
       float ss = x0 * x0 + x1 * x1;
-      ss = HALF == 64 ? wave_sum_dpp(ss) : half_wave_sum(ss);
+      ss = HALF == 64 ? wave_sum(ss) : half_wave_sum(ss);
       const float rms = sqrtf(ss / (float)HD + eps);
       x0 = x0 / rms * gg[2 * p];
       x1 = x1 / rms * gg[2 * p + 1];
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
   }
 #pragma unroll
   for (int r = 0; r < RATIO; r++) {
-    mx[r] = wave_max_dpp(mx[r]);
+    mx[r] = wave_max(mx[r]);
     if ((tid & 63) == 0) red[r][tid >> 6] = mx[r];
   }
   __syncthreads();
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     }
 #pragma unroll
   for (int r = 0; r < RATIO; r++) {
-    sum[r] = wave_sum_dpp(sum[r]);
+    sum[r] = wave_sum(sum[r]);
     if ((tid & 63) == 0) red[r][4 + (tid >> 6)] = sum[r];
   }
   __syncthreads();

@@ -631,12 +631,14 @@ def test_classifier_pieces_match_whole():
     beside the previous update's tail).  An identity vocabulary map runs the same GEMM whole
     after the entire update: over two micro-steps and updates both give bit-identical losses,
     gradients and weights (the pieces change neither the tiles nor their sums, and each waits
-    for its rows' update)."""
+    for its rows' update).  The gradient norm is summed by different kernels in the two
+    forms (the embedding gradient's GEMM tiles against a pass over the scattered compact
+    gradient), so it is compared to 1e-6 and the updates run unclipped."""
     cfg = om.tiny(**CASES["qwen3"], n_layers=1, dim=1024, hidden=3072, n_heads=16, kv_heads=8,
                   head_dim=128, vocab=151936, seq=256)
     P = om.init_params(cfg, seed=0, std=0.02)
     toks = [om.tokens_for_step(cfg, 1, cfg.seq, seed=s) for s in (1, 2)]
-    opt = dict(lr=3e-4, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_scale=1 / 256, clip=1.0)
+    opt = dict(lr=3e-4, b1=0.9, b2=0.95, eps=1e-8, wd=0.1, grad_scale=1 / 256, clip=1e9)
     out = []
     for mapped in (False, True):
         print(f"\nidentity map {mapped}", flush=True)
@@ -647,14 +649,16 @@ def test_classifier_pieces_match_whole():
         m.set_params(P)
         if mapped:
             m.set_vocab_map(np.arange(cfg.vocab, dtype=np.int32))
-        rec = [m.train_step(toks[0], 256.0), m.optimizer_step(**opt), m.train_step(toks[1], 256.0)]
+        losses, norms = [m.train_step(toks[0], 256.0)], [m.optimizer_step(**opt)]
+        losses.append(m.train_step(toks[1], 256.0))
         g = m.get_all(shapes(cfg), ne.NE_GRAD)
-        rec.append(m.optimizer_step(**opt))
-        rec.append(m.train_step(toks[0], 256.0))
-        out.append((rec, g, m.get_all(shapes(cfg))))
+        norms.append(m.optimizer_step(**opt))
+        losses.append(m.train_step(toks[0], 256.0))
+        out.append((losses, norms, g, m.get_all(shapes(cfg))))
         m.close()
-    (r0, *t0), (r1, *t1) = out
-    assert r1 == r0
+    (l0, n0, *t0), (l1, n1, *t1) = out
+    assert l1 == l0
+    np.testing.assert_allclose(n1, n0, rtol=1e-6)
     for a, b in zip(t1, t0):
         for n in b:
             np.testing.assert_array_equal(a[n], b[n], err_msg=n)
