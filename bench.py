@@ -377,6 +377,14 @@ def counters_collect(outdir, result, commands):
                           "pct": float(row["Percentage"])})
     stats.sort(key=lambda d: -d["total_ms"])
     avg_us = {d["kernel"]: d["avg_us"] for d in stats}
+    # launches per step: the dispatches from one embedding lookup to the next (a training step and
+    # its optimizer step), without the runtime's copies and the MFMA-ceiling measurement
+    with open(os.path.join(outdir, "trace", "run_kernel_trace.csv")) as f:
+        disp = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    names = [_short(r["Kernel_Name"]) for r in disp]
+    starts = [i for i, n in enumerate(names) if n.startswith("embed_fwd")]
+    per_step = [sum(1 for n in names[a:b] if not n.startswith(("__amd_rocclr", "mfma_ceiling")))
+                for a, b in zip(starts, starts[1:])]
 
     def pmc(key):
         """{kernel: {counter: (sum over dispatches, dispatches)}} of a counter pass, and the
@@ -419,6 +427,8 @@ def counters_collect(outdir, result, commands):
             row["hbm_frac"] = gbs * 1e9 / PEAK_HBM
         rows.append(row)
     result["counters"] = {"kernels": rows[:40],
+                          "launches_per_step": sorted(per_step)[len(per_step) // 2] if per_step else None,
+                          "steps_traced": len(per_step),
                           "calibration": {"fetch_bytes_per_unit": fs, "write_bytes_per_unit": wsc,
                                           "how": "three 1 GiB device copies (__amd_rocclr_copyBuffer) in the "
                                                  "byte-counter passes"},
@@ -441,7 +451,10 @@ def counters_markdown(res, made_by):
     out = [f"# rocprofv3 per-kernel report: training step of {res['config']['workload']}", "",
            f"Made by `{made_by}` (one run: its child processes below).", "",
            f"Traced run (eager launches on one stream: each kernel runs alone, so its duration, counters and "
-           f"rates are its own): {res['ms_per_step']:.3f} ms per step.", "",
+           f"rates are its own): {res['ms_per_step']:.3f} ms per step, {c['launches_per_step']} kernel launches per "
+           f"step (a training step and its optimizer step; median over {c['steps_traced']} traced steps, the runtime's "
+           "copies not counted; the two-stream schedule runs the same kernels with the AdamW pass in "
+           f"{res['roofline'].get('update_launches', 'L + 1 + P')} launches instead of one).", "",
            "Commands of the child processes:", ""]
     out += [f"    {v}" for v in c["commands"].values()]
     out += ["", "Durations from the kernel trace; HBM bytes per launch from FETCH_SIZE and WRITE_SIZE scaled by "
@@ -545,7 +558,8 @@ def main():
                 "traffic": ADAM_TRAFFIC_B_PER_PARAM * npar,
                 "traffic_source": ADAM_TRAFFIC_SOURCE,
                 "bytes_per_pass": adam_bytes, "pass_ms": adam_ms, "launches_per_pass": adam_launches,
-                "bytes_per_launch": adam_bytes / adam_launches, "avg_launch_ms": adam_ms / adam_launches}
+                "bytes_per_launch": adam_bytes / adam_launches, "avg_launch_ms": adam_ms / adam_launches,
+                "update_launches": r["upd_launches"]}
     out = {
         "metric": "Qwen3-0.6B train tokens/s + step ms on 1 MI355X; MFMA util %; decode tok/s",
         "value": summ["tokens_per_s"],
