@@ -55,6 +55,13 @@ def test_counters_collect_joins_passes(bench, tmp_path):
             [[adam, "FETCH_SIZE", 1000.0], [adam, "FETCH_SIZE", 3000.0], [gemm, "FETCH_SIZE", 50.0]]
     write = [[copy, "WRITE_SIZE", 1048576.0]] * 3 + [[adam, "WRITE_SIZE", 500.0], [gemm, "WRITE_SIZE", 8.0]]
     mfma = [[gemm, "MfmaUtil", 5.0], [gemm, "SQ_INSTS_VALU_MFMA_MOPS_F16", 1000.0], [adam, "MfmaUtil", 0.0]]
+    # dispatch order: two steps, each from one embedding lookup to the next (copies and the
+    # MFMA-ceiling probe are not counted)
+    emb = "void (anonymous namespace)::embed_fwd_kernel(float const*, int const*, float*, int, int)"
+    probe = "void (anonymous namespace)::mfma_ceiling_kernel<H16F, true>(float*, int)"
+    seq = [emb, gemm, copy, gemm, adam, emb, gemm, probe, gemm, adam, emb]
+    _write(os.path.join(d, "trace", "run_kernel_trace.csv"), ["Kernel_Name", "Start_Timestamp"],
+           [[n, 100 * (i + 1)] for i, n in reversed(list(enumerate(seq)))])
     _write(os.path.join(d, "fetch", "run_counter_collection.csv"), cols, fetch)
     _write(os.path.join(d, "write", "run_counter_collection.csv"), cols, write)
     _write(os.path.join(d, "mfma", "run_counter_collection.csv"), cols, mfma)
@@ -75,8 +82,10 @@ def test_counters_collect_joins_passes(bench, tmp_path):
     assert cal["fetch_bytes_per_unit"] == pytest.approx(2048.0) and cal["write_bytes_per_unit"] == pytest.approx(1024.0)
     assert res["roofline"]["traffic"] == pytest.approx((2000.0 * 2048 + 500.0 * 1024) * 29)
     assert "FETCH_SIZE" in res["roofline"]["traffic_source"]
+    assert res["counters"]["launches_per_step"] == 4 and res["counters"]["steps_traced"] == 2
     md = bench.counters_markdown(res, "python3 bench.py --counters d")
     assert "`adam_kernel<H16F, true>`" in md and "python3 bench.py --counters d" in md
+    assert "4 kernel launches per step" in md
 
 
 def test_more_than_one_gpu_is_refused():
