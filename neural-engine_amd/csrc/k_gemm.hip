@@ -161,21 +161,29 @@ __device__ __forceinline__ void block_sumsq_store(float s, double *out) {
   }
 }
 
-// Final store of one output element v (alpha already applied) for every non-CE epilogue;
+// Final store of one output element v (alpha already applied) for every non-CE epilogue.  NT:
+// fp32 outputs go out (and, accumulating, come in) as non-temporal accesses: the weight and
+// embedding gradients of a short step (2.4 GB per 256-token Qwen3-0.6B step, read back only by
+// the next update) then stream past the caches the activation-gradient chain beside them works
+// from (that step 7.58-7.64 -> 7.45-7.55 ms).  Not on the 256x256 tile, which reads back what it
+// stored for the sums of squares;
 // returns the fp32 value stored (EPI_F32, EPI_F32_ACC; else 0).
-template <typename HT, int EPI>
+template <typename HT, int EPI, bool NT = false>
 __device__ __forceinline__ float store_out(const GemmArgs &g, int row, int col, float v, bool &bad) {
   if constexpr (EPI == EPI_H16) {
     const h16_t o = HT::h(v);
     bad |= HT::bad(o);
     ((h16_t *)g.C)[(long)row * g.ldc + col] = o;
   } else if constexpr (EPI == EPI_F32) {
-    ((float *)g.C)[(long)row * g.ldc + col] = v;
+    float *c = (float *)g.C + (long)row * g.ldc + col;
+    if constexpr (NT) __builtin_nontemporal_store(v, c);
+    else *c = v;
     return v;
   } else if constexpr (EPI == EPI_F32_ACC) {
     float *c = (float *)g.C + (long)row * g.ldc + col;
-    const float o = *c + v;
-    *c = o;
+    const float o = (NT ? __builtin_nontemporal_load(c) : *c) + v;
+    if constexpr (NT) __builtin_nontemporal_store(o, c);
+    else *c = o;
     return o;
   } else if constexpr (EPI == EPI_RESID) {
     ((float *)g.C)[(long)row * g.ldc + col] = ((const float *)g.R)[(long)row * g.ldr + col] + v;
@@ -524,7 +532,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &g, const int mt, const
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int row = m0 + wm * TM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const float o = store_out<HT, EPI>(g, row, col, acc[i][j][e] * alpha, bad);
+        const float o = store_out<HT, EPI, SQ_INLINE>(g, row, col, acc[i][j][e] * alpha, bad);
         if constexpr (epi_sq<EPI>() && SQ_INLINE) sq += o * o;
       }
     }
