@@ -588,10 +588,16 @@ __device__ __forceinline__ void grouped_tile(int u, int num_m, int num_n, int &m
 
 template <typename HT, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, int EPI, int KMODE>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmArgs g) {
-  const int num_m = gridDim.y, num_n = gridDim.x;
+  // The K splits (grid.z) take part in the stretches: an XCD runs all the tiles of a split
+  // (tile fastest in the sequence), so a split's slice of the shared operand is fetched into one
+  // L2.  With the stretches over the tile plane alone, a launch of few tiles and many splits
+  // (the LM-head dX of a 256-token step: 8 tiles x 32 splits) put each split's 8 tiles on the 8
+  // XCDs, and every XCD fetched every slice of dlogits (933 MB read per launch for 389 MB).
+  const int num_m = gridDim.y, num_n = gridDim.x, plane = num_m * num_n;
+  const int u = xcd_stretch(blockIdx.x + num_n * (blockIdx.y + num_m * blockIdx.z), plane * gridDim.z);
   int mt, nt;
-  grouped_tile(xcd_stretch(blockIdx.y * num_n + blockIdx.x, num_m * num_n), num_m, num_n, mt, nt);
-  gemm_body<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KMODE>(g, mt, nt, blockIdx.z);
+  grouped_tile(u % plane, num_m, num_n, mt, nt);
+  gemm_body<HT, BM, BN, BK, WM, WN, AKC, BKC, EPI, KMODE>(g, mt, nt, u / plane);
 }
 
 // Several GEMMs of one shape class in one launch (the weight gradients of a layer): problem
