@@ -232,7 +232,8 @@ int ce_forward_finish(int dt, const int32_t *targets, int T, int D, int V, int n
                       float *tgt_logit, float *lse, float *loss_rows, float *loss, float scale, void *dlogits,
                       int *ovf, hipStream_t s) {
   const int n_tiles = gemm_ce_tiles(T, V, D);
-  NE_CHECK(launch_ce_reduce(part, n_tiles, tgt_logit, lse, loss_rows, loss, T, s));
+  NE_CHECK(launch_ce_rows(part, n_tiles, tgt_logit, lse, loss_rows, T, s));
+  if (loss) NE_CHECK(launch_ce_mean(loss_rows, loss, T, s));
   int mc, wm, wr;
   gemm_ce_layout(T, V, D, &mc, &wm, &wr);
   return launch_ce_grad(dt, (h16_t *)dlogits, T, V, n_valid, part, n_tiles, mc, wm, wr, lse, tgt_logit, targets,

@@ -872,7 +872,8 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
         NE_CHECK(ce_forward_piece(dt, c->xf, Ecls, c->tok_tgt, T, D, V, V, c->ce_cut[p], c->ce_cut[p + 1],
                                   c->ce_part, c->ce_tgt, c->dlogits, c->st));
       }
-      NE_CHECK(ce_forward_finish(dt, c->tok_tgt, T, D, V, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows, c->loss,
+      // the loss's mean is taken below, off the backward's chain
+      NE_CHECK(ce_forward_finish(dt, c->tok_tgt, T, D, V, V, c->ce_part, c->ce_tgt, c->ce_lse, c->ce_rows, nullptr,
                                  c->gs, c->dlogits, ovf + OVF_DLOGITS, c->st));
     }
   }
@@ -913,6 +914,16 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
   };
   if (c->de_pieces == 1) NE_CHECK(add_de(0));
   NE_CHECK(wq.flush());
+  if (!compact) {  // the loss's mean, beside the backward on two streams (the join waits for it)
+    ProfScope ps(c, NE_PROF_CE);
+    hipStream_t sm = c->st;
+    if (wq.on) {  // after the row losses (the flush above forks only when it had jobs)
+      NE_HIP(hipEventRecord(c->ev_fork, c->st));
+      NE_HIP(hipStreamWaitEvent(c->st2, c->ev_fork, 0));
+      sm = c->st2;
+    }
+    NE_CHECK(launch_ce_mean(c->ce_rows, c->loss, T, sm));
+  }
   NE_CHECK(gemm_split(c, NE_PROF_CE, GEMM_NN, EPI_F32, T, D, Vc, c->dlogits, Vc, Ecls, D, c->dtmp, &sp_d));
   {
     ProfScope ps(c, NE_PROF_NORM);

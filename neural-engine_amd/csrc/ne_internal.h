@@ -200,6 +200,11 @@ int launch_attn_fwd(int dt, const AttnArgs &a, hipStream_t s);
 int launch_attn_bwd(int dt, const AttnArgs &a, hipStream_t s);
 
 // ---- cross-entropy (k_ce.hip over the EPI_CE_* GEMM epilogues) ----
+// The row log-sum-exp and loss of the logits GEMM's tile partials (launch_ce_rows), and the
+// mean of the row losses (launch_ce_mean); launch_ce_reduce runs both.
+int launch_ce_rows(const float *part, int n_tiles, const float *tgt_logit, float *lse, float *loss_rows, int T,
+                   hipStream_t s);
+int launch_ce_mean(const float *loss_rows, float *loss, int T, hipStream_t s);
 int launch_ce_reduce(const float *part, int n_tiles, const float *tgt_logit, float *lse,
                      float *loss_rows, float *loss, int T, hipStream_t s);
 // V columns of which the first n_valid take part in the softmax (n_valid <= V; the rest
@@ -217,8 +222,8 @@ int ce_forward_grad(int dt, const void *x, const void *E, const int32_t *targets
                     float scale, void *dlogits, int *ovf, hipStream_t s);
 // The same in parts: ce_forward_piece runs the logits GEMM over vocabulary columns [c0, c1)
 // (boundaries from gemm_ce_pieces(T, V, D, ...)) against E rows [c0, c1); once every piece has
-// run, ce_forward_finish reduces the rows and forms the gradient.  The pieces give the same bits
-// as the whole.
+// run, ce_forward_finish reduces the rows and forms the gradient (loss null: the mean of the row
+// losses is left to the caller, launch_ce_mean).  The pieces give the same bits as the whole.
 int ce_forward_piece(int dt, const void *x, const void *E, const int32_t *targets, int T, int D, int V,
                      int n_valid, int c0, int c1, float *part, float *tgt_logit, void *dlogits, hipStream_t s);
 int ce_forward_finish(int dt, const int32_t *targets, int T, int D, int V, int n_valid, float *part,
