@@ -27,6 +27,12 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr int BLK = 64;  // keys per kv tile, queries per q tile
 
+// A compile-time flag passed to a generic lambda (one instance per value).
+template <bool V>
+struct Bool {
+  static constexpr bool value = V;
+};
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename HT>
@@ -324,7 +330,7 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
 // Block (bx, by, bz) of the dK / dV grid; lds: [buffer][Q tile, dO tile].
 template <typename HT, int HD, int NW, int RG, bool SPLIT>
 __device__ __forceinline__ void dkdv_block(const AttnArgs &a, int bx, int by, int bz, h16_t (*lds)[2 * BLK * (HD + 16)],
-                                           float (*lse_s)[BLK], float (*dl_s)[BLK]) {
+                                           float (*lse_s)[BLK], float (*ndl_s)[BLK]) {
   constexpr int RP = HD + 16, NK = HD / 32, ND = HD / 16, NT = NW * 64, TILE = BLK * RP;
   constexpr int ROWS = NW * 16 * RG;  // keys per block
   const int nqb = a.S / BLK;
@@ -374,7 +380,7 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs &a, int bx, int by, in
     cp.template store<RP>(1, lds[buf] + TILE);
     if (threadIdx.x < BLK) {
       lse_s[buf][threadIdx.x] = lse_r;
-      dl_s[buf][threadIdx.x] = dl_r;
+      ndl_s[buf][threadIdx.x] = -dl_r;
     }
   };
   fetch(0);
@@ -388,9 +394,15 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs &a, int bx, int by, in
       const h16_t *Qs = lds[cur], *dOs = lds[cur] + TILE;
       f32x4 sp[RG][4], dp[RG][4];
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++)
+      for (int mb = 0; mb < 4; mb++) {
+        // dP starts from -delta of its query rows, so the MFMAs leave dP - delta
+        const f32x4 nd = *(const f32x4 *)&ndl_s[cur][mb * 16 + g * 4];
 #pragma unroll
-        for (int r = 0; r < RG; r++) sp[r][mb] = dp[r][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < RG; r++) {
+          sp[r][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[r][mb] = nd;
+        }
+      }
 #pragma unroll
       for (int kk = 0; kk < NK; kk++)
 #pragma unroll
@@ -404,26 +416,31 @@ __device__ __forceinline__ void dkdv_block(const AttnArgs &a, int bx, int by, in
           }
         }
       // sp[r][mb][i] = score(query qb*64 + mb*16 + 4g + i, key ki[r])
+      // Only the first query tile of a head crosses this wave's keys: the others skip the mask.
       const bool diag = kw + 16 * RG - 1 > qb * BLK;  // some key of this wave above some query
       typename HT::v8 pb[RG][2], sb[RG][2];
+      auto elem = [&](auto masked) {
 #pragma unroll
-      for (int r = 0; r < RG; r++) {
+        for (int r = 0; r < RG; r++) {
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++)
+          for (int mb = 0; mb < 4; mb++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const int ql = mb * 16 + g * 4 + i;
-            float p = fexp2(fmaf(sp[r][mb][i], sl2, -lse_s[cur][ql]));
-            if (diag && ki[r] > qb * BLK + ql) p = 0.f;
-            sp[r][mb][i] = p;
-            dp[r][mb][i] = p * (dp[r][mb][i] - dl_s[cur][ql]);
+            for (int i = 0; i < 4; i++) {
+              const int ql = mb * 16 + g * 4 + i;
+              float p = fexp2(fmaf(sp[r][mb][i], sl2, -lse_s[cur][ql]));
+              if (decltype(masked)::value && ki[r] > qb * BLK + ql) p = 0.f;
+              sp[r][mb][i] = p;
+              dp[r][mb][i] = p * dp[r][mb][i];
+            }
+#pragma unroll
+          for (int c = 0; c < 2; c++) {
+            pb[r][c] = pack_acc<HT>(sp[r][2 * c], sp[r][2 * c + 1]);
+            sb[r][c] = pack_acc<HT>(dp[r][2 * c], dp[r][2 * c + 1]);
           }
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-          pb[r][c] = pack_acc<HT>(sp[r][2 * c], sp[r][2 * c + 1]);
-          sb[r][c] = pack_acc<HT>(dp[r][2 * c], dp[r][2 * c + 1]);
         }
-      }
+      };
+      if (diag) elem(Bool<true>{});
+      else elem(Bool<false>{});
 #pragma unroll
       for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -554,7 +571,10 @@ __device__ __forceinline__ void dq_block(const AttnArgs &a, int bx, int by, int 
 #pragma unroll
       for (int nb = 0; nb < 4; nb++)
 #pragma unroll
-        for (int r = 0; r < RG; r++) sp[r][nb] = dp[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < RG; r++) {
+          sp[r][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[r][nb] = f32x4{-dl[r], -dl[r], -dl[r], -dl[r]};  // the MFMAs leave dP - delta
+        }
 #pragma unroll
       for (int kk = 0; kk < NK; kk++)
 #pragma unroll
@@ -568,21 +588,26 @@ __device__ __forceinline__ void dq_block(const AttnArgs &a, int bx, int by, int 
           }
         }
       // sp[r][nb][i] = score(key kb*64 + nb*16 + 4g + i, query qi[r])
+      // Only the last key tile crosses this wave's queries: the others skip the mask.
       const bool diag = kb * BLK + BLK - 1 > qw;  // some key of the tile above some query
       typename HT::v8 sb[RG][2];
+      auto elem = [&](auto masked) {
 #pragma unroll
-      for (int r = 0; r < RG; r++) {
+        for (int r = 0; r < RG; r++) {
 #pragma unroll
-        for (int nb = 0; nb < 4; nb++)
+          for (int nb = 0; nb < 4; nb++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float p = fexp2(fmaf(sp[r][nb][i], sl2, -lse2[r]));
-            if (diag && kb * BLK + nb * 16 + g * 4 + i > qi[r]) p = 0.f;
-            dp[r][nb][i] = p * (dp[r][nb][i] - dl[r]);
-          }
-        sb[r][0] = pack_acc<HT>(dp[r][0], dp[r][1]);
-        sb[r][1] = pack_acc<HT>(dp[r][2], dp[r][3]);
-      }
+            for (int i = 0; i < 4; i++) {
+              float p = fexp2(fmaf(sp[r][nb][i], sl2, -lse2[r]));
+              if (decltype(masked)::value && kb * BLK + nb * 16 + g * 4 + i > qi[r]) p = 0.f;
+              dp[r][nb][i] = p * dp[r][nb][i];
+            }
+          sb[r][0] = pack_acc<HT>(dp[r][0], dp[r][1]);
+          sb[r][1] = pack_acc<HT>(dp[r][2], dp[r][3]);
+        }
+      };
+      if (diag) elem(Bool<true>{});
+      else elem(Bool<false>{});
 #pragma unroll
       for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -659,11 +684,11 @@ int fwd_t(const AttnArgs &a, hipStream_t s) {
 template <typename HT, int HD, int NW, int RG, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_kernel(AttnArgs a, int nkv, int nky) {
   __shared__ __attribute__((aligned(16))) h16_t lds[2][2 * BLK * (HD + 16)];
-  __shared__ float lse_s[2][BLK], dl_s[2][BLK];
+  __shared__ __attribute__((aligned(16))) float lse_s[2][BLK], ndl_s[2][BLK];
   int bx, by, bz;
   xcd_block(bx, by, bz);
   if (bx < nkv) {
-    if (by < nky) dkdv_block<HT, HD, NW, RG, SPLIT>(a, bx, by, bz, lds, lse_s, dl_s);
+    if (by < nky) dkdv_block<HT, HD, NW, RG, SPLIT>(a, bx, by, bz, lds, lse_s, ndl_s);
   } else {
     dq_block<HT, HD, NW, RG>(a, bx - nkv, by, bz, gridDim.x - nkv, lds);
   }
