@@ -730,6 +730,20 @@ int bwd_t(const AttnArgs &a, hipStream_t s) {
 
 }  // namespace
 
+// With GQA the dK/dV blocks either take one query head each and leave fp32 partials that the
+// QK-prep backward sums (twice the blocks: a 256-token Qwen3-0.6B step has 64 dK/dV blocks
+// per layer without them, 7.37 vs 7.52-7.57 ms per step), or loop over the query heads of
+// their KV head and write dK and dV directly (no partials to write and read back: 268 MB
+// per layer less of each at batch 8 x 2048, 103.2-103.4 vs 101.6-102.1 ms per step).  The
+// split is taken below two dK/dV blocks per CU.
+bool attn_bwd_split_heads(int B, int S, int NH, int NKV) {
+  if (NH == NKV || S % BLK) return false;
+  AttnArgs a = {};
+  a.B = B; a.S = S; a.NH = NH; a.NKV = NKV;
+  const int rows = pick_shape(a) == SHAPE_2x1 ? 32 : 64;  // keys per dK/dV block (RG = 1)
+  return (long)(S / rows) * NKV * B < 512;
+}
+
 int launch_attn_fwd(int dt, const AttnArgs &a, hipStream_t s) {
   NE_CHECK(check(a));
   return DISPATCH_H16(dt, fwd_t<HT>(a, s));

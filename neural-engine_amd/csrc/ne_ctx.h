@@ -93,6 +93,7 @@ struct ne_ctx {
   float *xL, *rf;
   h16_t *xf;
   float *dx, *dx2, *dtmp, *dq, *dk, *delta, *attn_part;
+  bool attn_split = false;  // GQA attention backward through per-query-head partials (attn_part)
   // per layer (the weight-gradient GEMMs on st2 read them while st moves on): dbf [2L][T, D]
   // (alpha * dx into the FFN of layer l at 2l, into its attention at 2l + 1), dh13 [L][T, 2H],
   // dqkv [L][T, QKV]

@@ -485,7 +485,8 @@ extern "C" ne_ctx *ne_create(const ne_config *cfg) {
   pl.add(&c->xL, T * D); pl.add(&c->rf, T); pl.add(&c->xf, T * D);
   pl.add(&c->dx, T * D); pl.add(&c->dx2, T * D); pl.add(&c->dtmp, T * D);
   pl.add(&c->dq, T * Q); pl.add(&c->dk, T * KV); pl.add(&c->delta, T * NH);
-  pl.add(&c->attn_part, c->NH != c->NKV ? 2 * T * Q : 1);
+  c->attn_split = attn_bwd_split_heads(c->B, c->S, c->NH, c->NKV);
+  pl.add(&c->attn_part, c->attn_split ? 2 * T * Q : 1);
   const size_t L = c->L;
   pl.add(&c->dbf, 2 * L * T * D); pl.add(&c->dh13, L * T * 2 * H); pl.add(&c->dattn, T * Q);
   pl.add(&c->dqkv, L * T * QKV);
@@ -963,7 +964,7 @@ static int train_step_enqueue(ne_ctx *c, float loss_scale, bool fresh, bool two,
       at.o = a.attn; at.ldo = Q; at.lse = a.lse;
       at.dout = c->dattn; at.lddo = Q; at.delta = c->delta;
       at.dq = c->dq; at.lddq = Q; at.dk = c->dk; at.lddk = KV; at.dv = dqkv + Q + KV; at.lddv = QKV;
-      at.part = c->NH != c->NKV ? c->attn_part : nullptr;
+      at.part = c->attn_split ? c->attn_part : nullptr;
       at.defer_gqa = at.part != nullptr;  // the QK-prep backward sums the per-query-head dK/dV
       at.ovf = ovf + OVF_DV;
       NE_CHECK(launch_attn_bwd(dt, at, c->st));

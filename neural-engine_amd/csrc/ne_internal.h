@@ -198,6 +198,9 @@ struct AttnArgs {
 };
 int launch_attn_fwd(int dt, const AttnArgs &a, hipStream_t s);
 int launch_attn_bwd(int dt, const AttnArgs &a, hipStream_t s);
+// Whether the backward at this shape should take per-query-head dK/dV partials (AttnArgs::part)
+// with GQA: yes when the KV heads alone give too few dK/dV blocks to fill the device.
+bool attn_bwd_split_heads(int B, int S, int NH, int NKV);
 
 // ---- cross-entropy (k_ce.hip over the EPI_CE_* GEMM epilogues) ----
 // The row log-sum-exp and loss of the logits GEMM's tile partials (launch_ce_rows), and the
