@@ -59,7 +59,8 @@ def test_train_step_matches_oracle(case, dtype):
     m.close()
 
 
-def test_gqa_step_on_long_sequences_matches_oracle():
+@pytest.mark.parametrize("dtype", [ne.NE_FP16, ne.NE_BF16])
+def test_gqa_step_on_long_sequences_matches_oracle(dtype):
     """GQA at 4 x 1024 tokens with 8 KV heads: the KV heads alone give the attention backward
     512 dK/dV blocks, so each block loops over the query heads of its KV head and writes dK and
     dV itself (shorter steps, as in the other cases here, take per-query-head partials that the
@@ -68,15 +69,15 @@ def test_gqa_step_on_long_sequences_matches_oracle():
                   vocab=512, seq=1024)
     P = om.init_params(cfg, seed=0, std=0.02)
     tok = om.tokens_for_step(cfg, 4, cfg.seq, seed=1)
-    m, loss, G = run_step(cfg, P, tok)
-    Pm = as_multiplied(P, ne.NE_FP16)
+    m, loss, G = run_step(cfg, P, tok, dtype=dtype)
+    Pm = as_multiplied(P, dtype)
     lo, cache = om.forward(cfg, Pm, tok, loss_scale=256.0)
     Go = om.backward(cfg, Pm, cache)
     assert abs(loss - lo) <= LOSS_RTOL * abs(lo), (loss, lo)
     errs = sorted(((rel_l2(G[n], Go[n]), n) for n in P), reverse=True)
     print("\n  worst grad rel-L2: " + ", ".join(f"{n}={e:.2e}" for e, n in errs[:6]))
     for n in P:
-        assert rel_l2(G[n], Go[n]) <= grad_tol(n, ne.NE_FP16), (n, rel_l2(G[n], Go[n]))
+        assert rel_l2(G[n], Go[n]) <= grad_tol(n, dtype), (n, rel_l2(G[n], Go[n]))
     m.close()
 
 
