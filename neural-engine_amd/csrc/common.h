@@ -134,6 +134,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(v, __shfl_xor(v, 32, 64));
 }
 
+// The same butterfly over aligned groups of W lanes (W = 8, 16, 32 or 64), the sum left in
+// every lane of the group: the same partial sums added in the same order as the xor-shuffle
+// butterfly of strides 1 .. W/2, so the same bits.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group_sum: 8, 16, 32 or 64 lanes");
+  if constexpr (W == 64) return wave_sum(v);
+  if constexpr (W == 32) return half_wave_sum(v);
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  if constexpr (W == 16) v += dpp_mov<0x140>(v);
+  return v;
+}
+
 // Reductions over the 4 lane groups {l, l^16, l^32, l^48} (lanes sharing l % 16).
 __device__ __forceinline__ float quad16_sum(float v) {
   v += __shfl_xor(v, 16, 64);

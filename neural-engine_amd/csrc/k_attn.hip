@@ -317,8 +317,7 @@ __global__ void attn_delta_kernel(AttnArgs a, long rows) {
 #pragma unroll
     for (int e = 0; e < 8; e++) s += HT::f(o[e]) * HT::f(d[e]);
   }
-#pragma unroll
-  for (int off = 1; off < L; off <<= 1) s += __shfl_xor(s, off, 64);
+  s = group_sum<L>(s);
   if (row < rows && j == 0) a.delta[row] = s;
 }
 

@@ -507,8 +507,7 @@ __global__ __launch_bounds__(256) void qk_prep_fwd_kernel(h16_t *__restrict__ qk
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) ss += x[e] * x[e];
-#pragma unroll
-      for (int o = 1; o < TPH; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      ss = group_sum<TPH>(ss);
       const float r = 1.0f / sqrtf(ss / (float)HD + eps);
       const float *gg = (isq ? gq : gk) + 8 * j;
       const float4 g0 = *(const float4 *)gg, g1 = *(const float4 *)(gg + 4);
@@ -607,7 +606,7 @@ __global__ __launch_bounds__(256) void qk_prep_bwd_kernel(
       const float x0 = HT::f((h16_t)(pr & 0xFFFF)), x1 = HT::f((h16_t)(pr >> 16));
       const float r = isq ? rq[t * NH + hh] : rk[t * NKV + hh];
       float dot = d0 * x0 * g0 + d1 * x1 * g1;
-      for (int o = 1; o < half; o <<= 1) dot += __shfl_xor(dot, o, 64);
+      dot = half == 64 ? group_sum<64>(dot) : group_sum<32>(dot);  // HD = 128 or 64
       const float cc = r * r * r * dot / (float)HD;
       a0 += d0 * x0 * r;
       a1 += d1 * x1 * r;
